@@ -1,0 +1,151 @@
+/*
+ * lbr_executor.h — C ABI of the MI355X (gfx950) compiled-executor library
+ * `liblbr_executor.so`.
+ *
+ * The library replaces the reference's CPU dispatch loop
+ *   void execute(OpNode* nodes, int n_nodes)          csrc/executor.c:458-467
+ * loaded by ctypes in runtime/executor/common.py:148-163 and called from
+ * runtime/executor/compiled.py:87/91.  The node record and the op codes are
+ * byte-identical to csrc/runtime.h:11-69 (mirrored by COpNode,
+ * runtime/executor/common.py:125-141), so the Python host layer builds the
+ * same node array it builds for the CPU executor; the only difference is
+ * that every pointer in inputs[] / output is a device address (arena base +
+ * planner offset, a device-resident weight, or a fixed device staging
+ * buffer for a graph input).
+ *
+ * Differences from the reference boundary, all deliberate:
+ *   - every call returns an int status (LBR_OK = 0) instead of abort();
+ *     lbr_last_error() returns the message of the most recent failure on
+ *     the calling thread;
+ *   - device memory is owned by the library (lbr_device_alloc/free), since
+ *     the caller's numpy arena cannot be read by the GPU;
+ *   - a node array can be turned into a plan once (validated, decoded into
+ *     kernel launches, optionally captured into a hipGraph) and replayed.
+ *
+ * Threading contract (same as the reference): one caller at a time per
+ * plan; all work is issued on the library's single stream.
+ */
+#ifndef LBR_EXECUTOR_H
+#define LBR_EXECUTOR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Op codes — identical values to csrc/runtime.h:11-55 and runtime/ir.py:36-90. */
+enum OpType {
+    OP_RELU = 100, OP_EXP = 101, OP_TANH = 102, OP_POW = 103, OP_GELU = 104,
+    OP_RSQRT = 105, OP_SILU = 106, OP_NEG = 107, OP_COS = 108, OP_SIN = 109,
+
+    OP_ADD = 200, OP_SUB = 201, OP_MUL = 202, OP_DIV = 203,
+
+    OP_MAX = 300, OP_SUM = 301, OP_SOFTMAX = 302,
+
+    OP_MATMUL = 400,
+
+    OP_RESHAPE = 500, OP_TRANSPOSE = 501, OP_PERMUTE = 502, OP_SLICE = 503,
+    OP_EMBEDDING = 504, OP_CAT = 505,
+
+    OP_LAYERNORM = 600, OP_RMSNORM = 601,
+
+    OP_MATMUL_ADD = 1000, OP_FUSED_BIAS_RELU = 1001, OP_ATTENTION = 1002,
+    OP_GATED_ACT = 1003
+};
+
+#define MAX_INPUTS 12
+#define MAX_DIMS   24
+
+/* Node record — layout identical to csrc/runtime.h:60-69 (312 bytes on
+ * x86-64).  `extra` holds the op-specific integers packed by the host
+ * layer's extras packers (runtime/ops.py:137-329); floats are bit-cast. */
+typedef struct {
+    int   op;
+    int   n_inputs;
+    void* inputs[MAX_INPUTS];
+    void* output;
+    int   out_shape[MAX_DIMS];
+    int   n_dims;
+    int   elem_size;
+    int   extra[MAX_DIMS];
+} OpNode;
+
+/* Status codes. */
+#define LBR_OK              0
+#define LBR_ERR_INVALID     1   /* malformed node / argument             */
+#define LBR_ERR_UNSUPPORTED 2   /* op code with no device kernel          */
+#define LBR_ERR_HIP         3   /* a HIP runtime call failed              */
+#define LBR_ERR_NO_DEVICE   4   /* no usable gfx950 device                */
+
+/* Message of the most recent failure on this thread ("" if none). */
+const char* lbr_last_error(void);
+
+/* Library version string. */
+const char* lbr_version(void);
+
+/* sizeof(OpNode) as compiled into the library (312), so the ctypes mirror
+ * can be checked at load time. */
+int lbr_opnode_size(void);
+
+/* Select `device`, check it is a gfx950 part and create the library stream.
+ * Idempotent for the same device.  Every other entry point that touches the
+ * GPU calls it with device 0 if it has not been called. */
+int lbr_init(int device);
+
+/* 1 if op code `op` has a device kernel (the dispatch-table coverage the
+ * host layer's compiled-dispatch validator checks; runtime/validation/
+ * execution.py:16-34 keeps the CPU executor's set). */
+int lbr_op_supported(int op);
+
+/* Device memory owned by the library.  lbr_device_alloc returns memory
+ * aligned to 256 bytes. */
+int lbr_device_alloc(size_t bytes, void** out_ptr);
+int lbr_device_free(void* ptr);
+int lbr_memcpy_h2d(void* dst_device, const void* src_host, size_t bytes);
+int lbr_memcpy_d2h(void* dst_host, const void* src_device, size_t bytes);
+int lbr_memcpy_d2d(void* dst_device, const void* src_device, size_t bytes);
+int lbr_memset(void* dst_device, int value, size_t bytes);
+
+/* Drop-in for execute(OpNode*, int) (csrc/executor.c:458-467): launch every
+ * node in order on the library stream and wait for completion.  Returns
+ * LBR_ERR_UNSUPPORTED for an op without a kernel (where the reference
+ * aborts), LBR_ERR_INVALID for a node whose fields do not fit its op. */
+int lbr_execute(const OpNode* nodes, int n_nodes);
+
+/* Plans: validate and decode the node array once; launches reuse the
+ * decoded kernel arguments.  With use_graph != 0 the launch sequence is
+ * captured into a hipGraph at creation and every lbr_plan_launch replays it
+ * (the device pointers in the nodes must stay valid and unchanged). */
+typedef struct lbr_plan lbr_plan;
+int lbr_plan_create(const OpNode* nodes, int n_nodes, int use_graph,
+                    lbr_plan** out_plan);
+int lbr_plan_destroy(lbr_plan* plan);
+int lbr_plan_num_nodes(const lbr_plan* plan);
+
+/* Enqueue one forward pass on the library stream (asynchronous). */
+int lbr_plan_launch(lbr_plan* plan);
+
+/* Wait for all work on the library stream. */
+int lbr_synchronize(void);
+
+/* Time `iters` back-to-back lbr_plan_launch calls with hipEvents recorded
+ * on the library stream; *out_ms = total elapsed milliseconds. */
+int lbr_plan_time(lbr_plan* plan, int iters, float* out_ms);
+
+/* Per-node device time: runs the plan `iters` times eagerly with a hipEvent
+ * pair around every node's launches (on the library stream) and writes the
+ * mean milliseconds of node i to out_ms[i] (n_out >= number of nodes). */
+int lbr_plan_profile(lbr_plan* plan, int iters, float* out_ms, int n_out);
+
+/* Number of kernel launches node `index` decodes into, and a short name of
+ * its kernel (for reports). */
+int lbr_plan_node_kernel(const lbr_plan* plan, int index, char* name_out,
+                         int name_cap);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LBR_EXECUTOR_H */

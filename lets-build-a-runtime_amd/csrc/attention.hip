@@ -1,0 +1,333 @@
+// attention.hip — fused attention on the gfx950 matrix cores.
+//
+// Replaces kernel_attention / kernel_attention_flash (csrc/ops/attn.c:26-253)
+// behind ATTENTION (csrc/executor.c:371-397):
+//   O[bh] = softmax(Q[bh]·K[kv]ᵀ · 1/√hd  (+ mask[bh])  (causal: −∞ above the
+//           diagonal)) · V[kv],      kv = bh / group_size   (attn.c:73, 247)
+// Q, K, V, O are [batch·heads, S, hd] contiguous.  extras
+// [seq_len, head_dim, causal, has_mask, group_size] (runtime/ops.py:257-262);
+// inputs [Q, K, V, scratch] or [Q, K, V, mask, scratch].  The planner's
+// scratch slot is not needed: the online-softmax state lives in registers.
+//
+// One single-pass online-softmax kernel serves every sequence length (the
+// reference's S ≤ 256 / mask path and its flash path compute the same
+// function).  Layout choice: the kernel computes Sᵀ = K·Qᵀ and Oᵀ = Vᵀ·Pᵀ with
+// v_mfma_f32_32x32x2_f32, so in both accumulators lane l owns query row
+// q0 + l%32.  The running max / sum and the rescale of O are then per-lane
+// scalars, the row max needs one cross-half exchange (lane l ↔ l^32), and
+// the exponentiated scores are fed straight back as the B operand of the
+// P·V product without leaving registers.
+//
+// Workgroup = 4 wavefronts × 32 query rows = 128 rows of one (batch·head);
+// K/V tiles of 64 keys are staged in LDS (zero-filled past S and past hd).
+// Causal: tiles entirely above a wavefront's rows are skipped; workgroups are
+// issued heaviest-first (last query block first) to balance the triangle.
+#include "lbr_device.h"
+
+#include <float.h>
+#include <math.h>
+
+namespace {
+
+constexpr int AT_NT = 256;       // 4 waves
+constexpr int AT_QB = 128;       // query rows per workgroup
+constexpr int AT_KB = 64;        // keys per LDS tile
+constexpr float LOG2E = 1.4426950408889634f;
+
+struct AttnArgs {
+    const float* Q;
+    const float* K;
+    const float* V;
+    float* O;
+    const float* mask;
+    int S, D, group_size, n_qblocks;
+    float scale_log2;            // (1/√hd)·log2(e)
+};
+
+template <int DP, bool CAUSAL, bool HAS_MASK>
+__global__ __launch_bounds__(AT_NT, 2) void attn_fwd_mfma(AttnArgs g) {
+    constexpr int LDD = DP + 4;
+    constexpr int NCH = DP / 8;      // 8-wide d chunks
+    constexpr int NDB = DP / 32;     // 32-wide d blocks of Oᵀ
+    __shared__ float Ks[AT_KB][LDD];
+    __shared__ float Vs[AT_KB][LDD];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lq = lane & 31, lh = lane >> 5;
+    const int qblk = CAUSAL ? (g.n_qblocks - 1 - (int)blockIdx.x) : (int)blockIdx.x;
+    const long long bh = blockIdx.y;
+    const long long kvh = bh / g.group_size;
+    const int S = g.S, D = g.D;
+    const float* __restrict__ Qb = g.Q + bh * (long long)S * D;
+    const float* __restrict__ Kb = g.K + kvh * (long long)S * D;
+    const float* __restrict__ Vb = g.V + kvh * (long long)S * D;
+    const int q_wave0 = qblk * AT_QB + wave * 32;
+    const int q = q_wave0 + lq;            // this lane's query row
+
+    // Q fragment, pre-scaled: lane holds Q[q][8c + 4h + 0..3] for every chunk c
+    floatx4 qf[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int d = c * 8 + lh * 4;
+        floatx4 v = {0.f, 0.f, 0.f, 0.f};
+        if (q < S && d < D) {
+            const float4 t = *reinterpret_cast<const float4*>(Qb + (long long)q * D + d);
+            v[0] = t.x * g.scale_log2;
+            v[1] = t.y * g.scale_log2;
+            v[2] = t.z * g.scale_log2;
+            v[3] = t.w * g.scale_log2;
+        }
+        qf[c] = v;
+    }
+
+    floatx16 oacc[NDB];
+#pragma unroll
+    for (int b = 0; b < NDB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[b][r] = 0.f;
+    float m_run = -FLT_MAX, l_run = 0.f;
+
+    const int n_tiles_all = (S + AT_KB - 1) / AT_KB;
+    int n_tiles = n_tiles_all;
+    if (CAUSAL) {
+        const int last_q = min(S - 1, qblk * AT_QB + AT_QB - 1);
+        n_tiles = min(n_tiles_all, last_q / AT_KB + 1);
+    }
+
+    for (int kt = 0; kt < n_tiles; ++kt) {
+        const int k0 = kt * AT_KB;
+        __syncthreads();
+        // stage K and V tiles: 64 rows × DP (float4 granules), zero past S / D
+        for (int idx = tid; idx < AT_KB * (DP / 4); idx += AT_NT) {
+            const int r = idx / (DP / 4), d = (idx % (DP / 4)) * 4;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (k0 + r < S && d < D) {
+                kv = *reinterpret_cast<const float4*>(Kb + (long long)(k0 + r) * D + d);
+                vv = *reinterpret_cast<const float4*>(Vb + (long long)(k0 + r) * D + d);
+            }
+            *reinterpret_cast<float4*>(&Ks[r][d]) = kv;
+            *reinterpret_cast<float4*>(&Vs[r][d]) = vv;
+        }
+        __syncthreads();
+
+        // Causal: a tile whose first key is past this wave's last row contributes nothing.
+        if (CAUSAL && k0 > q_wave0 + 31) continue;
+
+        // Sᵀ[kv][q] for kv blocks 0..1 of the tile (scaled by log2 e / √hd)
+        floatx16 sacc[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[b][r] = 0.f;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const floatx4 kf = *reinterpret_cast<const floatx4*>(&Ks[b * 32 + lq][c * 8 + lh * 4]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    sacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i], qf[c][i], sacc[b], 0, 0, 0);
+            }
+        }
+
+        // mask / causal / tail, then the tile's row max
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int kv = k0 + b * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                float sv = sacc[b][r];
+                if (HAS_MASK && kv < S && q < S) sv += g.mask[(bh * S + q) * (long long)S + kv] * LOG2E;
+                if (kv >= S || (CAUSAL && kv > q)) sv = -INFINITY;
+                sacc[b][r] = sv;
+                tmax = fmaxf(tmax, sv);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float m_new = fmaxf(m_run, tmax);
+        const float corr = exp2f(m_run - m_new);
+        float psum = 0.f;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = exp2f(sacc[b][r] - m_new);
+                sacc[b][r] = p;
+                psum += p;
+            }
+        psum += __shfl_xor(psum, 32, 64);
+        l_run = l_run * corr + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[db][r] *= corr;
+
+        // Oᵀ[d][q] += Σ_kv V[kv][d] · P[q][kv]
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int kvl = b * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    const float vv = Vs[kvl][db * 32 + lq];
+                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, sacc[b][r], oacc[db], 0, 0, 0);
+                }
+    }
+
+    // O[q][d] = Oᵀ[d][q] / l ; lane holds d = 32·db + 8·j + 4·h + (0..3)
+    if (q < S) {
+        const float inv_l = 1.0f / l_run;
+        float* __restrict__ Ob = g.O + bh * (long long)S * D + (long long)q * D;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int d = db * 32 + 8 * j + 4 * lh;
+                if (d < D) {
+                    float4 o;
+                    o.x = oacc[db][4 * j + 0] * inv_l;
+                    o.y = oacc[db][4 * j + 1] * inv_l;
+                    o.z = oacc[db][4 * j + 2] * inv_l;
+                    o.w = oacc[db][4 * j + 3] * inv_l;
+                    *reinterpret_cast<float4*>(Ob + d) = o;
+                }
+            }
+    }
+}
+
+// Fallback for head dims the MFMA kernel does not take (hd % 8 != 0 or
+// hd > 256): one workgroup per (bh, query row), scores held in LDS.
+__global__ __launch_bounds__(256) void attn_fwd_rows(AttnArgs g, int causal) {
+    extern __shared__ float sc[];
+    __shared__ float red[4];
+    const long long bh = blockIdx.y;
+    const int q = blockIdx.x;
+    const int S = g.S, D = g.D;
+    const long long kvh = bh / g.group_size;
+    const float* Qr = g.Q + (bh * S + q) * (long long)D;
+    const float* Kb = g.K + kvh * (long long)S * D;
+    const float* Vb = g.V + kvh * (long long)S * D;
+    const float scale = g.scale_log2 / LOG2E;
+    float mx = -INFINITY;
+    for (int j = threadIdx.x; j < S; j += blockDim.x) {
+        float acc = 0.f;
+        for (int d = 0; d < D; ++d) acc += Qr[d] * Kb[(long long)j * D + d];
+        float sv = acc * scale;
+        if (g.mask) sv += g.mask[(bh * S + q) * (long long)S + j];
+        if (causal && j > q) sv = -INFINITY;
+        sc[j] = sv;
+        mx = fmaxf(mx, sv);
+    }
+    mx = block_max(mx, red);
+    float sum = 0.f;
+    for (int j = threadIdx.x; j < S; j += blockDim.x) {
+        const float e = expf(sc[j] - mx);
+        sc[j] = e;
+        sum += e;
+    }
+    sum = block_sum(sum, red);
+    __syncthreads();
+    float* Or = g.O + (bh * S + q) * (long long)D;
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        float acc = 0.f;
+        for (int j = 0; j < S; ++j) acc += sc[j] * Vb[(long long)j * D + d];
+        Or[d] = acc / sum;
+    }
+}
+
+// Step::i: [0]=bh [1]=S [2]=D [3]=causal [4]=group [5]=DP (0 = row fallback)
+AttnArgs make_args(const Step& s) {
+    AttnArgs g;
+    g.Q = (const float*)s.in[0];
+    g.K = (const float*)s.in[1];
+    g.V = (const float*)s.in[2];
+    g.mask = (const float*)s.in[3];
+    g.O = (float*)s.out;
+    g.S = (int)s.i[1];
+    g.D = (int)s.i[2];
+    g.group_size = (int)s.i[4];
+    g.n_qblocks = (g.S + AT_QB - 1) / AT_QB;
+    g.scale_log2 = s.f[0] * LOG2E;
+    return g;
+}
+
+template <int DP, bool CAUSAL, bool HAS_MASK>
+void launch_attn(const Step& s, hipStream_t st) {
+    AttnArgs g = make_args(s);
+    if (g.S <= 0 || s.i[0] <= 0) return;
+    hipLaunchKernelGGL((attn_fwd_mfma<DP, CAUSAL, HAS_MASK>), dim3(g.n_qblocks, (unsigned)s.i[0]), dim3(AT_NT), 0, st,
+                       g);
+}
+
+void launch_attn_rows(const Step& s, hipStream_t st) {
+    AttnArgs g = make_args(s);
+    if (g.S <= 0 || s.i[0] <= 0) return;
+    hipLaunchKernelGGL(attn_fwd_rows, dim3(g.S, (unsigned)s.i[0]), dim3(256), (size_t)g.S * sizeof(float), st, g,
+                       (int)s.i[3]);
+}
+
+template <int DP>
+step_fn pick(bool causal, bool mask) {
+    if (causal) return mask ? launch_attn<DP, true, true> : launch_attn<DP, true, false>;
+    return mask ? launch_attn<DP, false, true> : launch_attn<DP, false, false>;
+}
+
+}  // namespace
+
+int decode_attention(const OpNode* n, Step* s) {
+    const int seq = n->extra[0], hd = n->extra[1], causal = n->extra[2] != 0, has_mask = n->extra[3] != 0;
+    const int group = n->extra[4] > 0 ? n->extra[4] : 1;
+    if (n->n_inputs < (has_mask ? 4 : 3) || !n->output || n->n_dims < 2) {
+        lbr_set_error("attention: malformed node");
+        return LBR_ERR_INVALID;
+    }
+    for (int i = 0; i < (has_mask ? 4 : 3); ++i)
+        if (!n->inputs[i]) {
+            lbr_set_error("attention: input %d is null", i);
+            return LBR_ERR_INVALID;
+        }
+    long long bh = 1;
+    for (int i = 0; i < n->n_dims - 2; ++i) bh *= n->out_shape[i];
+    if (seq <= 0 || hd <= 0 || bh > 65535 || (group > 1 && bh % group != 0)) {
+        if (seq == 0 || bh == 0) {
+            s->run = [](const Step&, hipStream_t) {};
+            s->name = "attention_empty";
+            return LBR_OK;
+        }
+        lbr_set_error("attention: unsupported sizes bh=%lld S=%d hd=%d group=%d", bh, seq, hd, group);
+        return LBR_ERR_UNSUPPORTED;
+    }
+    s->in[0] = n->inputs[0];
+    s->in[1] = n->inputs[1];
+    s->in[2] = n->inputs[2];
+    s->in[3] = has_mask ? n->inputs[3] : nullptr;
+    s->out = n->output;
+    s->i[0] = bh;
+    s->i[1] = seq;
+    s->i[2] = hd;
+    s->i[3] = causal;
+    s->i[4] = group;
+    s->f[0] = 1.0f / sqrtf((float)hd);   // attn.c:68/242
+    const bool aligned = lbr_aligned(n->inputs[0], 16) && lbr_aligned(n->inputs[1], 16) &&
+                         lbr_aligned(n->inputs[2], 16) && lbr_aligned(n->output, 16);
+    if (hd % 8 == 0 && hd <= 256 && aligned) {
+        const int dp = hd <= 32 ? 32 : hd <= 64 ? 64 : hd <= 128 ? 128 : 256;
+        s->i[5] = dp;
+        switch (dp) {
+            case 32: s->run = pick<32>(causal, has_mask); break;
+            case 64: s->run = pick<64>(causal, has_mask); break;
+            case 128: s->run = pick<128>(causal, has_mask); break;
+            default: s->run = pick<256>(causal, has_mask); break;
+        }
+        s->name = "attn_fwd_mfma_f32";
+        return LBR_OK;
+    }
+    if ((long long)seq * 4 > 60 * 1024) {
+        lbr_set_error("attention: fallback path holds S scores in LDS; S=%d too long for hd=%d", seq, hd);
+        return LBR_ERR_UNSUPPORTED;
+    }
+    s->i[5] = 0;
+    s->run = launch_attn_rows;
+    s->name = "attn_fwd_rows";
+    return LBR_OK;
+}

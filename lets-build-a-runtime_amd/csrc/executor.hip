@@ -1,0 +1,375 @@
+// executor.hip — the C ABI of liblbr_executor.so: device setup, memory,
+// the dispatch table, plans (decoded launch lists, optional hipGraph) and
+// timing.  Declarations and the contract are in include/lbr_executor.h.
+//
+// The dispatch table mirrors csrc/executor.c:409-452 (same op codes, same
+// extras decoding); instead of calling a CPU kernel, each entry decodes its
+// OpNode once into a Step (validated kernel arguments) and the Step's
+// launcher enqueues the HIP kernel on the library stream.  Unknown ops return
+// LBR_ERR_UNSUPPORTED where the reference prints and aborts
+// (executor.c:461-464).
+#include "lbr_device.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#define LBR_VERSION "lbr-executor 0.1 gfx950"
+
+static_assert(sizeof(OpNode) == 312, "OpNode must match csrc/runtime.h:60-69 (312 bytes)");
+static_assert(offsetof(OpNode, inputs) == 8, "OpNode.inputs offset");
+static_assert(offsetof(OpNode, output) == 104, "OpNode.output offset");
+static_assert(offsetof(OpNode, out_shape) == 112, "OpNode.out_shape offset");
+static_assert(offsetof(OpNode, n_dims) == 208, "OpNode.n_dims offset");
+static_assert(offsetof(OpNode, elem_size) == 212, "OpNode.elem_size offset");
+static_assert(offsetof(OpNode, extra) == 216, "OpNode.extra offset");
+
+// ------------------------------------------------------------------ errors
+static thread_local char g_err[512] = "";
+
+void lbr_set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+#define HIP_TRY(expr)                                                                       \
+    do {                                                                                    \
+        hipError_t _e = (expr);                                                             \
+        if (_e != hipSuccess) {                                                             \
+            lbr_set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(_e), __FILE__,  \
+                          __LINE__);                                                        \
+            return LBR_ERR_HIP;                                                             \
+        }                                                                                   \
+    } while (0)
+
+// ------------------------------------------------------------------ device
+static std::mutex g_mu;
+static int g_device = -1;
+static hipStream_t g_stream = nullptr;
+
+static int ensure_init() {
+    if (g_stream) return LBR_OK;
+    return lbr_init(0);
+}
+
+// ------------------------------------------------------------------ dispatch table
+typedef int (*decode_fn)(const OpNode*, Step*);
+
+static decode_fn decoder_for(int op) {
+    switch (op) {
+        case OP_RELU: case OP_EXP: case OP_TANH: case OP_POW: case OP_GELU:
+        case OP_RSQRT: case OP_SILU: case OP_NEG: case OP_COS: case OP_SIN:
+            return decode_unary;
+        case OP_ADD: case OP_SUB: case OP_MUL: case OP_DIV:
+            return decode_binary;
+        case OP_MAX: case OP_SUM:
+            return decode_reduce;
+        case OP_SOFTMAX:
+            return decode_softmax;
+        case OP_MATMUL: case OP_MATMUL_ADD:
+            return decode_matmul;
+        case OP_RESHAPE:
+            return decode_reshape;
+        case OP_TRANSPOSE:
+            return decode_transpose;
+        case OP_SLICE:
+            return decode_slice;
+        case OP_EMBEDDING:
+            return decode_embedding;
+        case OP_CAT:
+            return decode_cat;
+        case OP_LAYERNORM:
+            return decode_layernorm;
+        case OP_RMSNORM:
+            return decode_rmsnorm;
+        case OP_FUSED_BIAS_RELU:
+            return decode_bias_relu;
+        case OP_ATTENTION:
+            return decode_attention;
+        case OP_GATED_ACT:
+            return decode_gated_act;
+        default:
+            return nullptr;  // OP_PERMUTE has no kernel, as in the reference
+    }
+}
+
+static int decode_node(const OpNode* n, int index, Step* s) {
+    memset(s, 0, sizeof(*s));
+    s->node_index = index;
+    decode_fn d = decoder_for(n->op);
+    if (!d) {
+        lbr_set_error("executor: unknown op %d (node %d)", n->op, index);
+        return LBR_ERR_UNSUPPORTED;
+    }
+    if (n->n_inputs < 0 || n->n_inputs > MAX_INPUTS || n->n_dims < 0 || n->n_dims > MAX_DIMS) {
+        lbr_set_error("executor: node %d has n_inputs=%d n_dims=%d", index, n->n_inputs, n->n_dims);
+        return LBR_ERR_INVALID;
+    }
+    for (int i = 0; i < n->n_dims; ++i)
+        if (n->out_shape[i] < 0) {
+            lbr_set_error("executor: node %d has a negative dim", index);
+            return LBR_ERR_INVALID;
+        }
+    s->n_in = n->n_inputs;
+    int rc = d(n, s);
+    if (rc != LBR_OK) {
+        char tmp[512];
+        snprintf(tmp, sizeof(tmp), "node %d (op %d): %s", index, n->op, g_err);
+        lbr_set_error("%s", tmp);
+    }
+    return rc;
+}
+
+// ------------------------------------------------------------------ plan
+struct lbr_plan {
+    std::vector<Step> steps;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+static void run_steps(const std::vector<Step>& steps, hipStream_t st) {
+    for (const Step& s : steps) s.run(s, st);
+}
+
+extern "C" {
+
+const char* lbr_last_error(void) { return g_err; }
+
+const char* lbr_version(void) { return LBR_VERSION; }
+
+int lbr_opnode_size(void) { return (int)sizeof(OpNode); }
+
+int lbr_init(int device) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (g_stream && g_device == device) return LBR_OK;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= device || device < 0) {
+        lbr_set_error("lbr_init: no HIP device %d (found %d)", device, count);
+        return LBR_ERR_NO_DEVICE;
+    }
+    HIP_TRY(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        lbr_set_error("lbr_init: device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
+        return LBR_ERR_NO_DEVICE;
+    }
+    if (g_stream) {
+        hipStreamDestroy(g_stream);
+        g_stream = nullptr;
+    }
+    HIP_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    g_device = device;
+    return LBR_OK;
+}
+
+int lbr_op_supported(int op) { return decoder_for(op) != nullptr; }
+
+int lbr_device_alloc(size_t bytes, void** out_ptr) {
+    if (!out_ptr) {
+        lbr_set_error("lbr_device_alloc: null out_ptr");
+        return LBR_ERR_INVALID;
+    }
+    int rc = ensure_init();
+    if (rc) return rc;
+    *out_ptr = nullptr;
+    HIP_TRY(hipMalloc(out_ptr, bytes ? bytes : 256));
+    return LBR_OK;
+}
+
+int lbr_device_free(void* ptr) {
+    if (!ptr) return LBR_OK;
+    HIP_TRY(hipFree(ptr));
+    return LBR_OK;
+}
+
+int lbr_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    int rc = ensure_init();
+    if (rc) return rc;
+    if (!bytes) return LBR_OK;
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return LBR_OK;
+}
+
+int lbr_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    int rc = ensure_init();
+    if (rc) return rc;
+    if (!bytes) return LBR_OK;
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return LBR_OK;
+}
+
+int lbr_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+    int rc = ensure_init();
+    if (rc) return rc;
+    if (!bytes) return LBR_OK;
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return LBR_OK;
+}
+
+int lbr_memset(void* dst, int value, size_t bytes) {
+    int rc = ensure_init();
+    if (rc) return rc;
+    if (!bytes) return LBR_OK;
+    HIP_TRY(hipMemsetAsync(dst, value, bytes, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return LBR_OK;
+}
+
+int lbr_execute(const OpNode* nodes, int n_nodes) {
+    if (n_nodes < 0 || (n_nodes > 0 && !nodes)) {
+        lbr_set_error("lbr_execute: bad node array");
+        return LBR_ERR_INVALID;
+    }
+    int rc = ensure_init();
+    if (rc) return rc;
+    std::vector<Step> steps((size_t)n_nodes);
+    for (int i = 0; i < n_nodes; ++i) {
+        rc = decode_node(&nodes[i], i, &steps[i]);
+        if (rc) return rc;
+    }
+    run_steps(steps, g_stream);
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return LBR_OK;
+}
+
+int lbr_plan_create(const OpNode* nodes, int n_nodes, int use_graph, lbr_plan** out_plan) {
+    if (!out_plan || n_nodes < 0 || (n_nodes > 0 && !nodes)) {
+        lbr_set_error("lbr_plan_create: bad arguments");
+        return LBR_ERR_INVALID;
+    }
+    *out_plan = nullptr;
+    int rc = ensure_init();
+    if (rc) return rc;
+    lbr_plan* p = new lbr_plan();
+    p->steps.resize((size_t)n_nodes);
+    for (int i = 0; i < n_nodes; ++i) {
+        rc = decode_node(&nodes[i], i, &p->steps[i]);
+        if (rc) {
+            delete p;
+            return rc;
+        }
+    }
+    if (use_graph && n_nodes > 0) {
+        hipError_t e = hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal);
+        if (e == hipSuccess) {
+            run_steps(p->steps, g_stream);
+            e = hipStreamEndCapture(g_stream, &p->graph);
+        }
+        if (e == hipSuccess) e = hipGraphInstantiate(&p->exec, p->graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            lbr_set_error("lbr_plan_create: graph capture failed: %s", hipGetErrorString(e));
+            if (p->graph) hipGraphDestroy(p->graph);
+            delete p;
+            return LBR_ERR_HIP;
+        }
+    }
+    *out_plan = p;
+    return LBR_OK;
+}
+
+int lbr_plan_destroy(lbr_plan* p) {
+    if (!p) return LBR_OK;
+    if (p->exec) hipGraphExecDestroy(p->exec);
+    if (p->graph) hipGraphDestroy(p->graph);
+    delete p;
+    return LBR_OK;
+}
+
+int lbr_plan_num_nodes(const lbr_plan* p) { return p ? (int)p->steps.size() : 0; }
+
+int lbr_plan_launch(lbr_plan* p) {
+    if (!p) {
+        lbr_set_error("lbr_plan_launch: null plan");
+        return LBR_ERR_INVALID;
+    }
+    if (p->exec) {
+        HIP_TRY(hipGraphLaunch(p->exec, g_stream));
+    } else {
+        run_steps(p->steps, g_stream);
+        HIP_TRY(hipGetLastError());
+    }
+    return LBR_OK;
+}
+
+int lbr_synchronize(void) {
+    int rc = ensure_init();
+    if (rc) return rc;
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return LBR_OK;
+}
+
+int lbr_plan_time(lbr_plan* p, int iters, float* out_ms) {
+    if (!p || !out_ms || iters <= 0) {
+        lbr_set_error("lbr_plan_time: bad arguments");
+        return LBR_ERR_INVALID;
+    }
+    hipEvent_t a, b;
+    HIP_TRY(hipEventCreate(&a));
+    HIP_TRY(hipEventCreate(&b));
+    HIP_TRY(hipEventRecord(a, g_stream));
+    for (int i = 0; i < iters; ++i) {
+        int rc = lbr_plan_launch(p);
+        if (rc) {
+            (void)hipEventDestroy(a);
+            (void)hipEventDestroy(b);
+            return rc;
+        }
+    }
+    HIP_TRY(hipEventRecord(b, g_stream));
+    HIP_TRY(hipEventSynchronize(b));
+    float ms = 0.f;
+    HIP_TRY(hipEventElapsedTime(&ms, a, b));
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    *out_ms = ms;
+    return LBR_OK;
+}
+
+int lbr_plan_profile(lbr_plan* p, int iters, float* out_ms, int n_out) {
+    if (!p || !out_ms || iters <= 0 || n_out < (int)p->steps.size()) {
+        lbr_set_error("lbr_plan_profile: bad arguments");
+        return LBR_ERR_INVALID;
+    }
+    const size_t n = p->steps.size();
+    std::vector<hipEvent_t> ev(n + 1);
+    for (auto& e : ev) HIP_TRY(hipEventCreate(&e));
+    std::vector<double> acc(n, 0.0);
+    for (int it = 0; it < iters; ++it) {
+        HIP_TRY(hipEventRecord(ev[0], g_stream));
+        for (size_t i = 0; i < n; ++i) {
+            p->steps[i].run(p->steps[i], g_stream);
+            HIP_TRY(hipEventRecord(ev[i + 1], g_stream));
+        }
+        HIP_TRY(hipEventSynchronize(ev[n]));
+        HIP_TRY(hipGetLastError());
+        for (size_t i = 0; i < n; ++i) {
+            float ms = 0.f;
+            HIP_TRY(hipEventElapsedTime(&ms, ev[i], ev[i + 1]));
+            acc[i] += ms;
+        }
+    }
+    for (auto& e : ev) (void)hipEventDestroy(e);
+    for (size_t i = 0; i < n; ++i) out_ms[i] = (float)(acc[i] / iters);
+    return LBR_OK;
+}
+
+int lbr_plan_node_kernel(const lbr_plan* p, int index, char* name_out, int name_cap) {
+    if (!p || index < 0 || index >= (int)p->steps.size() || !name_out || name_cap <= 0) {
+        lbr_set_error("lbr_plan_node_kernel: bad arguments");
+        return LBR_ERR_INVALID;
+    }
+    snprintf(name_out, (size_t)name_cap, "%s", p->steps[index].name ? p->steps[index].name : "?");
+    return LBR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,430 @@
+// gemm.hip — fp32 GEMM on the gfx950 matrix cores (v_mfma_f32_32x32x2_f32).
+//
+// Replaces kernel_matmul_ab / kernel_matmul_gemv (csrc/ops/matmul.c:19-79,
+// cblas_sgemm / cblas_sgemv) behind MATMUL and MATMUL_ADD
+// (csrc/executor.c:197-224, 312-346):
+//   MATMUL      C = alpha · A · op(B)
+//   MATMUL_ADD  C = bias[n] + A · op(B)   (alpha is not applied: the
+//               reference hard-codes alpha = 1 on this path, executor.c:341/344)
+// op(B) = Bᵀ when trans_b (B stored [N, K], nn.Linear layout) else B ([K, N]).
+//
+// Tiling: a 256-thread workgroup (4 wavefronts, 2×2) owns a 128×128 tile of
+// C; each wavefront owns 64×64 = 2×2 MFMA blocks of 32×32 (64 accumulator
+// registers per lane).  K advances in steps of 32: the next A/B tiles are
+// fetched from global memory into registers while the current ones are
+// consumed from LDS (rows padded to 36 floats so 16-byte LDS reads are
+// conflict-free).  Each lane reads a float4 of 4 consecutive k for its row;
+// the four components feed four MFMAs, so one MFMA reduces over k and k+4
+// (the half-wave split of the 32x32x2 operand layout) — a reordering of the
+// K sum, exact in real arithmetic.
+//
+// Workgroups are numbered so that consecutive ids share an A row panel and
+// are mapped round-robin over the 8 XCDs by the hardware; the remap below
+// gives each XCD a contiguous range of tiles so neighbouring tiles (which
+// reuse the same A and B panels) hit the same L2.
+#include "lbr_device.h"
+
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 32, LDK = BK + 4;
+constexpr int NT = 256;
+constexpr int N_XCD = 8;
+constexpr int GROUP_M = 8;   // tile rows per L2 group
+
+struct GemmArgs {
+    const float* A;
+    const float* B;
+    float* C;
+    const float* bias;
+    int M, N, K;
+    long long sA, sB, sC;     // batch strides (elements)
+    float alpha;
+    int tiles_m, tiles_n;
+};
+
+__device__ __forceinline__ void tile_coords(const GemmArgs& g, int& tm, int& tn) {
+    // XCD-aware remap: hardware places workgroup id w on XCD w % 8.
+    const int tiles = g.tiles_m * g.tiles_n;
+    int w = blockIdx.x;
+    if (tiles % N_XCD == 0) {
+        const int per = tiles / N_XCD;
+        w = (w % N_XCD) * per + (w / N_XCD);
+    }
+    // grouped ordering: GROUP_M tile-rows advance together along N
+    const int group_size = GROUP_M * g.tiles_n;
+    const int gid = w / group_size;
+    const int first_m = gid * GROUP_M;
+    const int gm = min(g.tiles_m - first_m, GROUP_M);
+    const int in_group = w % group_size;
+    tm = first_m + in_group % gm;
+    tn = in_group / gm;
+}
+
+template <bool TRANS_B, bool VEC>
+__device__ __forceinline__ void load_tiles(const GemmArgs& g, const float* __restrict__ A, const float* __restrict__ B,
+                                           int m0, int n0, int k0, float4 (&ra)[4], float4 (&rb)[4]) {
+    const int tid = threadIdx.x;
+    if (VEC) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int idx = tid + p * NT;       // 0..1023
+            const int row = idx >> 3;           // 0..127
+            const int kc = (idx & 7) * 4;       // 0..28
+            const int gm = m0 + row, gk = k0 + kc;
+            ra[p] = (gm < g.M && gk < g.K) ? *reinterpret_cast<const float4*>(A + (long long)gm * g.K + gk)
+                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (TRANS_B) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int idx = tid + p * NT;
+                const int row = idx >> 3;
+                const int kc = (idx & 7) * 4;
+                const int gn = n0 + row, gk = k0 + kc;
+                rb[p] = (gn < g.N && gk < g.K) ? *reinterpret_cast<const float4*>(B + (long long)gn * g.K + gk)
+                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        } else {
+            // B is [K, N]: read 4 consecutive n of one k row
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int idx = tid + p * NT;   // 0..1023
+                const int kk = idx >> 5;        // 0..31
+                const int nc = (idx & 31) * 4;  // 0..124
+                const int gn = n0 + nc, gk = k0 + kk;
+                rb[p] = (gn < g.N && gk < g.K) ? *reinterpret_cast<const float4*>(B + (long long)gk * g.N + gn)
+                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    } else {
+        // scalar fallback: 16 elements of each tile per thread, packed into float4 slots
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            float v[4], w[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int idx = tid + (p * 4 + q) * NT;  // 0..4095
+                const int row = idx >> 5, kk = idx & 31;
+                const int gm = m0 + row, gk = k0 + kk;
+                v[q] = (gm < g.M && gk < g.K) ? A[(long long)gm * g.K + gk] : 0.f;
+                const int gn = n0 + row;
+                if (TRANS_B) w[q] = (gn < g.N && gk < g.K) ? B[(long long)gn * g.K + gk] : 0.f;
+                else w[q] = (gn < g.N && gk < g.K) ? B[(long long)gk * g.N + gn] : 0.f;
+            }
+            ra[p] = make_float4(v[0], v[1], v[2], v[3]);
+            rb[p] = make_float4(w[0], w[1], w[2], w[3]);
+        }
+    }
+}
+
+template <bool TRANS_B, bool VEC>
+__device__ __forceinline__ void store_tiles(float (*As)[LDK], float (*Bs)[LDK], const float4 (&ra)[4],
+                                            const float4 (&rb)[4]) {
+    const int tid = threadIdx.x;
+    if (VEC) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int idx = tid + p * NT;
+            const int row = idx >> 3, kc = (idx & 7) * 4;
+            *reinterpret_cast<float4*>(&As[row][kc]) = ra[p];
+        }
+        if (TRANS_B) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int idx = tid + p * NT;
+                const int row = idx >> 3, kc = (idx & 7) * 4;
+                *reinterpret_cast<float4*>(&Bs[row][kc]) = rb[p];
+            }
+        } else {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int idx = tid + p * NT;
+                const int kk = idx >> 5, nc = (idx & 31) * 4;
+                Bs[nc + 0][kk] = rb[p].x;
+                Bs[nc + 1][kk] = rb[p].y;
+                Bs[nc + 2][kk] = rb[p].z;
+                Bs[nc + 3][kk] = rb[p].w;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const float v[4] = {ra[p].x, ra[p].y, ra[p].z, ra[p].w};
+            const float w[4] = {rb[p].x, rb[p].y, rb[p].z, rb[p].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int idx = tid + (p * 4 + q) * NT;
+                const int row = idx >> 5, kk = idx & 31;
+                As[row][kk] = v[q];
+                Bs[row][kk] = w[q];
+            }
+        }
+    }
+}
+
+template <bool TRANS_B, bool VEC, bool HAS_BIAS>
+__global__ __launch_bounds__(NT, 2) void gemm_mfma_f32(GemmArgs g) {
+    __shared__ float As[BM][LDK];
+    __shared__ float Bs[BN][LDK];
+
+    int tm, tn;
+    tile_coords(g, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const long long bz = blockIdx.z;
+    const float* __restrict__ A = g.A + bz * g.sA;
+    const float* __restrict__ B = g.B + bz * g.sB;
+    float* __restrict__ C = g.C + bz * g.sC;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lrow = lane & 31, lhalf = lane >> 5;
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    float4 ra[4], rb[4];
+    const int nk = (g.K + BK - 1) / BK;
+    load_tiles<TRANS_B, VEC>(g, A, B, m0, n0, 0, ra, rb);
+    store_tiles<TRANS_B, VEC>(As, Bs, ra, rb);
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; ++kt) {
+        if (kt + 1 < nk) load_tiles<TRANS_B, VEC>(g, A, B, m0, n0, (kt + 1) * BK, ra, rb);
+#pragma unroll
+        for (int c = 0; c < BK / 8; ++c) {
+            const int kc = c * 8 + lhalf * 4;
+            floatx4 a[2], b[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                a[i] = *reinterpret_cast<const floatx4*>(&As[wm * 64 + i * 32 + lrow][kc]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                b[j] = *reinterpret_cast<const floatx4*>(&Bs[wn * 64 + j * 32 + lrow][kc]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+        if (kt + 1 < nk) {
+            store_tiles<TRANS_B, VEC>(As, Bs, ra, rb);
+            __syncthreads();
+        }
+    }
+
+    // Epilogue.  Accumulator layout of the 32x32 block: lane l, register r
+    // holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = n0 + wn * 64 + j * 32 + lrow;
+            if (n >= g.N) continue;
+            const float bv = HAS_BIAS ? g.bias[n] : 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+                if (m < g.M) {
+                    const float v = acc[i][j][r];
+                    C[(long long)m * g.N + n] = HAS_BIAS ? (v + bv) : g.alpha * v;
+                }
+            }
+        }
+}
+
+// ---------------------------------------------------------------- GEMV
+// M == 1 (decode): the reference switches to sgemv here (executor.c:217).
+// trans_b: one wavefront per output column, lanes stride over K.
+template <bool VEC, bool HAS_BIAS>
+__global__ __launch_bounds__(256) void gemv_t(GemmArgs g) {
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= g.N) return;
+    const long long bz = blockIdx.y;
+    const float* __restrict__ a = g.A + bz * g.sA;
+    const float* __restrict__ b = g.B + bz * g.sB + (long long)n * g.K;
+    float acc = 0.f;
+    if (VEC) {
+        const int k4 = g.K / 4;
+        const float4* a4 = reinterpret_cast<const float4*>(a);
+        const float4* b4 = reinterpret_cast<const float4*>(b);
+        for (int k = lane; k < k4; k += 64) {
+            const float4 x = a4[k], y = b4[k];
+            acc += (x.x * y.x + x.y * y.y) + (x.z * y.z + x.w * y.w);
+        }
+    } else {
+        for (int k = lane; k < g.K; k += 64) acc += a[k] * b[k];
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) {
+        float* c = g.C + bz * g.sC;
+        c[n] = HAS_BIAS ? acc + g.bias[n] : g.alpha * acc;
+    }
+}
+
+// B is [K, N]: one thread per output column, loop over K (coalesced over n).
+template <bool HAS_BIAS>
+__global__ __launch_bounds__(256) void gemv_n(GemmArgs g) {
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= g.N) return;
+    const long long bz = blockIdx.y;
+    const float* __restrict__ a = g.A + bz * g.sA;
+    const float* __restrict__ b = g.B + bz * g.sB;
+    float acc = 0.f;
+    for (int k = 0; k < g.K; ++k) acc += a[k] * b[(long long)k * g.N + n];
+    float* c = g.C + bz * g.sC;
+    c[n] = HAS_BIAS ? acc + g.bias[n] : g.alpha * acc;
+}
+
+// Step::i: [0]=M [1]=N [2]=K [3]=batches [4]=trans_b [5]=vec [6]=has_bias
+//          [7]=sA [8]=sB [9]=sC ; f[0] = alpha
+GemmArgs make_args(const Step& s) {
+    GemmArgs g;
+    g.A = (const float*)s.in[0];
+    g.B = (const float*)s.in[1];
+    g.bias = (const float*)s.in[2];
+    g.C = (float*)s.out;
+    g.M = (int)s.i[0];
+    g.N = (int)s.i[1];
+    g.K = (int)s.i[2];
+    g.sA = s.i[7];
+    g.sB = s.i[8];
+    g.sC = s.i[9];
+    g.alpha = s.f[0];
+    g.tiles_m = (g.M + BM - 1) / BM;
+    g.tiles_n = (g.N + BN - 1) / BN;
+    return g;
+}
+
+template <bool TRANS_B, bool VEC, bool HAS_BIAS>
+void launch_gemm_t(const Step& s, hipStream_t st) {
+    GemmArgs g = make_args(s);
+    if (g.M <= 0 || g.N <= 0) return;
+    dim3 grid(g.tiles_m * g.tiles_n, 1, (unsigned)s.i[3]);
+    hipLaunchKernelGGL((gemm_mfma_f32<TRANS_B, VEC, HAS_BIAS>), grid, dim3(NT), 0, st, g);
+}
+
+template <bool VEC, bool HAS_BIAS>
+void launch_gemv_t(const Step& s, hipStream_t st) {
+    GemmArgs g = make_args(s);
+    if (g.N <= 0) return;
+    hipLaunchKernelGGL((gemv_t<VEC, HAS_BIAS>), dim3((g.N + 3) / 4, (unsigned)s.i[3]), dim3(256), 0, st, g);
+}
+
+template <bool HAS_BIAS>
+void launch_gemv_n(const Step& s, hipStream_t st) {
+    GemmArgs g = make_args(s);
+    if (g.N <= 0) return;
+    hipLaunchKernelGGL((gemv_n<HAS_BIAS>), dim3((g.N + 255) / 256, (unsigned)s.i[3]), dim3(256), 0, st, g);
+}
+
+void zero_k_fill(const Step& s, hipStream_t st);
+
+// K == 0: C = bias (MATMUL_ADD) or 0.
+__global__ void fill_rows(float* C, const float* bias, long long rows, int N) {
+    const long long n = rows * N;
+    for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n;
+         i += (long long)gridDim.x * blockDim.x)
+        C[i] = bias ? bias[i % N] : 0.f;
+}
+
+void zero_k_fill(const Step& s, hipStream_t st) {
+    const long long rows = s.i[0] * s.i[3];
+    const int N = (int)s.i[1];
+    if (rows * N <= 0) return;
+    hipLaunchKernelGGL(fill_rows, dim3(lbr_grid(rows * N, 256, 4096)), dim3(256), 0, st, (float*)s.out,
+                       s.i[6] ? (const float*)s.in[2] : nullptr, rows, N);
+}
+
+}  // namespace
+
+// MATMUL extras [K, trans_b, b_is_2d, alpha_bits] (alpha_bits 0 ⇒ 1.0);
+// MATMUL_ADD inputs [A, B, bias] with the same extras (executor.c:197-224,
+// 312-346).  M == 1 goes to the GEMV kernels as in the reference.
+int decode_matmul(const OpNode* n, Step* s) {
+    const bool has_bias = n->op == OP_MATMUL_ADD;
+    const int need = has_bias ? 3 : 2;
+    if (n->n_inputs < need || !n->output || n->n_dims < 1) {
+        lbr_set_error("matmul: expected %d inputs, an output and n_dims >= 1", need);
+        return LBR_ERR_INVALID;
+    }
+    for (int i = 0; i < need; ++i)
+        if (!n->inputs[i]) {
+            lbr_set_error("matmul: input %d is null", i);
+            return LBR_ERR_INVALID;
+        }
+    const int N = n->out_shape[n->n_dims - 1];
+    const int K = n->extra[0];
+    const int trans_b = n->extra[1] != 0;
+    const int b_is_2d = n->extra[2] != 0;
+    const float alpha = n->extra[3] ? node_extra_float(n, 3) : 1.0f;
+    long long M, batches;
+    if (b_is_2d) {
+        M = node_leading(n);
+        batches = 1;
+    } else {
+        if (n->n_dims < 2) {
+            lbr_set_error("matmul: batched form needs n_dims >= 2");
+            return LBR_ERR_INVALID;
+        }
+        M = n->out_shape[n->n_dims - 2];
+        batches = 1;
+        for (int i = 0; i < n->n_dims - 2; ++i) batches *= n->out_shape[i];
+    }
+    if (M > INT32_MAX || N < 0 || K < 0 || batches > 65535) {
+        lbr_set_error("matmul: unsupported sizes M=%lld N=%d K=%d batches=%lld", M, N, K, batches);
+        return LBR_ERR_UNSUPPORTED;
+    }
+    s->in[0] = n->inputs[0];
+    s->in[1] = n->inputs[1];
+    s->in[2] = has_bias ? n->inputs[2] : nullptr;
+    s->out = n->output;
+    s->i[0] = M;
+    s->i[1] = N;
+    s->i[2] = K;
+    s->i[3] = batches;
+    s->i[4] = trans_b;
+    s->i[6] = has_bias;
+    s->i[7] = M * (long long)K;
+    s->i[8] = (long long)N * K;
+    s->i[9] = M * (long long)N;
+    s->f[0] = has_bias ? 1.0f : alpha;
+    if (K == 0) {
+        s->run = zero_k_fill;
+        s->name = "matmul_k0";
+        return LBR_OK;
+    }
+    if (M == 1) {
+        if (trans_b) {
+            const bool vec = K % 4 == 0 && lbr_aligned(n->inputs[0], 16) && lbr_aligned(n->inputs[1], 16);
+            s->run = vec ? (has_bias ? launch_gemv_t<true, true> : launch_gemv_t<true, false>)
+                         : (has_bias ? launch_gemv_t<false, true> : launch_gemv_t<false, false>);
+            s->name = "gemv_t";
+        } else {
+            s->run = has_bias ? launch_gemv_n<true> : launch_gemv_n<false>;
+            s->name = "gemv_n";
+        }
+        return LBR_OK;
+    }
+    const bool vec = lbr_aligned(n->inputs[0], 16) && lbr_aligned(n->inputs[1], 16) && K % 4 == 0 &&
+                     (trans_b || N % 4 == 0);
+    if (trans_b) {
+        if (vec) s->run = has_bias ? launch_gemm_t<true, true, true> : launch_gemm_t<true, true, false>;
+        else s->run = has_bias ? launch_gemm_t<true, false, true> : launch_gemm_t<true, false, false>;
+        s->name = "gemm_mfma_f32_nt";
+    } else {
+        if (vec) s->run = has_bias ? launch_gemm_t<false, true, true> : launch_gemm_t<false, true, false>;
+        else s->run = has_bias ? launch_gemm_t<false, false, true> : launch_gemm_t<false, false, false>;
+        s->name = "gemm_mfma_f32_nn";
+    }
+    return LBR_OK;
+}

@@ -1,0 +1,131 @@
+// lbr_device.h — device-side helpers shared by the gfx950 kernels, and the
+// decoded-launch record (`Step`) the executor builds from each OpNode.
+//
+// Wavefronts are 64 lanes wide on CDNA4; every reduction here is written for
+// that width (no 32-lane warp assumptions).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/lbr_executor.h"
+
+#define LBR_WAVE 64
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// ---------------------------------------------------------------------------
+// Wave / block reductions (64-lane wavefronts)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, LBR_WAVE);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, LBR_WAVE));
+    return v;
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (<= 1024).  `red` must hold
+// at least blockDim.x/64 floats.  All threads get the result.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    const int lane = threadIdx.x & (LBR_WAVE - 1);
+    const int wid = threadIdx.x / LBR_WAVE;
+    const int nw = blockDim.x / LBR_WAVE;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < nw; ++i) t += red[i];
+    return t;
+}
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+    const int lane = threadIdx.x & (LBR_WAVE - 1);
+    const int wid = threadIdx.x / LBR_WAVE;
+    const int nw = blockDim.x / LBR_WAVE;
+    v = wave_max(v);
+    __syncthreads();
+    if (lane == 0) red[wid] = v;
+    __syncthreads();
+    float t = red[0];
+    for (int i = 1; i < nw; ++i) t = fmaxf(t, red[i]);
+    return t;
+}
+
+// ---------------------------------------------------------------------------
+// Decoded launch record
+// ---------------------------------------------------------------------------
+//
+// Each OpNode decodes (once, at plan creation) into one Step: the host
+// launcher to call plus every argument it needs, already validated.
+struct Step;
+typedef void (*step_fn)(const Step&, hipStream_t);
+
+struct Step {
+    step_fn run;
+    const char* name;         // kernel name for reports
+    int node_index;
+    const void* in[MAX_INPUTS];
+    void* out;
+    int n_in;
+    long long i[40];          // integer parameters (meaning per launcher)
+    float f[4];               // float parameters
+};
+
+static inline bool lbr_aligned(const void* p, size_t a) {
+    return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+static inline unsigned lbr_grid(long long work, int per_block, unsigned cap) {
+    long long g = (work + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > (long long)cap) g = cap;
+    return (unsigned)g;
+}
+
+// Decoders, one per op family (each returns LBR_OK or an error code after
+// setting the thread's error message through lbr_set_error()).
+void lbr_set_error(const char* fmt, ...);
+
+int decode_unary(const OpNode* n, Step* s);
+int decode_binary(const OpNode* n, Step* s);
+int decode_bias_relu(const OpNode* n, Step* s);
+int decode_gated_act(const OpNode* n, Step* s);
+int decode_reduce(const OpNode* n, Step* s);
+int decode_softmax(const OpNode* n, Step* s);
+int decode_layernorm(const OpNode* n, Step* s);
+int decode_rmsnorm(const OpNode* n, Step* s);
+int decode_reshape(const OpNode* n, Step* s);
+int decode_transpose(const OpNode* n, Step* s);
+int decode_slice(const OpNode* n, Step* s);
+int decode_cat(const OpNode* n, Step* s);
+int decode_embedding(const OpNode* n, Step* s);
+int decode_matmul(const OpNode* n, Step* s);
+int decode_attention(const OpNode* n, Step* s);
+
+// Helpers over the node record (same meaning as csrc/executor.c:30-48).
+static inline long long node_total(const OpNode* n) {
+    long long t = 1;
+    for (int i = 0; i < n->n_dims; ++i) t *= n->out_shape[i];
+    return t;
+}
+static inline long long node_leading(const OpNode* n) {
+    long long r = 1;
+    for (int i = 0; i < n->n_dims - 1; ++i) r *= n->out_shape[i];
+    return r;
+}
+static inline int node_last_dim(const OpNode* n) {
+    return n->n_dims > 0 ? n->out_shape[n->n_dims - 1] : 1;
+}
+static inline float node_extra_float(const OpNode* n, int idx) {
+    union { int i; float f; } u;
+    u.i = n->extra[idx];
+    return u.f;
+}

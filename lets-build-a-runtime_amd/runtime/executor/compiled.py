@@ -1,0 +1,285 @@
+"""Compiled executor on the MI355X: the whole plan as one hipGraph replay.
+
+Drop-in for the reference's CompiledExecutor (runtime/executor/compiled.py:
+20-157): ``compile(plan)`` once, ``run(inputs) -> outputs`` many times, same
+node filtering and OpNode contents.  What changes is where memory lives:
+
+* the arena is one device allocation of ``plan.arena_size`` bytes; every
+  intermediate is at ``arena + plan.offsets[name]`` and every scratch slot
+  at ``arena + plan.scratch[id][0]`` — the planner's layout, byte for byte;
+* constants are uploaded once into one device block (256-byte aligned
+  slots);
+* each graph input gets a fixed device staging buffer, so node pointers
+  never change after compile and the launch sequence can be captured into a
+  hipGraph once and replayed (``run`` = H2D inputs, graph launch, D2H
+  outputs).
+
+``launch()`` / ``synchronize()`` / ``time_launches()`` / ``profile_nodes()``
+run the plan on device-resident data for benchmarking.  There is no CPU
+fallback: a missing library or GPU raises at compile.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import time
+
+import numpy as np
+
+from ..ir import Graph, OpType
+from ..planner import MemoryPlan
+from .common import Executor, OpTiming, RunProfile
+from .hip_lib import HipLibrary, load_library
+from .nodes import build_nodes, check_extents, dispatch_order
+
+_ALIGN = 256
+
+
+def _align(n: int) -> int:
+    return (n + _ALIGN - 1) // _ALIGN * _ALIGN
+
+
+class DeviceWeights:
+    """Constants resident in one device block, keyed by tensor name."""
+
+    def __init__(self, lib: HipLibrary, graph: Graph, names: list[str]) -> None:
+        self._lib = lib
+        self.offsets: dict[str, int] = {}
+        self.keys: dict[str, tuple[int, int]] = {}
+        total = 0
+        for n in names:
+            buf = graph.tensors[n].buffer
+            if buf is None:
+                raise ValueError(f"constant '{n}' has no data")
+            self.offsets[n] = total
+            total += _align(buf.nbytes)
+        self.nbytes = total
+        self.base = lib.alloc(total) if total else 0
+        for n in names:
+            buf = np.ascontiguousarray(graph.tensors[n].buffer)
+            if buf.nbytes:
+                lib.h2d(self.base + self.offsets[n], buf.ctypes.data, buf.nbytes)
+            self.keys[n] = (id(graph.tensors[n].buffer), buf.nbytes)
+
+    def covers(self, graph: Graph, names: list[str]) -> bool:
+        """True if every named constant is resident with the same buffer object."""
+        for n in names:
+            t = graph.tensors.get(n)
+            if n not in self.keys or t is None or t.buffer is None or self.keys[n] != (id(t.buffer), t.buffer.nbytes):
+                return False
+        return True
+
+    def addr(self, name: str) -> int:
+        return self.base + self.offsets[name]
+
+    def free(self) -> None:
+        if self.base:
+            self._lib.free(self.base)
+            self.base = 0
+
+
+class CompiledExecutor(Executor):
+    """Plan → device OpNode array → hipGraph, replayed per run()."""
+
+    def __init__(self, profile: bool = False, use_graph: bool = True, device: int = 0,
+                 weights: DeviceWeights | None = None) -> None:
+        super().__init__(profile=profile)
+        self._use_graph = use_graph
+        self._device = device
+        self._lib: HipLibrary | None = None
+        self._graph: Graph | None = None
+        self._plan_handle = ctypes.c_void_p()
+        self._nodes = None
+        self._order = []
+        self._arena = 0
+        # weights handed over by a previous executor (Session.rebind) become ours
+        self._weights: DeviceWeights | None = weights
+        self._owns_weights = True
+        self._inputs: dict[str, tuple[int, int]] = {}   # name -> (device ptr, nbytes)
+        self._addr: dict[str, int] = {}
+
+    # ------------------------------------------------------------------ compile
+    def compile(self, plan: MemoryPlan) -> None:
+        self.close()
+        lib = load_library(self._device)
+        self._lib = lib
+        graph = plan.graph
+        self._graph = graph
+        external = set(graph.inputs) | set(graph.constants)
+
+        # constants referenced by dispatched nodes (and constant outputs)
+        order = dispatch_order(plan)
+        check_extents(order, graph)
+        for node in order:
+            if not lib.lbr_op_supported(node.op.value):
+                raise RuntimeError(f"Op {node.op.name} (node {node.id}) has no device kernel")
+        used_consts: list[str] = []
+        seen = set()
+        for node in order:
+            for t in node.inputs:
+                if t in graph.constants and t not in seen:
+                    seen.add(t)
+                    used_consts.append(t)
+        for t in graph.outputs:
+            if t in graph.constants and t not in seen:
+                seen.add(t)
+                used_consts.append(t)
+
+        if self._weights is None or not self._weights.covers(graph, used_consts):
+            if self._weights is not None and self._owns_weights:
+                self._weights.free()
+            self._weights = DeviceWeights(lib, graph, used_consts)
+            self._owns_weights = True
+
+        self._arena = lib.alloc(max(plan.arena_size, 1))
+        self._inputs = {}
+        for name in graph.inputs:
+            t = graph.tensors[name]
+            nb = int(np.prod(t.shape)) * np.dtype(t.dtype).itemsize
+            self._inputs[name] = (lib.alloc(max(nb, 1)), nb)
+
+        addr: dict[str, int] = {}
+        for name, off in plan.offsets.items():
+            if name not in external:
+                addr[name] = self._arena + off
+        for name, (ptr, _) in self._inputs.items():
+            addr[name] = ptr
+        for name in used_consts:
+            addr[name] = self._weights.addr(name)
+        self._addr = addr
+
+        def resolve(name: str) -> int:
+            if name not in addr:
+                raise RuntimeError(f"tensor '{name}' has no device address (not an input, constant or "
+                                   f"planned intermediate)")
+            return addr[name]
+
+        arr, order = build_nodes(plan, resolve, lambda off, size: self._arena + off)
+        for i, node in enumerate(order):
+            if node.op == OpType.EMBEDDING:
+                # device kernel bounds-checks ids against the table's row count
+                arr[i].extra[1] = graph.tensors[node.inputs[1]].shape[0]
+        self._nodes = arr
+        self._order = order
+        handle = ctypes.c_void_p()
+        lib.check(lib.lbr_plan_create(arr, len(order), 1 if self._use_graph else 0, ctypes.byref(handle)),
+                  "lbr_plan_create")
+        self._plan_handle = handle
+
+    # ------------------------------------------------------------------ run
+    def _upload_inputs(self, inputs: dict[str, np.ndarray]) -> None:
+        graph = self._graph
+        for name, (ptr, nb) in self._inputs.items():
+            if name not in inputs:
+                raise ValueError(f"Missing input tensor: '{name}'")
+            t = graph.tensors[name]
+            arr = np.ascontiguousarray(inputs[name])
+            if arr.dtype != np.dtype(t.dtype):
+                raise ValueError(f"input '{name}' is {arr.dtype}, graph expects {t.dtype}")
+            if arr.nbytes != nb:
+                raise ValueError(f"input '{name}' has shape {arr.shape}, graph expects {t.shape}")
+            self._lib.h2d(ptr, arr.ctypes.data, nb)
+
+    def _download_outputs(self) -> dict[str, np.ndarray]:
+        graph = self._graph
+        out = {}
+        for name in graph.outputs:
+            t = graph.tensors[name]
+            host = np.empty(t.shape, dtype=np.dtype(t.dtype))
+            if host.nbytes:
+                self._lib.d2h(host.ctypes.data, self._addr[name], host.nbytes)
+            out[name] = host
+        return out
+
+    def run(self, inputs: dict[str, np.ndarray]) -> dict[str, np.ndarray]:
+        if self._lib is None:
+            raise RuntimeError("CompiledExecutor.run() before compile()")
+        self._upload_inputs(inputs)
+        if self._profile:
+            times = self.profile_nodes(1)
+            self._last_profile = RunProfile(
+                op_timings=[OpTiming(node.id, node.op.name, int(ms * 1e6), node.output,
+                                     tuple(self._graph.tensors[node.output].shape))
+                            for node, ms in zip(self._order, times)],
+                total_ns=int(sum(times) * 1e6))
+        else:
+            t0 = time.perf_counter_ns()
+            self.launch()
+            self.synchronize()
+            self._last_profile = RunProfile(total_ns=time.perf_counter_ns() - t0)
+        return self._download_outputs()
+
+    # ------------------------------------------------------------------ device-resident API
+    def upload_inputs(self, inputs: dict[str, np.ndarray]) -> None:
+        self._upload_inputs(inputs)
+
+    def download_outputs(self) -> dict[str, np.ndarray]:
+        return self._download_outputs()
+
+    def launch(self) -> None:
+        self._lib.check(self._lib.lbr_plan_launch(self._plan_handle), "lbr_plan_launch")
+
+    def synchronize(self) -> None:
+        self._lib.check(self._lib.lbr_synchronize(), "lbr_synchronize")
+
+    def time_launches(self, iters: int) -> float:
+        """Milliseconds for ``iters`` back-to-back launches (hipEvents on the library stream)."""
+        ms = ctypes.c_float()
+        self._lib.check(self._lib.lbr_plan_time(self._plan_handle, int(iters), ctypes.byref(ms)), "lbr_plan_time")
+        return float(ms.value)
+
+    def profile_nodes(self, iters: int = 1) -> list[float]:
+        """Mean milliseconds per dispatched node (eager launches, hipEvent pairs)."""
+        n = len(self._order)
+        buf = (ctypes.c_float * max(n, 1))()
+        self._lib.check(self._lib.lbr_plan_profile(self._plan_handle, int(iters), buf, max(n, 1)),
+                        "lbr_plan_profile")
+        return [float(buf[i]) for i in range(n)]
+
+    def kernel_names(self) -> list[str]:
+        names = []
+        for i in range(len(self._order)):
+            b = ctypes.create_string_buffer(64)
+            self._lib.check(self._lib.lbr_plan_node_kernel(self._plan_handle, i, b, 64), "lbr_plan_node_kernel")
+            names.append(b.value.decode())
+        return names
+
+    @property
+    def dispatch_order(self):
+        return list(self._order)
+
+    @property
+    def weights(self) -> DeviceWeights | None:
+        return self._weights
+
+    def device_address(self, name: str) -> int:
+        return self._addr[name]
+
+    # ------------------------------------------------------------------ teardown
+    def close(self) -> None:
+        lib = self._lib
+        if lib is None:
+            return
+        if self._plan_handle:
+            lib.lbr_plan_destroy(self._plan_handle)
+            self._plan_handle = ctypes.c_void_p()
+        for ptr, _ in self._inputs.values():
+            lib.free(ptr)
+        self._inputs = {}
+        if self._arena:
+            lib.free(self._arena)
+            self._arena = 0
+        if self._weights is not None and self._owns_weights:
+            self._weights.free()
+            self._weights = None
+
+    def release_weights(self) -> DeviceWeights | None:
+        """Hand the resident weights to another executor (Session.rebind); this one stops owning them."""
+        self._owns_weights = False
+        return self._weights
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
