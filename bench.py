@@ -1,0 +1,281 @@
+#!/usr/bin/env python3
+"""Benchmark: fp32 forward of a BASELINE workload through Session on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 7b4k]
+
+A step is one forward pass (Session's compiled plan, replayed as a hipGraph)
+over one batch of synthetic input that is already resident in HBM.  W
+untimed warm-up steps, then exactly K steps between two device
+synchronisations; ms_per_step is host wall time / K (hipEvent time on the
+library stream is reported beside it).  value = tokens/s = batch·seq /
+(ms_per_step/1000).
+
+Also reported, on the same JSON line:
+  roofline      dominant kernel (largest share of device time): algorithmic
+                FLOPs (or bytes) per launch ÷ its mean launch duration,
+                measured with hipEvent pairs on the library stream over K
+                eager steps, against MI355X peak (fp32 MFMA 157.3 TFLOP/s,
+                HBM 8 TB/s); `traffic` = HBM bytes per launch from the
+                committed rocprofv3 counter summary when one exists;
+  kernels       the same per-kernel figures for every kernel in the step;
+  parity        GPU output vs the CPU oracle on the same plan and input;
+  cpu_baseline  the oracle (C restatement of the reference CPU executor),
+                one forward of the same workload on the host's cores.
+
+Only one GPU is used; --gpus above 1 exits with a message.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT / "lets-build-a-runtime_amd"), str(ROOT)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+METRIC = "fp32 forward latency (ms) + tokens/s per shape; MFMA % and HBM GB/s of roofline"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- per-node work
+
+def node_work(node, graph) -> tuple[float, float]:
+    """(algorithmic FLOPs, algorithmic HBM bytes) of one dispatched node.
+
+    GEMM: 2·M·N·K flops, bytes = A + B + C (+ bias).  Attention: 4·bh·S²·hd,
+    halved when causal; bytes = Q + K + V + O.  Memory-bound ops: minimum
+    traffic, every input element read once and the output written once.
+    """
+    from runtime.ir import OpType
+    from runtime.ops import OP_REGISTRY
+
+    def numel(name):
+        n = 1
+        for d in graph.tensors[name].shape:
+            n *= d
+        return n
+
+    def nbytes(name):
+        return numel(name) * np.dtype(graph.tensors[name].dtype).itemsize
+
+    out_b = nbytes(node.output)
+    op = node.op
+    if op in (OpType.MATMUL, OpType.MATMUL_ADD):
+        ex = OP_REGISTRY[op].extras(node, graph)
+        K = ex[0]
+        shape = graph.tensors[node.output].shape
+        flops = 2.0 * numel(node.output) * K
+        return flops, float(sum(nbytes(t) for t in node.inputs) + out_b)
+    if op == OpType.ATTENTION:
+        q = graph.tensors[node.inputs[0]].shape
+        bh = int(np.prod(q[:-2]))
+        s, hd = q[-2], q[-1]
+        flops = 4.0 * bh * s * s * hd * (0.5 if node.attrs.get("causal") else 1.0)
+        return flops, float(sum(nbytes(t) for t in node.inputs[:3]) + out_b)
+    return 0.0, float(sum(nbytes(t) for t in node.inputs) + out_b)
+
+
+def kernel_table(names, order, graph, ms):
+    """Aggregate per-node device times by kernel name."""
+    agg: dict[str, dict] = {}
+    for name, node, t in zip(names, order, ms):
+        f, b = node_work(node, graph)
+        a = agg.setdefault(name, {"kernel": name, "launches": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0})
+        a["launches"] += 1
+        a["ms"] += t
+        a["flops"] += f
+        a["bytes"] += b
+    rows = []
+    total = sum(a["ms"] for a in agg.values()) or 1.0
+    for a in agg.values():
+        sec = a["ms"] / 1e3
+        mfma = a["flops"] > 0
+        achieved = (a["flops"] / sec / 1e12) if mfma else (a["bytes"] / sec / 1e9)
+        peak = PEAK_FP32_MFMA_TFLOPS if mfma else PEAK_HBM_GBS
+        rows.append({
+            "kernel": a["kernel"], "launches": a["launches"], "ms_per_step": round(a["ms"], 4),
+            "share": round(a["ms"] / total, 4), "bound": "mfma" if mfma else "hbm",
+            "achieved": round(achieved, 2), "unit": "TFLOP/s" if mfma else "GB/s", "frac": round(achieved / peak, 4),
+            "flops_per_launch": a["flops"] / a["launches"], "bytes_per_launch": a["bytes"] / a["launches"],
+            "mean_launch_us": round(a["ms"] * 1e3 / a["launches"], 2),
+        })
+    rows.sort(key=lambda r: r["ms_per_step"], reverse=True)
+    return rows
+
+
+def committed_traffic(kernel: str, workload: str):
+    """HBM bytes per launch from profiles/traffic_<kernel>_<workload>.json (rocprofv3 --pmc), if committed."""
+    p = ROOT / "profiles" / f"traffic_{kernel}_{workload}.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+def calibrate_copy(mib: int) -> int:
+    """Run the device copy kernel (a RESHAPE node through lbr_execute) over `mib` MiB, 5 times.
+
+    Under ``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` its per-dispatch
+    counters read ≈ mib·1024 KiB each; the ratio scales the counters of the
+    benchmarked kernels to bytes.
+    """
+    from runtime.executor.common import COpNode
+    from runtime.executor.hip_lib import load_library
+    lib = load_library(0)
+    n = mib * 2**20
+    src, dst = lib.alloc(n), lib.alloc(n)
+    host = np.arange(n // 4, dtype=np.float32)
+    lib.h2d(src, host.ctypes.data, n)
+    node = (COpNode * 1)()
+    node[0].op = 500  # RESHAPE of an external buffer = plain copy
+    node[0].n_inputs = 1
+    node[0].inputs[0] = src
+    node[0].output = dst
+    node[0].n_dims = 1
+    node[0].out_shape[0] = n // 4
+    node[0].elem_size = 4
+    for _ in range(5):
+        lib.check(lib.lbr_execute(node, 1), "lbr_execute(copy)")
+    back = np.empty_like(host)
+    lib.d2h(back.ctypes.data, dst, n)
+    ok = bool(np.array_equal(back, host))
+    lib.free(src)
+    lib.free(dst)
+    print(json.dumps({"calibration": "copy", "bytes_read": n, "bytes_written": n, "dispatches": 5, "ok": ok}))
+    return 0 if ok else 1
+
+
+# ---------------------------------------------------------------- main
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="7b4k", help="workload key (toy, gpt2w, gpt2, 7b4k, qwen3_4b)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-parity", action="store_true", help="skip the GPU-vs-oracle output check")
+    ap.add_argument("--eager", action="store_true", help="launch node by node instead of replaying a hipGraph")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run the library's copy kernel over MIB MiB, 5 times (reference for HBM counters)")
+    args = ap.parse_args()
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(the multi-GPU sharding is a design note only; nothing here launches collectives)",
+              file=sys.stderr)
+        return 2
+
+    from runtime.session import Session
+    from workloads import WORKLOADS, export_workload
+
+    wl = WORKLOADS[args.config]
+    t0 = time.time()
+    model, x, graph = export_workload(args.config)
+    del model
+    sess = Session(graph)
+    sess.create(use_graph=not args.eager)
+    ex = sess.executor
+    log(f"[bench] {wl.title}: export+optimise+plan+compile {time.time() - t0:.1f}s, "
+        f"{len(ex.dispatch_order)} kernels/step, arena {sess.plan_stats.arena_bytes / 2**20:.1f} MiB")
+
+    ex.upload_inputs({graph.inputs[0]: x})
+    ex.synchronize()
+    for _ in range(args.warmup):
+        ex.launch()
+    ex.synchronize()
+
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        ex.launch()
+    ex.synchronize()
+    wall_ms = (time.perf_counter() - t_start) * 1e3 / args.steps
+    event_ms = ex.time_launches(args.steps) / args.steps
+    ms_per_step = wall_ms
+    tokens = x.shape[0] * x.shape[1]
+    log(f"[bench] {args.steps} steps: {wall_ms:.3f} ms/step wall, {event_ms:.3f} ms/step hipEvent")
+
+    # per-kernel device time (eager launches, hipEvent pairs on the library stream)
+    names = ex.kernel_names()
+    node_ms = ex.profile_nodes(max(1, min(args.steps, 20)))
+    rows = kernel_table(names, ex.dispatch_order, sess.resolved_graph, node_ms)
+    dom = rows[0]
+    for r in rows:
+        log(f"[bench]   {r['kernel']:<22} x{r['launches']:<3} {r['ms_per_step']:8.3f} ms "
+            f"({100 * r['share']:5.1f}%)  {r['achieved']:9.2f} {r['unit']:<8} {100 * r['frac']:5.1f}% of peak")
+
+    y = ex.download_outputs()[graph.outputs[0]]
+    parity = None
+    cpu = None
+    if not (args.no_parity and args.no_cpu):
+        from oracle.host_exec import OracleRun, num_threads
+        orc = OracleRun(sess.memory_plan)
+        t1 = time.perf_counter()
+        o = orc.run({graph.inputs[0]: x})[graph.outputs[0]]
+        cpu_s = time.perf_counter() - t1
+        err = float(np.abs(y.astype(np.float64) - o).max())
+        rel = err / float(np.abs(o).max())
+        parity = {"vs": "cpu oracle, same plan and input", "max_abs_err": err, "normwise_rel_err": rel,
+                  "tolerance": 1e-3, "ok": bool(np.isfinite(y).all() and rel <= 1e-3)}
+        log(f"[bench] parity vs oracle: normwise rel {rel:.3e}, max abs {err:.3e}")
+        if not args.no_cpu:
+            cpu = {"value": round(tokens / cpu_s, 2), "unit": "tokens/s", "cores": num_threads(),
+                   "kind": "port", "ms_per_step": round(cpu_s * 1e3, 1),
+                   "sample": f"one full forward of the same workload ({wl.title}) on the CPU oracle "
+                             f"(C restatement of the reference compiled executor, OpenMP)"}
+            log(f"[bench] cpu oracle: {cpu_s:.2f} s/forward on {num_threads()} threads")
+
+    traffic = committed_traffic(dom["kernel"], args.config)
+    result = {
+        "metric": METRIC,
+        "value": round(tokens / (ms_per_step / 1e3), 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "event_ms_per_step": round(event_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) input, random-init N(0,0.02) weights)",
+        "config": {"workload": args.config, "title": wl.title, "batch": int(x.shape[0]),
+                   "seq_len": int(x.shape[1]), "d_model": int(x.shape[2]),
+                   "graph": "hipGraph replay" if not args.eager else "eager launches",
+                   "kernels_per_step": len(ex.dispatch_order)},
+        "roofline": {"kernel": dom["kernel"], "bound": dom["bound"], "achieved": dom["achieved"],
+                     "peak": PEAK_FP32_MFMA_TFLOPS if dom["bound"] == "mfma" else PEAK_HBM_GBS,
+                     "unit": dom["unit"], "frac": dom["frac"], "traffic": traffic,
+                     "mean_launch_us": dom["mean_launch_us"], "launches_per_step": dom["launches"],
+                     "work_per_launch": dom["flops_per_launch"] if dom["bound"] == "mfma"
+                     else dom["bytes_per_launch"]},
+        "kernels": [{k: r[k] for k in ("kernel", "launches", "ms_per_step", "share", "achieved", "unit", "frac")}
+                    for r in rows],
+        "parity": parity,
+        "cpu_baseline": cpu,
+    }
+    sess.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
