@@ -19,7 +19,11 @@
 // P·V product without leaving registers.
 //
 // Workgroup = 4 wavefronts × 32 query rows = 128 rows of one (batch·head);
-// K/V tiles of 64 keys are staged in LDS (zero-filled past S and past hd).
+// K/V tiles of 32 keys are staged in LDS (zero-filled past S and past hd);
+// the next tile is fetched into registers while the current one is consumed
+// from LDS, so global-load latency hides behind the MFMAs.  Exponentials use
+// the hardware v_exp_f32 (exp2; a denormal result flushes to zero, which
+// cannot change a softmax row that always contains a term equal to 1).
 // Causal: tiles entirely above a wavefront's rows are skipped; workgroups are
 // issued heaviest-first (last query block first) to balance the triangle.
 #include "lbr_device.h"
@@ -31,7 +35,7 @@ namespace {
 
 constexpr int AT_NT = 256;       // 4 waves
 constexpr int AT_QB = 128;       // query rows per workgroup
-constexpr int AT_KB = 64;        // keys per LDS tile
+constexpr int AT_KB = 32;        // keys per LDS tile (one 32-row MFMA block)
 constexpr float LOG2E = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -44,13 +48,47 @@ struct AttnArgs {
     float scale_log2;            // (1/√hd)·log2(e)
 };
 
+// One K/V tile (AT_KB keys × DP) staged through registers: thread t holds the
+// float4 granules idx = t + i·AT_NT of each tile in row-major order.  Keys
+// past S and columns past D read as zero.
+template <int DP>
+struct AttnStage {
+    static constexpr int PER = AT_KB * DP / 4 / AT_NT;
+    float4 k[PER];
+    float4 v[PER];
+};
+
+template <int DP>
+__device__ __forceinline__ void attn_load_tile(const float* __restrict__ Kb, const float* __restrict__ Vb, int k0,
+                                               int S, int D, AttnStage<DP>& st) {
+#pragma unroll
+    for (int i = 0; i < AttnStage<DP>::PER; ++i) {
+        const int idx = threadIdx.x + i * AT_NT;
+        const int r = idx / (DP / 4), d = (idx % (DP / 4)) * 4;
+        const bool ok = k0 + r < S && d < D;
+        const long long off = (long long)(k0 + r) * D + d;
+        st.k[i] = ok ? *reinterpret_cast<const float4*>(Kb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+        st.v[i] = ok ? *reinterpret_cast<const float4*>(Vb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+template <int DP>
+__device__ __forceinline__ void attn_store_tile(float (*Ks)[DP + 4], float (*Vs)[DP + 4], const AttnStage<DP>& st) {
+#pragma unroll
+    for (int i = 0; i < AttnStage<DP>::PER; ++i) {
+        const int idx = threadIdx.x + i * AT_NT;
+        const int r = idx / (DP / 4), d = (idx % (DP / 4)) * 4;
+        *reinterpret_cast<float4*>(&Ks[r][d]) = st.k[i];
+        *reinterpret_cast<float4*>(&Vs[r][d]) = st.v[i];
+    }
+}
+
 template <int DP, bool CAUSAL, bool HAS_MASK>
-__global__ __launch_bounds__(AT_NT, 2) void attn_fwd_mfma(AttnArgs g) {
-    constexpr int LDD = DP + 4;
+__global__ __launch_bounds__(AT_NT, DP >= 256 ? 1 : 2) void attn_fwd_mfma(AttnArgs g) {
     constexpr int NCH = DP / 8;      // 8-wide d chunks
     constexpr int NDB = DP / 32;     // 32-wide d blocks of Oᵀ
-    __shared__ float Ks[AT_KB][LDD];
-    __shared__ float Vs[AT_KB][LDD];
+    __shared__ float Ks[AT_KB][DP + 4];
+    __shared__ float Vs[AT_KB][DP + 4];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lq = lane & 31, lh = lane >> 5;
@@ -64,7 +102,7 @@ __global__ __launch_bounds__(AT_NT, 2) void attn_fwd_mfma(AttnArgs g) {
     const int q_wave0 = qblk * AT_QB + wave * 32;
     const int q = q_wave0 + lq;            // this lane's query row
 
-    // Q fragment, pre-scaled: lane holds Q[q][8c + 4h + 0..3] for every chunk c
+    // Q fragment, pre-scaled by log2(e)/√hd: lane holds Q[q][8c + 4h + 0..3]
     floatx4 qf[NCH];
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
@@ -87,91 +125,77 @@ __global__ __launch_bounds__(AT_NT, 2) void attn_fwd_mfma(AttnArgs g) {
         for (int r = 0; r < 16; ++r) oacc[b][r] = 0.f;
     float m_run = -FLT_MAX, l_run = 0.f;
 
-    const int n_tiles_all = (S + AT_KB - 1) / AT_KB;
-    int n_tiles = n_tiles_all;
-    if (CAUSAL) {
-        const int last_q = min(S - 1, qblk * AT_QB + AT_QB - 1);
-        n_tiles = min(n_tiles_all, last_q / AT_KB + 1);
-    }
+    int n_tiles = (S + AT_KB - 1) / AT_KB;
+    if (CAUSAL) n_tiles = min(n_tiles, min(S - 1, qblk * AT_QB + AT_QB - 1) / AT_KB + 1);
+
+    AttnStage<DP> st;
+    attn_load_tile<DP>(Kb, Vb, 0, S, D, st);
+    attn_store_tile<DP>(Ks, Vs, st);
+    __syncthreads();
 
     for (int kt = 0; kt < n_tiles; ++kt) {
         const int k0 = kt * AT_KB;
-        __syncthreads();
-        // stage K and V tiles: 64 rows × DP (float4 granules), zero past S / D
-        for (int idx = tid; idx < AT_KB * (DP / 4); idx += AT_NT) {
-            const int r = idx / (DP / 4), d = (idx % (DP / 4)) * 4;
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-            if (k0 + r < S && d < D) {
-                kv = *reinterpret_cast<const float4*>(Kb + (long long)(k0 + r) * D + d);
-                vv = *reinterpret_cast<const float4*>(Vb + (long long)(k0 + r) * D + d);
-            }
-            *reinterpret_cast<float4*>(&Ks[r][d]) = kv;
-            *reinterpret_cast<float4*>(&Vs[r][d]) = vv;
-        }
-        __syncthreads();
+        // next tile's global loads are in flight while this one is consumed from LDS
+        if (kt + 1 < n_tiles) attn_load_tile<DP>(Kb, Vb, k0 + AT_KB, S, D, st);
 
         // Causal: a tile whose first key is past this wave's last row contributes nothing.
-        if (CAUSAL && k0 > q_wave0 + 31) continue;
-
-        // Sᵀ[kv][q] for kv blocks 0..1 of the tile (scaled by log2 e / √hd)
-        floatx16 sacc[2];
+        if (!CAUSAL || k0 <= q_wave0 + 31) {
+            // Sᵀ[kv][q] for the tile's 32 keys (already scaled by log2 e / √hd)
+            floatx16 sacc;
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[b][r] = 0.f;
+            for (int r = 0; r < 16; ++r) sacc[r] = 0.f;
 #pragma unroll
             for (int c = 0; c < NCH; ++c) {
-                const floatx4 kf = *reinterpret_cast<const floatx4*>(&Ks[b * 32 + lq][c * 8 + lh * 4]);
+                const floatx4 kf = *reinterpret_cast<const floatx4*>(&Ks[lq][c * 8 + lh * 4]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    sacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i], qf[c][i], sacc[b], 0, 0, 0);
+                    sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[i], qf[c][i], sacc, 0, 0, 0);
             }
-        }
 
-        // mask / causal / tail, then the tile's row max
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
+            // mask / causal / tail, then the tile's row max
+            float tmax = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int kv = k0 + b * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                float sv = sacc[b][r];
+                const int kv = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                float sv = sacc[r];
                 if (HAS_MASK && kv < S && q < S) sv += g.mask[(bh * S + q) * (long long)S + kv] * LOG2E;
                 if (kv >= S || (CAUSAL && kv > q)) sv = -INFINITY;
-                sacc[b][r] = sv;
+                sacc[r] = sv;
                 tmax = fmaxf(tmax, sv);
             }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float m_new = fmaxf(m_run, tmax);
-        const float corr = exp2f(m_run - m_new);
-        float psum = 0.f;
-#pragma unroll
-        for (int b = 0; b < 2; ++b)
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+            const float m_new = fmaxf(m_run, tmax);
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+            float psum = 0.f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = exp2f(sacc[b][r] - m_new);
-                sacc[b][r] = p;
+                const float p = __builtin_amdgcn_exp2f(sacc[r] - m_new);
+                sacc[r] = p;
                 psum += p;
             }
-        psum += __shfl_xor(psum, 32, 64);
-        l_run = l_run * corr + psum;
-        m_run = m_new;
+            psum += __shfl_xor(psum, 32, 64);
+            l_run = l_run * corr + psum;
+            m_run = m_new;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+            for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[db][r] *= corr;
+                for (int r = 0; r < 16; ++r) oacc[db][r] *= corr;
 
-        // Oᵀ[d][q] += Σ_kv V[kv][d] · P[q][kv]
+            // Oᵀ[d][q] += Σ_kv V[kv][d] · P[q][kv]
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+            for (int r = 0; r < 16; ++r) {
+                const int kvl = 8 * (r >> 2) + 4 * lh + (r & 3);
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int kvl = b * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                    const float vv = Vs[kvl][db * 32 + lq];
-                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, sacc[b][r], oacc[db], 0, 0, 0);
-                }
+                for (int db = 0; db < NDB; ++db)
+                    oacc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[kvl][db * 32 + lq], sacc[r], oacc[db], 0,
+                                                                   0, 0);
+            }
+        }
+        __syncthreads();
+        if (kt + 1 < n_tiles) {
+            attn_store_tile<DP>(Ks, Vs, st);
+            __syncthreads();
+        }
     }
 
     // O[q][d] = Oᵀ[d][q] / l ; lane holds d = 32·db + 8·j + 4·h + (0..3)
