@@ -51,6 +51,21 @@ void lbr_set_error(const char* fmt, ...) {
 static std::mutex g_mu;
 static int g_device = -1;
 static hipStream_t g_stream = nullptr;
+static int g_cus = 0;
+
+int lbr_device_cus() { return g_cus; }
+
+// One device workspace for a step list: sized to the largest step's need and
+// shared by all of them (they run in order on one stream).
+static int assign_workspace(std::vector<Step>& steps, void** out) {
+    size_t need = 0;
+    for (const Step& s : steps) need = s.ws_bytes > need ? s.ws_bytes : need;
+    *out = nullptr;
+    if (!need) return LBR_OK;
+    HIP_TRY(hipMalloc(out, need));
+    for (Step& s : steps) s.ws = *out;
+    return LBR_OK;
+}
 
 static int ensure_init() {
     if (g_stream) return LBR_OK;
@@ -130,6 +145,7 @@ struct lbr_plan {
     std::vector<Step> steps;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    void* ws = nullptr;          // shared step workspace (split-K partial sums)
 };
 
 static void run_steps(const std::vector<Step>& steps, hipStream_t st) {
@@ -165,6 +181,7 @@ int lbr_init(int device) {
     }
     HIP_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     g_device = device;
+    g_cus = prop.multiProcessorCount;
     return LBR_OK;
 }
 
@@ -236,9 +253,17 @@ int lbr_execute(const OpNode* nodes, int n_nodes) {
         rc = decode_node(&nodes[i], i, &steps[i]);
         if (rc) return rc;
     }
+    void* ws = nullptr;
+    rc = assign_workspace(steps, &ws);
+    if (rc) return rc;
     run_steps(steps, g_stream);
-    HIP_TRY(hipGetLastError());
-    HIP_TRY(hipStreamSynchronize(g_stream));
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    if (ws) (void)hipFree(ws);
+    if (e != hipSuccess) {
+        lbr_set_error("lbr_execute: %s", hipGetErrorString(e));
+        return LBR_ERR_HIP;
+    }
     return LBR_OK;
 }
 
@@ -259,6 +284,11 @@ int lbr_plan_create(const OpNode* nodes, int n_nodes, int use_graph, lbr_plan** 
             return rc;
         }
     }
+    rc = assign_workspace(p->steps, &p->ws);
+    if (rc) {
+        delete p;
+        return rc;
+    }
     if (use_graph && n_nodes > 0) {
         hipError_t e = hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal);
         if (e == hipSuccess) {
@@ -268,7 +298,8 @@ int lbr_plan_create(const OpNode* nodes, int n_nodes, int use_graph, lbr_plan** 
         if (e == hipSuccess) e = hipGraphInstantiate(&p->exec, p->graph, nullptr, nullptr, 0);
         if (e != hipSuccess) {
             lbr_set_error("lbr_plan_create: graph capture failed: %s", hipGetErrorString(e));
-            if (p->graph) hipGraphDestroy(p->graph);
+            if (p->graph) (void)hipGraphDestroy(p->graph);
+            if (p->ws) (void)hipFree(p->ws);
             delete p;
             return LBR_ERR_HIP;
         }
@@ -279,8 +310,9 @@ int lbr_plan_create(const OpNode* nodes, int n_nodes, int use_graph, lbr_plan** 
 
 int lbr_plan_destroy(lbr_plan* p) {
     if (!p) return LBR_OK;
-    if (p->exec) hipGraphExecDestroy(p->exec);
-    if (p->graph) hipGraphDestroy(p->graph);
+    if (p->exec) (void)hipGraphExecDestroy(p->exec);
+    if (p->graph) (void)hipGraphDestroy(p->graph);
+    if (p->ws) (void)hipFree(p->ws);
     delete p;
     return LBR_OK;
 }

@@ -40,6 +40,8 @@ struct GemmArgs {
     long long sA, sB, sC;     // batch strides (elements)
     float alpha;
     int tiles_m, tiles_n;
+    float* W;                 // split-K partial sums [ksplit][batches][M][N] (ksplit > 1)
+    int ksplit, kchunk;       // number of K ranges, K per range (multiple of BK)
 };
 
 __device__ __forceinline__ void tile_coords(const GemmArgs& g, int& tm, int& tn) {
@@ -188,14 +190,19 @@ __global__ __launch_bounds__(NT, 2) void gemm_mfma_f32(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+    // K range of this workgroup: all of K, or split ks of ksplit (kchunk is a
+    // multiple of BK, so only the last range can end inside a K step).
+    const int ks = blockIdx.y;
+    const int kbeg = ks * g.kchunk;
+    const int kend = min(g.K, kbeg + g.kchunk);
     float4 ra[4], rb[4];
-    const int nk = (g.K + BK - 1) / BK;
-    load_tiles<TRANS_B, VEC>(g, A, B, m0, n0, 0, ra, rb);
+    const int nk = (kend - kbeg + BK - 1) / BK;
+    load_tiles<TRANS_B, VEC>(g, A, B, m0, n0, kbeg, ra, rb);
     store_tiles<TRANS_B, VEC>(As, Bs, ra, rb);
     __syncthreads();
 
     for (int kt = 0; kt < nk; ++kt) {
-        if (kt + 1 < nk) load_tiles<TRANS_B, VEC>(g, A, B, m0, n0, (kt + 1) * BK, ra, rb);
+        if (kt + 1 < nk) load_tiles<TRANS_B, VEC>(g, A, B, m0, n0, kbeg + (kt + 1) * BK, ra, rb);
 #pragma unroll
         for (int c = 0; c < BK / 8; ++c) {
             const int kc = c * 8 + lhalf * 4;
@@ -223,6 +230,23 @@ __global__ __launch_bounds__(NT, 2) void gemm_mfma_f32(GemmArgs g) {
 
     // Epilogue.  Accumulator layout of the 32x32 block: lane l, register r
     // holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+    if (g.ksplit > 1) {
+        // raw partial sums; splitk_reduce applies alpha / bias in a fixed order
+        float* __restrict__ Wp = g.W + ((long long)ks * gridDim.z + bz) * (long long)g.M * g.N;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = n0 + wn * 64 + j * 32 + lrow;
+                if (n >= g.N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+                    if (m < g.M) Wp[(long long)m * g.N + n] = acc[i][j][r];
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -302,15 +326,96 @@ GemmArgs make_args(const Step& s) {
     g.alpha = s.f[0];
     g.tiles_m = (g.M + BM - 1) / BM;
     g.tiles_n = (g.N + BN - 1) / BN;
+    g.ksplit = s.i[10] > 1 ? (int)s.i[10] : 1;
+    g.kchunk = g.ksplit > 1 ? (int)s.i[11] : g.K;
+    g.W = (float*)s.ws;
     return g;
+}
+
+// C[i] = alpha·Σ_ks W[ks][i] (MATMUL) or Σ_ks W[ks][i] + bias[i % N]
+// (MATMUL_ADD), summing the K ranges in increasing order.
+template <bool HAS_BIAS, bool VEC>
+__global__ void splitk_reduce(const float* __restrict__ W, float* __restrict__ C, const float* __restrict__ bias,
+                              long long total, int N, int ksplit, float alpha) {
+    if (VEC) {
+        const long long t4 = total / 4;
+        for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < t4;
+             i += (long long)gridDim.x * blockDim.x) {
+            float4 s = reinterpret_cast<const float4*>(W)[i];
+            for (int k = 1; k < ksplit; ++k) {
+                const float4 w = reinterpret_cast<const float4*>(W + (long long)k * total)[i];
+                s.x += w.x; s.y += w.y; s.z += w.z; s.w += w.w;
+            }
+            if (HAS_BIAS) {
+                const float4 b = reinterpret_cast<const float4*>(bias)[(i * 4 % N) / 4];
+                s.x += b.x; s.y += b.y; s.z += b.z; s.w += b.w;
+            } else {
+                s.x *= alpha; s.y *= alpha; s.z *= alpha; s.w *= alpha;
+            }
+            reinterpret_cast<float4*>(C)[i] = s;
+        }
+    } else {
+        for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+             i += (long long)gridDim.x * blockDim.x) {
+            float s = W[i];
+            for (int k = 1; k < ksplit; ++k) s += W[(long long)k * total + i];
+            C[i] = HAS_BIAS ? s + bias[i % N] : alpha * s;
+        }
+    }
 }
 
 template <bool TRANS_B, bool VEC, bool HAS_BIAS>
 void launch_gemm_t(const Step& s, hipStream_t st) {
     GemmArgs g = make_args(s);
     if (g.M <= 0 || g.N <= 0) return;
-    dim3 grid(g.tiles_m * g.tiles_n, 1, (unsigned)s.i[3]);
+    dim3 grid(g.tiles_m * g.tiles_n, g.ksplit, (unsigned)s.i[3]);
     hipLaunchKernelGGL((gemm_mfma_f32<TRANS_B, VEC, HAS_BIAS>), grid, dim3(NT), 0, st, g);
+    if (g.ksplit > 1) {
+        const long long total = (long long)g.M * g.N * s.i[3];
+        const bool v4 = s.i[12] != 0;
+        const unsigned blocks = lbr_grid(v4 ? total / 4 : total, 256, 4096);
+        if (v4)
+            hipLaunchKernelGGL((splitk_reduce<HAS_BIAS, true>), dim3(blocks), dim3(256), 0, st, g.W, g.C, g.bias,
+                               total, g.N, g.ksplit, g.alpha);
+        else
+            hipLaunchKernelGGL((splitk_reduce<HAS_BIAS, false>), dim3(blocks), dim3(256), 0, st, g.W, g.C, g.bias,
+                               total, g.N, g.ksplit, g.alpha);
+    }
+}
+
+// Number of K ranges for a GEMM of `tiles` 128×128 output tiles: the tile
+// grid alone leaves CUs idle or unevenly loaded when it is small (e.g.
+// M=1024, N=2560 → 160 tiles on 256 CUs).  Model: a CU's time ∝ the work of
+// the workgroups it receives ÷ its efficiency with that many resident
+// workgroups (0.75 for one, 0.95 for two, 1 for three or more), plus the
+// extra HBM traffic of writing and re-reading the partial sums.  Split only
+// when that predicts at least a 5% gain.
+int choose_ksplit(long long tiles, int K, long long MN, int cus, int* kchunk) {
+    *kchunk = K;
+    if (cus <= 0 || K < 1024) return 1;
+    auto eff = [](long long n) { return n <= 1 ? 0.75 : n == 2 ? 0.95 : 1.0; };
+    const double gemm_s = 2.0 * MN * (double)K / 130e12;           // per batch, at ~83% of peak
+    auto cost = [&](int s, int chunk) {
+        const long long n = (tiles * s + cus - 1) / cus;             // workgroups on the busiest CU
+        const double t = (double)n * chunk / K / eff(n);
+        const double extra = s > 1 ? (2.0 * s + 1.0) * MN * 4.0 / 8e12 / gemm_s : 0.0;
+        return t * (1.0 + extra);
+    };
+    double best = cost(1, K);
+    int best_s = 1, best_chunk = K;
+    for (int s = 2; s <= 16; ++s) {
+        const int chunk = ((K + s - 1) / s + BK - 1) / BK * BK;
+        if (chunk < 256) break;
+        const int s_eff = (K + chunk - 1) / chunk;
+        const double c = cost(s_eff, chunk);
+        if (c < best * 0.95 && c < best) {
+            best = c;
+            best_s = s_eff;
+            best_chunk = chunk;
+        }
+    }
+    *kchunk = best_chunk;
+    return best_s;
 }
 
 template <bool VEC, bool HAS_BIAS>
@@ -417,6 +522,15 @@ int decode_matmul(const OpNode* n, Step* s) {
     }
     const bool vec = lbr_aligned(n->inputs[0], 16) && lbr_aligned(n->inputs[1], 16) && K % 4 == 0 &&
                      (trans_b || N % 4 == 0);
+    {
+        const long long tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN) * batches;
+        int kchunk = K;
+        const int ks = choose_ksplit(tiles, K, M * (long long)N, lbr_device_cus(), &kchunk);
+        s->i[10] = ks;
+        s->i[11] = kchunk;
+        s->i[12] = (N % 4 == 0) && lbr_aligned(n->output, 16) && (!has_bias || lbr_aligned(n->inputs[2], 16));
+        s->ws_bytes = ks > 1 ? (size_t)ks * batches * M * N * sizeof(float) : 0;
+    }
     if (trans_b) {
         if (vec) s->run = has_bias ? launch_gemm_t<true, true, true> : launch_gemm_t<true, true, false>;
         else s->run = has_bias ? launch_gemm_t<true, false, true> : launch_gemm_t<true, false, false>;

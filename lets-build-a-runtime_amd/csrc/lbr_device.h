@@ -77,7 +77,12 @@ struct Step {
     int n_in;
     long long i[40];          // integer parameters (meaning per launcher)
     float f[4];               // float parameters
+    size_t ws_bytes;          // device workspace this step needs (0 = none)
+    void* ws;                 // workspace assigned by the plan (shared by all steps)
 };
+
+// Number of compute units of the initialised device (0 before lbr_init).
+int lbr_device_cus();
 
 static inline bool lbr_aligned(const void* p, size_t a) {
     return (reinterpret_cast<uintptr_t>(p) % a) == 0;

@@ -41,6 +41,9 @@ GEMM_CASES = [
     (1, 512, 256, True, 1, True),     # M == 1 → GEMV
     (1, 300, 128, False, 2, False),   # batched GEMV, B [K, N]
     (5, 7, 1, True, 1, True),         # K = 1
+    (256, 384, 4096, True, 1, True),  # few tiles, long K → split-K + reduction
+    (200, 300, 2050, True, 1, True),  # split-K, ragged K on the scalar path
+    (64, 128, 3000, False, 2, False), # split-K, batched, B [K, N]
 ]
 
 
