@@ -171,6 +171,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-parity", action="store_true", help="skip the GPU-vs-oracle output check")
     ap.add_argument("--eager", action="store_true", help="launch node by node instead of replaying a hipGraph")
+    ap.add_argument("--nodes", action="store_true", help="log every node's device time and roofline fraction")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run the library's copy kernel over MIB MiB, 5 times (reference for HBM counters)")
     args = ap.parse_args()
@@ -217,6 +218,14 @@ def main() -> int:
     node_ms = ex.profile_nodes(max(1, min(args.steps, 20)))
     rows = kernel_table(names, ex.dispatch_order, sess.resolved_graph, node_ms)
     dom = rows[0]
+    if args.nodes:
+        rg = sess.resolved_graph
+        for name, node, t in zip(names, ex.dispatch_order, node_ms):
+            f, b = node_work(node, rg)
+            rate = f"{f / t / 1e9:8.1f} TF/s {100 * f / t / 1e9 / PEAK_FP32_MFMA_TFLOPS:5.1f}%" if f else \
+                f"{b / t / 1e6:8.1f} GB/s {100 * b / t / 1e6 / PEAK_HBM_GBS:5.1f}%"
+            log(f"[node] {node.id:>4} {node.op.name:<11} {name:<20} {str(rg.tensors[node.output].shape):<24} "
+                f"{t * 1e3:9.1f} us {rate}")
     for r in rows:
         log(f"[bench]   {r['kernel']:<22} x{r['launches']:<3} {r['ms_per_step']:8.3f} ms "
             f"({100 * r['share']:5.1f}%)  {r['achieved']:9.2f} {r['unit']:<8} {100 * r['frac']:5.1f}% of peak")

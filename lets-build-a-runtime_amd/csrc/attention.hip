@@ -46,6 +46,7 @@ struct AttnArgs {
     const float* mask;
     int S, D, group_size, n_qblocks;
     float scale_log2;            // (1/√hd)·log2(e)
+    int fold;                    // causal: workgroup j also runs query block j (16x16 kernel)
 };
 
 // One K/V tile (AT_KB keys × DP) staged through registers: thread t holds the
@@ -219,6 +220,218 @@ __global__ __launch_bounds__(AT_NT, DP >= 256 ? 1 : 2) void attn_fwd_mfma(AttnAr
     }
 }
 
+// ---------------------------------------------------------------------------
+// Head dims ≤ 128: v_mfma_f32_16x16x4_f32 with 16 query rows per wavefront.
+//
+// Same transposed formulation (Sᵀ = K·Qᵀ, Oᵀ = Vᵀ·Pᵀ, lane owns query row
+// l%16), but the 16-row wavefront tile halves the per-wave register state
+// (Q: hd/4, O: hd/4, scores: 8 VGPRs), so an 8-wavefront workgroup of 128
+// query rows runs at 4 wavefronts per SIMD and the matrix core has twice as
+// many independent instruction streams to hide LDS and softmax latency.
+// Operand layout of the 16x16x4 MFMA: A[i][k] from lane 16k+i, B[k][j] from
+// lane 16k+j, D[4g+r][j] in register r of lane 16g+j.  K-chunks of 16 d:
+// lane group g reads K/Q[.][16c+4g .. +3] as one float4; MFMA i of the chunk
+// reduces d = 16c+4g+i over the four groups.
+// In Oᵀ = Vᵀ·Pᵀ the row index i of d-block db stands for head dim
+//   d(db, i) = W·i + db%W + 16W·(db/W),   W = min(4, hd/16),
+// so one lane's V operands for the W blocks db = W·h .. W·h+W-1 are the W
+// consecutive floats V[key][16W·h + W·i ..] — one LDS vector read feeds W
+// MFMAs — and one lane's outputs O[q][..] are runs of 4W consecutive floats.
+// LDS rows are padded to hd+4 floats: the K reads (16 rows × 4 groups of
+// 16 B) and the V reads (4 rows × 16 lanes × W consecutive floats) hit
+// distinct banks.
+constexpr int A16_NT = 512;      // 8 waves
+constexpr int A16_QB = 128;      // query rows per workgroup (16 per wave)
+constexpr int A16_KB = 32;       // keys per tile
+
+// One 128-row query block of one head: streams the key tiles it needs
+// through Ks/Vs and writes its output rows.
+template <int DP, bool CAUSAL, bool HAS_MASK>
+__device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int qblk, float (*Ks)[DP + 4],
+                                              float (*Vs)[DP + 4]) {
+    constexpr int NCH = DP / 16;     // 16-wide d chunks (S reduction) and d blocks (O)
+    constexpr int W = NCH < 4 ? NCH : 4;
+    typedef float VW __attribute__((ext_vector_type(W)));
+    constexpr int TILE4 = A16_KB * DP / 4;                       // float4 granules per K (or V) tile
+    constexpr int PER = (TILE4 + A16_NT - 1) / A16_NT;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lr = lane & 15, lg = lane >> 4;
+    const long long bh = blockIdx.y;
+    const long long kvh = bh / g.group_size;
+    const int S = g.S, D = g.D;
+    const float* __restrict__ Qb = g.Q + bh * (long long)S * D;
+    const float* __restrict__ Kb = g.K + kvh * (long long)S * D;
+    const float* __restrict__ Vb = g.V + kvh * (long long)S * D;
+    const int q_wave0 = qblk * A16_QB + wave * 16;
+    const int q = q_wave0 + lr;
+
+    floatx4 qf[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int d = 16 * c + 4 * lg;
+        floatx4 v = {0.f, 0.f, 0.f, 0.f};
+        if (q < S && d < D) {
+            const float4 t = *reinterpret_cast<const float4*>(Qb + (long long)q * D + d);
+            v[0] = t.x * g.scale_log2;
+            v[1] = t.y * g.scale_log2;
+            v[2] = t.z * g.scale_log2;
+            v[3] = t.w * g.scale_log2;
+        }
+        qf[c] = v;
+    }
+
+    floatx4 oacc[NCH];
+#pragma unroll
+    for (int b = 0; b < NCH; ++b) oacc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -FLT_MAX, l_run = 0.f;
+
+    int n_tiles = (S + A16_KB - 1) / A16_KB;
+    if (CAUSAL) n_tiles = min(n_tiles, min(S - 1, qblk * A16_QB + A16_QB - 1) / A16_KB + 1);
+
+    float4 kr[PER], vr[PER];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = tid + i * A16_NT;
+            const int r = idx / (DP / 4), d = (idx % (DP / 4)) * 4;
+            const bool ok = idx < TILE4 && k0 + r < S && d < D;
+            const long long off = (long long)(k0 + r) * D + d;
+            kr[i] = ok ? *reinterpret_cast<const float4*>(Kb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+            vr[i] = ok ? *reinterpret_cast<const float4*>(Vb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int idx = tid + i * A16_NT;
+            if (idx < TILE4) {
+                const int r = idx / (DP / 4), d = (idx % (DP / 4)) * 4;
+                *reinterpret_cast<float4*>(&Ks[r][d]) = kr[i];
+                *reinterpret_cast<float4*>(&Vs[r][d]) = vr[i];
+            }
+        }
+    };
+
+    load(0);
+    store();
+    __syncthreads();
+
+    for (int kt = 0; kt < n_tiles; ++kt) {
+        const int k0 = kt * A16_KB;
+        if (kt + 1 < n_tiles) load(k0 + A16_KB);
+
+        if (!CAUSAL || k0 <= q_wave0 + 15) {
+            // Sᵀ for two 16-key blocks; register r of block b = key k0 + 16b + 4g + r
+            floatx4 sacc[2];
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                sacc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) {
+                    const floatx4 kf = *reinterpret_cast<const floatx4*>(&Ks[16 * b + lr][16 * c + 4 * lg]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        sacc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[i], qf[c][i], sacc[b], 0, 0, 0);
+                }
+            }
+
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int kv = k0 + 16 * b + 4 * lg + r;
+                    float sv = sacc[b][r];
+                    if (HAS_MASK && kv < S && q < S) sv += g.mask[(bh * S + q) * (long long)S + kv] * LOG2E;
+                    if (kv >= S || (CAUSAL && kv > q)) sv = -INFINITY;
+                    sacc[b][r] = sv;
+                    tmax = fmaxf(tmax, sv);
+                }
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+            const float m_new = fmaxf(m_run, tmax);
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+            float psum = 0.f;
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float p = __builtin_amdgcn_exp2f(sacc[b][r] - m_new);
+                    sacc[b][r] = p;
+                    psum += p;
+                }
+            psum += __shfl_xor(psum, 16, 64);
+            psum += __shfl_xor(psum, 32, 64);
+            l_run = l_run * corr + psum;
+            m_run = m_new;
+#pragma unroll
+            for (int db = 0; db < NCH; ++db) oacc[db] *= corr;
+
+            // Oᵀ[d][q] += Σ_kv V[kv][d]·P[q][kv]; MFMA (b, r) takes key 16b + 4g + r from group g
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int kvl = 16 * b + 4 * lg + r;
+#pragma unroll
+                    for (int h = 0; h < NCH / W; ++h) {
+                        const VW vv = *reinterpret_cast<const VW*>(&Vs[kvl][16 * W * h + W * lr]);
+#pragma unroll
+                        for (int w = 0; w < W; ++w)
+                            oacc[W * h + w] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[w], sacc[b][r], oacc[W * h + w],
+                                                                                  0, 0, 0);
+                    }
+                }
+        }
+        __syncthreads();
+        if (kt + 1 < n_tiles) {
+            store();
+            __syncthreads();
+        }
+    }
+
+    // O[q][d] = Oᵀ[d][q] / l; register r of block W·h + w holds row i = 4g + r,
+    // i.e. d = 16W·h + W·(4g + r) + w: W consecutive floats per (h, r)
+    if (q < S) {
+        const float inv_l = 1.0f / l_run;
+        float* __restrict__ Ob = g.O + bh * (long long)S * D + (long long)q * D;
+#pragma unroll
+        for (int h = 0; h < NCH / W; ++h)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int d = 16 * W * h + W * (4 * lg + r);
+                if (d < D) {
+                    VW o;
+#pragma unroll
+                    for (int w = 0; w < W; ++w) o[w] = oacc[W * h + w][r] * inv_l;
+                    *reinterpret_cast<VW*>(Ob + d) = o;
+                }
+            }
+    }
+}
+
+// Causal work per query block grows linearly with its index, and the
+// hardware places consecutive workgroups round-robin over the CUs, so a
+// one-block-per-workgroup grid leaves some CUs with only the longest blocks.
+// With g.fold set, workgroup j runs block n-1-j and then block j: every
+// workgroup carries the same number of key tiles.
+template <int DP, bool CAUSAL, bool HAS_MASK>
+__global__ __launch_bounds__(A16_NT, 4) void attn_fwd_mfma16(AttnArgs g) {
+    __shared__ float Ks[A16_KB][DP + 4];
+    __shared__ float Vs[A16_KB][DP + 4];
+    const int j = blockIdx.x, last = g.n_qblocks - 1 - j;
+    if (!CAUSAL) {
+        attn16_qblock<DP, CAUSAL, HAS_MASK>(g, j, Ks, Vs);
+        return;
+    }
+    attn16_qblock<DP, CAUSAL, HAS_MASK>(g, last, Ks, Vs);
+    if (g.fold && j < last) {
+        __syncthreads();
+        attn16_qblock<DP, CAUSAL, HAS_MASK>(g, j, Ks, Vs);
+    }
+}
+
 // Fallback for head dims the MFMA kernel does not take (hd % 8 != 0 or
 // hd > 256): one workgroup per (bh, query row), scores held in LDS.
 __global__ __launch_bounds__(256) void attn_fwd_rows(AttnArgs g, int causal) {
@@ -272,6 +485,7 @@ AttnArgs make_args(const Step& s) {
     g.group_size = (int)s.i[4];
     g.n_qblocks = (g.S + AT_QB - 1) / AT_QB;
     g.scale_log2 = s.f[0] * LOG2E;
+    g.fold = 0;
     return g;
 }
 
@@ -290,10 +504,26 @@ void launch_attn_rows(const Step& s, hipStream_t st) {
                        (int)s.i[3]);
 }
 
+template <int DP, bool CAUSAL, bool HAS_MASK>
+void launch_attn16(const Step& s, hipStream_t st) {
+    AttnArgs g = make_args(s);
+    if (g.S <= 0 || s.i[0] <= 0) return;
+    g.n_qblocks = (g.S + A16_QB - 1) / A16_QB;
+    g.fold = CAUSAL && s.i[6] != 0;
+    const unsigned gx = g.fold ? (unsigned)(g.n_qblocks + 1) / 2 : (unsigned)g.n_qblocks;
+    hipLaunchKernelGGL((attn_fwd_mfma16<DP, CAUSAL, HAS_MASK>), dim3(gx, (unsigned)s.i[0]), dim3(A16_NT), 0, st, g);
+}
+
 template <int DP>
 step_fn pick(bool causal, bool mask) {
     if (causal) return mask ? launch_attn<DP, true, true> : launch_attn<DP, true, false>;
     return mask ? launch_attn<DP, false, true> : launch_attn<DP, false, false>;
+}
+
+template <int DP>
+step_fn pick16(bool causal, bool mask) {
+    if (causal) return mask ? launch_attn16<DP, true, true> : launch_attn16<DP, true, false>;
+    return mask ? launch_attn16<DP, false, true> : launch_attn16<DP, false, false>;
 }
 
 }  // namespace
@@ -337,6 +567,24 @@ int decode_attention(const OpNode* n, Step* s) {
     if (hd % 8 == 0 && hd <= 256 && aligned) {
         const int dp = hd <= 32 ? 32 : hd <= 64 ? 64 : hd <= 128 ? 128 : 256;
         s->i[5] = dp;
+        // LBR_ATTN_TILE=32 keeps the 32x32 kernel for every head dim (A/B timing).
+        const char* tile = getenv("LBR_ATTN_TILE");
+        if (dp <= 128 && !(tile && atoi(tile) == 32)) {
+            // Fold causal query blocks in pairs while that still leaves one
+            // 8-wavefront workgroup per CU (LBR_ATTN_FOLD=0/1 overrides).
+            const long long nq = (seq + A16_QB - 1) / A16_QB;
+            const int cus = lbr_device_cus() > 0 ? lbr_device_cus() : 256;
+            s->i[6] = causal && (nq + 1) / 2 * bh >= cus;
+            const char* fold = getenv("LBR_ATTN_FOLD");
+            if (fold) s->i[6] = causal && atoi(fold) != 0;
+            switch (dp) {
+                case 32: s->run = pick16<32>(causal, has_mask); break;
+                case 64: s->run = pick16<64>(causal, has_mask); break;
+                default: s->run = pick16<128>(causal, has_mask); break;
+            }
+            s->name = "attn_fwd_mfma16_f32";
+            return LBR_OK;
+        }
         switch (dp) {
             case 32: s->run = pick<32>(causal, has_mask); break;
             case 64: s->run = pick<64>(causal, has_mask); break;

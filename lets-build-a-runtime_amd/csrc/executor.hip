@@ -176,7 +176,7 @@ int lbr_init(int device) {
         return LBR_ERR_NO_DEVICE;
     }
     if (g_stream) {
-        hipStreamDestroy(g_stream);
+        (void)hipStreamDestroy(g_stream);
         g_stream = nullptr;
     }
     HIP_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));

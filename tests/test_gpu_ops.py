@@ -102,11 +102,12 @@ ATTN_CASES = [
     (1, 2, 1, 64, True, 1),
     (1, 2, 40, 24, True, 1),        # hd % 8 == 0, padded to 32
     (1, 2, 33, 12, False, 1),       # hd % 8 != 0 → row fallback kernel
+    (1, 2, 200, 256, True, 1),      # hd > 128 → 32x32 MFMA kernel
+    (1, 3, 70, 160, False, 1),      # hd > 128, padded to 256
 ]
 
 
-@pytest.mark.parametrize("B,H,S,hd,causal,group", ATTN_CASES)
-def test_attention(B, H, S, hd, causal, group):
+def _attention_case(B, H, S, hd, causal, group):
     r = rng(S * 3 + hd + H)
     q = randn(r, B, H, S, hd)
     k = randn(r, B, H // group, S, hd)
@@ -119,6 +120,27 @@ def test_attention(B, H, S, hd, causal, group):
     _check(g, {"q": q, "k": k, "v": v}, ref, 1e-4)
 
 
+@pytest.mark.parametrize("B,H,S,hd,causal,group", ATTN_CASES)
+def test_attention(B, H, S, hd, causal, group):
+    _attention_case(B, H, S, hd, causal, group)
+
+
+# Kernel-selection overrides read when the plan is built: LBR_ATTN_FOLD=1
+# forces the paired causal schedule (workgroup j runs query blocks n-1-j and
+# j; odd n leaves the middle block alone), LBR_ATTN_TILE=32 the 32x32 kernel.
+@pytest.mark.parametrize("env", [{"LBR_ATTN_FOLD": "1"}, {"LBR_ATTN_TILE": "32"}], ids=["fold", "tile32"])
+@pytest.mark.parametrize("B,H,S,hd,causal,group", [
+    (1, 4, 257, 128, True, 1),      # 3 query blocks: pair (2, 0) and the middle block 1 alone
+    (1, 8, 512, 64, True, 2),       # 4 query blocks: pairs (3, 0), (2, 1)
+    (2, 2, 1000, 32, True, 1),
+    (1, 2, 130, 128, False, 1),     # non-causal ignores the fold flag
+])
+def test_attention_schedules(monkeypatch, env, B, H, S, hd, causal, group):
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    _attention_case(B, H, S, hd, causal, group)
+
+
 @pytest.mark.parametrize("S", [16, 300])
 def test_attention_mask(S):
     r = rng(S)
@@ -129,9 +151,6 @@ def test_attention_mask(S):
         mask[..., i, i] = 0.0
     g = one_node_graph(OpType.ATTENTION, {"q": q, "k": k, "v": v, "mask": mask}, (B, H, S, hd), {})
     ref = cf_attention(q, k, v, mask=mask)
-    if S > 256:
-        # the reference takes its standard path whenever a mask is present; same function
-        pass
     _check(g, {"q": q, "k": k, "v": v, "mask": mask}, ref, 1e-4)
 
 
