@@ -88,20 +88,56 @@ def node_work(node, graph) -> tuple[float, float]:
     return 0.0, float(sum(nbytes(t) for t in node.inputs) + out_b)
 
 
-def kernel_table(names, order, graph, ms):
-    """Aggregate per-node device times by kernel name."""
+def step_units(names, order, graph, ms, runs):
+    """One entry per kernel step: fused runs (first, count, kind) become one unit.
+
+    A fused run's work: the flops of its GEMM/attention nodes; bytes = what it
+    reads from outside the run (for a SLICE of an outside tensor, only the
+    sliced part) plus the outputs that leave the run (read by a later node or
+    graph outputs)."""
+    start = {f: c for f, c, _ in runs}
+    units, i = [], 0
+    while i < len(order):
+        c = start.get(i, 1)
+        nodes = order[i:i + c]
+        if c == 1:
+            f, b = node_work(nodes[0], graph)
+        else:
+            inside = {n.output for n in nodes}
+            later = {t for n in order[i + c:] for t in n.inputs} | set(graph.outputs)
+            f, b = 0.0, 0.0
+            seen = set()
+            for n in nodes:
+                nf, _ = node_work(n, graph)
+                f += nf
+                for t in n.inputs:
+                    if t in inside or t in seen:
+                        continue
+                    seen.add(t)
+                    t_node = n if n.op.name == "SLICE" else None
+                    src = t_node.output if t_node is not None else t
+                    b += np.prod(graph.tensors[src].shape) * np.dtype(graph.tensors[src].dtype).itemsize
+            for t in inside:
+                if t in later:
+                    b += np.prod(graph.tensors[t].shape) * np.dtype(graph.tensors[t].dtype).itemsize
+        units.append({"name": names[i], "nodes": nodes, "ms": ms[i], "flops": f, "bytes": float(b)})
+        i += c
+    return units
+
+
+def kernel_table(units):
+    """Aggregate per-step device times by kernel name."""
     agg: dict[str, dict] = {}
-    for name, node, t in zip(names, order, ms):
-        f, b = node_work(node, graph)
-        a = agg.setdefault(name, {"kernel": name, "launches": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0})
+    for u in units:
+        a = agg.setdefault(u["name"], {"kernel": u["name"], "launches": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0})
         a["launches"] += 1
-        a["ms"] += t
-        a["flops"] += f
-        a["bytes"] += b
+        a["ms"] += u["ms"]
+        a["flops"] += u["flops"]
+        a["bytes"] += u["bytes"]
     rows = []
     total = sum(a["ms"] for a in agg.values()) or 1.0
     for a in agg.values():
-        sec = a["ms"] / 1e3
+        sec = max(a["ms"], 1e-9) / 1e3
         mfma = a["flops"] > 0
         achieved = (a["flops"] / sec / 1e12) if mfma else (a["bytes"] / sec / 1e9)
         peak = PEAK_FP32_MFMA_TFLOPS if mfma else PEAK_HBM_GBS
@@ -195,7 +231,8 @@ def main() -> int:
     sess.create(use_graph=not args.eager)
     ex = sess.executor
     log(f"[bench] {wl.title}: export+optimise+plan+compile {time.time() - t0:.1f}s, "
-        f"{len(ex.dispatch_order)} kernels/step, arena {sess.plan_stats.arena_bytes / 2**20:.1f} MiB")
+        f"{len(ex.dispatch_order)} nodes/step, {len(ex.fused_runs())} fused runs, "
+        f"arena {sess.plan_stats.arena_bytes / 2**20:.1f} MiB")
 
     ex.upload_inputs({graph.inputs[0]: x})
     ex.synchronize()
@@ -216,15 +253,19 @@ def main() -> int:
     # per-kernel device time (eager launches, hipEvent pairs on the library stream)
     names = ex.kernel_names()
     node_ms = ex.profile_nodes(max(1, min(args.steps, 20)))
-    rows = kernel_table(names, ex.dispatch_order, sess.resolved_graph, node_ms)
+    rg = sess.resolved_graph
+    runs = ex.fused_runs()
+    units = step_units(names, ex.dispatch_order, rg, node_ms, runs)
+    rows = kernel_table(units)
     dom = rows[0]
     if args.nodes:
-        rg = sess.resolved_graph
-        for name, node, t in zip(names, ex.dispatch_order, node_ms):
-            f, b = node_work(node, rg)
+        for u in units:
+            node, t, f, b = u["nodes"][0], u["ms"], u["flops"], u["bytes"]
             rate = f"{f / t / 1e9:8.1f} TF/s {100 * f / t / 1e9 / PEAK_FP32_MFMA_TFLOPS:5.1f}%" if f else \
                 f"{b / t / 1e6:8.1f} GB/s {100 * b / t / 1e6 / PEAK_HBM_GBS:5.1f}%"
-            log(f"[node] {node.id:>4} {node.op.name:<11} {name:<20} {str(rg.tensors[node.output].shape):<24} "
+            ops = "+".join(n.op.name for n in u["nodes"]) if len(u["nodes"]) <= 3 else \
+                f"{u['nodes'][0].op.name}+{len(u['nodes']) - 1} nodes"
+            log(f"[node] {node.id:>4} {ops:<24} {u['name']:<24} {str(rg.tensors[node.output].shape):<22} "
                 f"{t * 1e3:9.1f} us {rate}")
     for r in rows:
         log(f"[bench]   {r['kernel']:<22} x{r['launches']:<3} {r['ms_per_step']:8.3f} ms "
@@ -269,7 +310,8 @@ def main() -> int:
         "config": {"workload": args.config, "title": wl.title, "batch": int(x.shape[0]),
                    "seq_len": int(x.shape[1]), "d_model": int(x.shape[2]),
                    "graph": "hipGraph replay" if not args.eager else "eager launches",
-                   "kernels_per_step": len(ex.dispatch_order)},
+                   "nodes_per_step": len(ex.dispatch_order), "kernels_per_step": len(units),
+                   "fused_runs": len(runs)},
         "roofline": {"kernel": dom["kernel"], "bound": dom["bound"], "achieved": dom["achieved"],
                      "peak": PEAK_FP32_MFMA_TFLOPS if dom["bound"] == "mfma" else PEAK_HBM_GBS,
                      "unit": dom["unit"], "frac": dom["frac"], "traffic": traffic,

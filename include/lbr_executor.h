@@ -139,10 +139,52 @@ int lbr_plan_time(lbr_plan* plan, int iters, float* out_ms);
  * mean milliseconds of node i to out_ms[i] (n_out >= number of nodes). */
 int lbr_plan_profile(lbr_plan* plan, int iters, float* out_ms, int n_out);
 
-/* Number of kernel launches node `index` decodes into, and a short name of
- * its kernel (for reports). */
+/* Short name of the kernel that executes node `index` (for reports); nodes
+ * inside a fused run after its first report "fused". */
 int lbr_plan_node_kernel(const lbr_plan* plan, int index, char* name_out,
                          int name_cap);
+
+/* ---------------------------------------------------------------------
+ * Peephole fusion.  No counterpart in the reference (its executor runs one
+ * kernel per node, csrc/executor.c:458-467); the node array stays exactly
+ * as the host layer builds it.  At plan creation runs of consecutive nodes
+ * that one kernel can execute are replaced by that kernel when every value
+ * the run produces, other than its final outputs, is dead afterwards (not
+ * read by a later node before being overwritten, not inside a live-out
+ * range) and no final output overlaps memory the fused kernel reads.
+ * Live-out ranges are the byte ranges the caller reads after a launch (the
+ * graph outputs); final outputs hold what the unfused nodes would write.
+ * ------------------------------------------------------------------- */
+#define LBR_FUSE_NONE          0
+#define LBR_FUSE_GEMM_RESID    1  /* MATMUL[_ADD] → ADD(C, R): R added in the GEMM epilogue     */
+#define LBR_FUSE_GEMM_HEADS    2  /* MATMUL[_ADD] → k × (SLICE → [ADD bias] → TRANSPOSE(S,H)):
+                                     the epilogue writes each column range as [B, H, S, hd]     */
+#define LBR_FUSE_HEAD_PROLOGUE 3  /* SLICE → [ADD bias] → [RMSNORM] → TRANSPOSE(S,H) → [RoPE]
+                                     (7-node rotate-half window) as one kernel                  */
+
+typedef struct {
+    int first;   /* index of the run's first node */
+    int count;   /* nodes in the run              */
+    int kind;    /* LBR_FUSE_*                    */
+} lbr_window;
+
+/* The runs lbr_plan_create_fused would fuse, without touching a device (the
+ * node pointers are only compared, never dereferenced).  Writes up to `cap`
+ * windows and their total count to *n_out. */
+int lbr_fusion_windows(const OpNode* nodes, int n_nodes,
+                       const void* const* live_ptr, const size_t* live_bytes,
+                       int n_live, lbr_window* out, int cap, int* n_out);
+
+/* lbr_plan_create with peephole fusion (live-out ranges as above). */
+int lbr_plan_create_fused(const OpNode* nodes, int n_nodes, int use_graph,
+                          const void* const* live_ptr,
+                          const size_t* live_bytes, int n_live,
+                          lbr_plan** out_plan);
+
+/* Kernel steps of a plan (≤ nodes) and the nodes step `step` covers. */
+int lbr_plan_num_steps(const lbr_plan* plan);
+int lbr_plan_step_info(const lbr_plan* plan, int step, int* first_node,
+                       int* n_nodes, int* kind);
 
 #ifdef __cplusplus
 }

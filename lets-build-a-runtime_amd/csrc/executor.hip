@@ -9,6 +9,7 @@
 // LBR_ERR_UNSUPPORTED where the reference prints and aborts
 // (executor.c:461-464).
 #include "lbr_device.h"
+#include "lbr_fusion.h"
 
 #include <stdarg.h>
 #include <stdio.h>
@@ -116,6 +117,7 @@ static decode_fn decoder_for(int op) {
 static int decode_node(const OpNode* n, int index, Step* s) {
     memset(s, 0, sizeof(*s));
     s->node_index = index;
+    s->n_nodes = 1;
     decode_fn d = decoder_for(n->op);
     if (!d) {
         lbr_set_error("executor: unknown op %d (node %d)", n->op, index);
@@ -143,6 +145,8 @@ static int decode_node(const OpNode* n, int index, Step* s) {
 // ------------------------------------------------------------------ plan
 struct lbr_plan {
     std::vector<Step> steps;
+    int n_nodes = 0;
+    std::vector<int> node_step;  // node → its step, −1 inside a fused run after its first node
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     void* ws = nullptr;          // shared step workspace (split-K partial sums)
@@ -150,6 +154,76 @@ struct lbr_plan {
 
 static void run_steps(const std::vector<Step>& steps, hipStream_t st) {
     for (const Step& s : steps) s.run(s, st);
+}
+
+static bool bad_live(const void* const* live_ptr, const size_t* live_bytes, int n_live) {
+    return n_live < 0 || (n_live > 0 && (!live_ptr || !live_bytes));
+}
+
+// Decode every node (so each is validated exactly as without fusion), then
+// replace the fused runs by their steps; capture a hipGraph if asked.
+static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fuse, const void* const* live_ptr,
+                       const size_t* live_bytes, int n_live, lbr_plan** out_plan) {
+    lbr_plan* p = new lbr_plan();
+    p->n_nodes = n_nodes;
+    std::vector<Step> decoded((size_t)n_nodes);
+    for (int i = 0; i < n_nodes; ++i) {
+        int rc = decode_node(&nodes[i], i, &decoded[i]);
+        if (rc) {
+            delete p;
+            return rc;
+        }
+    }
+    std::vector<FusedRun> runs;
+    if (fuse) {
+        int rc = lbr_find_fusions(nodes, n_nodes, live_ptr, live_bytes, n_live, &runs);
+        if (rc) {
+            delete p;
+            return rc;
+        }
+    }
+    p->node_step.assign((size_t)n_nodes, -1);
+    size_t r = 0;
+    for (int i = 0; i < n_nodes;) {
+        p->node_step[i] = (int)p->steps.size();
+        if (r < runs.size() && runs[r].first == i) {
+            Step s;
+            int rc = lbr_fused_step(nodes, runs[r], &s);
+            if (rc) {
+                delete p;
+                return rc;
+            }
+            s.fuse_kind = runs[r].kind;
+            p->steps.push_back(s);
+            i += runs[r].count;
+            ++r;
+        } else {
+            p->steps.push_back(decoded[i]);
+            ++i;
+        }
+    }
+    int rc = assign_workspace(p->steps, &p->ws);
+    if (rc) {
+        delete p;
+        return rc;
+    }
+    if (use_graph && !p->steps.empty()) {
+        hipError_t e = hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal);
+        if (e == hipSuccess) {
+            run_steps(p->steps, g_stream);
+            e = hipStreamEndCapture(g_stream, &p->graph);
+        }
+        if (e == hipSuccess) e = hipGraphInstantiate(&p->exec, p->graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            lbr_set_error("lbr_plan_create: graph capture failed: %s", hipGetErrorString(e));
+            if (p->graph) (void)hipGraphDestroy(p->graph);
+            if (p->ws) (void)hipFree(p->ws);
+            delete p;
+            return LBR_ERR_HIP;
+        }
+    }
+    *out_plan = p;
+    return LBR_OK;
 }
 
 extern "C" {
@@ -275,36 +349,50 @@ int lbr_plan_create(const OpNode* nodes, int n_nodes, int use_graph, lbr_plan** 
     *out_plan = nullptr;
     int rc = ensure_init();
     if (rc) return rc;
-    lbr_plan* p = new lbr_plan();
-    p->steps.resize((size_t)n_nodes);
-    for (int i = 0; i < n_nodes; ++i) {
-        rc = decode_node(&nodes[i], i, &p->steps[i]);
-        if (rc) {
-            delete p;
-            return rc;
-        }
+    return create_plan(nodes, n_nodes, use_graph, false, nullptr, nullptr, 0, out_plan);
+}
+
+int lbr_plan_create_fused(const OpNode* nodes, int n_nodes, int use_graph, const void* const* live_ptr,
+                          const size_t* live_bytes, int n_live, lbr_plan** out_plan) {
+    if (!out_plan || n_nodes < 0 || (n_nodes > 0 && !nodes) || bad_live(live_ptr, live_bytes, n_live)) {
+        lbr_set_error("lbr_plan_create_fused: bad arguments");
+        return LBR_ERR_INVALID;
     }
-    rc = assign_workspace(p->steps, &p->ws);
-    if (rc) {
-        delete p;
-        return rc;
+    *out_plan = nullptr;
+    int rc = ensure_init();
+    if (rc) return rc;
+    return create_plan(nodes, n_nodes, use_graph, true, live_ptr, live_bytes, n_live, out_plan);
+}
+
+int lbr_fusion_windows(const OpNode* nodes, int n_nodes, const void* const* live_ptr, const size_t* live_bytes,
+                       int n_live, lbr_window* out, int cap, int* n_out) {
+    if (!n_out || n_nodes < 0 || (n_nodes > 0 && !nodes) || cap < 0 || (cap > 0 && !out) ||
+        bad_live(live_ptr, live_bytes, n_live)) {
+        lbr_set_error("lbr_fusion_windows: bad arguments");
+        return LBR_ERR_INVALID;
     }
-    if (use_graph && n_nodes > 0) {
-        hipError_t e = hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal);
-        if (e == hipSuccess) {
-            run_steps(p->steps, g_stream);
-            e = hipStreamEndCapture(g_stream, &p->graph);
-        }
-        if (e == hipSuccess) e = hipGraphInstantiate(&p->exec, p->graph, nullptr, nullptr, 0);
-        if (e != hipSuccess) {
-            lbr_set_error("lbr_plan_create: graph capture failed: %s", hipGetErrorString(e));
-            if (p->graph) (void)hipGraphDestroy(p->graph);
-            if (p->ws) (void)hipFree(p->ws);
-            delete p;
-            return LBR_ERR_HIP;
-        }
+    std::vector<FusedRun> runs;
+    int rc = lbr_find_fusions(nodes, n_nodes, live_ptr, live_bytes, n_live, &runs);
+    if (rc) return rc;
+    for (size_t k = 0; k < runs.size() && (int)k < cap; ++k) {
+        out[k].first = runs[k].first;
+        out[k].count = runs[k].count;
+        out[k].kind = runs[k].kind;
     }
-    *out_plan = p;
+    *n_out = (int)runs.size();
+    return LBR_OK;
+}
+
+int lbr_plan_num_steps(const lbr_plan* p) { return p ? (int)p->steps.size() : 0; }
+
+int lbr_plan_step_info(const lbr_plan* p, int step, int* first_node, int* n_nodes, int* kind) {
+    if (!p || step < 0 || step >= (int)p->steps.size()) {
+        lbr_set_error("lbr_plan_step_info: bad arguments");
+        return LBR_ERR_INVALID;
+    }
+    if (first_node) *first_node = p->steps[step].node_index;
+    if (n_nodes) *n_nodes = p->steps[step].n_nodes;
+    if (kind) *kind = p->steps[step].fuse_kind;
     return LBR_OK;
 }
 
@@ -317,7 +405,7 @@ int lbr_plan_destroy(lbr_plan* p) {
     return LBR_OK;
 }
 
-int lbr_plan_num_nodes(const lbr_plan* p) { return p ? (int)p->steps.size() : 0; }
+int lbr_plan_num_nodes(const lbr_plan* p) { return p ? p->n_nodes : 0; }
 
 int lbr_plan_launch(lbr_plan* p) {
     if (!p) {
@@ -368,7 +456,7 @@ int lbr_plan_time(lbr_plan* p, int iters, float* out_ms) {
 }
 
 int lbr_plan_profile(lbr_plan* p, int iters, float* out_ms, int n_out) {
-    if (!p || !out_ms || iters <= 0 || n_out < (int)p->steps.size()) {
+    if (!p || !out_ms || iters <= 0 || n_out < p->n_nodes) {
         lbr_set_error("lbr_plan_profile: bad arguments");
         return LBR_ERR_INVALID;
     }
@@ -391,16 +479,20 @@ int lbr_plan_profile(lbr_plan* p, int iters, float* out_ms, int n_out) {
         }
     }
     for (auto& e : ev) (void)hipEventDestroy(e);
-    for (size_t i = 0; i < n; ++i) out_ms[i] = (float)(acc[i] / iters);
+    // a step's time goes to its first node; the other nodes of a fused run get 0
+    for (int i = 0; i < p->n_nodes; ++i) out_ms[i] = 0.f;
+    for (size_t i = 0; i < n; ++i) out_ms[p->steps[i].node_index] = (float)(acc[i] / iters);
     return LBR_OK;
 }
 
 int lbr_plan_node_kernel(const lbr_plan* p, int index, char* name_out, int name_cap) {
-    if (!p || index < 0 || index >= (int)p->steps.size() || !name_out || name_cap <= 0) {
+    if (!p || index < 0 || index >= p->n_nodes || !name_out || name_cap <= 0) {
         lbr_set_error("lbr_plan_node_kernel: bad arguments");
         return LBR_ERR_INVALID;
     }
-    snprintf(name_out, (size_t)name_cap, "%s", p->steps[index].name ? p->steps[index].name : "?");
+    const int st = p->node_step[index];
+    const char* name = st < 0 ? "fused" : (p->steps[st].name ? p->steps[st].name : "?");
+    snprintf(name_out, (size_t)name_cap, "%s", name);
     return LBR_OK;
 }
 

@@ -1,0 +1,579 @@
+// fusion.hip — peephole fusion over the unchanged OpNode array.
+//
+// The node stream the host layer builds (runtime/executor/nodes.py, the
+// reference's compiled.py:50-157) is kept exactly; at plan creation the
+// library looks for short runs of consecutive nodes that one kernel can do
+// and launches that kernel in their place.  A run is fused only when
+//   * its nodes match one of the patterns below exactly (ops, extras,
+//     pointer chaining, shapes), and
+//   * every value the run produces except its final outputs is dead: no
+//     later node reads it before the memory is overwritten, and it does not
+//     overlap a caller-declared live-out range (the graph outputs), and
+//   * no final output overlaps memory the fused kernel reads (the planner
+//     may place a node's output over its dead input; one fused kernel reads
+//     and writes with a different index map, so that reuse is refused).
+// Final outputs land at the planner's offsets with the values the unfused
+// nodes would write (same operation order for every rounding step; the only
+// reassociation is the sum of squares inside RMSNorm).
+//
+// Patterns:
+//   GEMM_RESID  MATMUL[_ADD] → ADD(same shape, C, R): R is added in the GEMM
+//               epilogue (the residual adds of every pre-norm block).
+//   GEMM_HEADS  MATMUL[_ADD] → k × (SLICE last dim → [ADD bias row] →
+//               TRANSPOSE(S,H)): the GEMM epilogue writes each column range
+//               straight into its [B, H, S, hd] output (merged QKV
+//               projections, passes.py merge_parallel_matmuls).
+//   HEAD_PROLOGUE  SLICE last dim → [ADD bias row] → [RMSNORM over hd] →
+//               TRANSPOSE(S,H) → [RoPE: MUL cos, SLICE, SLICE, NEG, CAT,
+//               MUL sin, ADD]: one wavefront per (token, head) row.
+#include "lbr_device.h"
+
+#include <math.h>
+#include <vector>
+
+#include "lbr_fusion.h"
+
+namespace {
+
+// ------------------------------------------------------------ device kernel
+
+struct HeadArgs {
+    const float* src;         // sliced tensor (rows × ld), columns col0 ..
+    long long ld;
+    int col0;
+    int B, S, H, hd;
+    const float* bias;        // [H·hd] or null
+    const float* w;           // RMSNorm weight [hd] or null
+    float eps;
+    const float* cos;         // RoPE tables, element (b,h,s,d) at b·c[0]+h·c[1]+s·c[2]+d
+    const float* sin;
+    long long cst[3], sst[3];
+    float* out;               // [B, H, S, hd]
+    long long rows;           // B·S·H
+};
+
+template <int VPL, bool BIAS, bool NORM, bool ROPE>
+__global__ __launch_bounds__(256) void head_prologue(HeadArgs a) {
+    const int lane = threadIdx.x & 63;
+    const long long row = blockIdx.x * 4LL + (threadIdx.x >> 6);   // (b·S + s)·H + h
+    if (row >= a.rows) return;
+    const int h = (int)(row % a.H);
+    const long long bs = row / a.H;
+    const int s = (int)(bs % a.S), b = (int)(bs / a.S);
+    const float* __restrict__ x = a.src + bs * a.ld + a.col0 + (long long)h * a.hd;
+    float v[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+        const int d = lane + 64 * j;
+        v[j] = x[d];
+        if (BIAS) v[j] = v[j] + a.bias[h * a.hd + d];
+    }
+    if (NORM) {   // norm.c:100-107 order: x · (1/sqrt(Σx²/n + eps)) · w
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) ss += v[j] * v[j];
+        ss = wave_sum(ss);
+        const float scale = 1.0f / sqrtf(ss / a.hd + a.eps);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) v[j] = v[j] * scale * a.w[lane + 64 * j];
+    }
+    float* __restrict__ o = a.out + (((long long)b * a.H + h) * a.S + s) * a.hd;
+    if (ROPE) {   // y = x·cos + rotate_half(x)·sin, rotate_half = cat(−x[half:], x[:half])
+        const int half = a.hd / 2;
+        const long long cb = b * a.cst[0] + h * a.cst[1] + s * a.cst[2];
+        const long long sb = b * a.sst[0] + h * a.sst[1] + s * a.sst[2];
+        float p[VPL];
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            if (VPL >= 2) p[j] = v[j ^ (VPL / 2)];      // half = 64·VPL/2: partner in this lane
+            else p[j] = __shfl_xor(v[j], 32, 64);         // hd = 64: partner 32 lanes away
+        }
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int d = lane + 64 * j;
+            const float rot = d < half ? -p[j] : p[j];
+            o[d] = __fadd_rn(__fmul_rn(v[j], a.cos[cb + d]), __fmul_rn(rot, a.sin[sb + d]));
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) o[lane + 64 * j] = v[j];
+    }
+}
+
+// Step::in[0]=src [1]=bias [2]=w [3]=cos [4]=sin; i[0]=ld [1]=col0 [2]=B
+// [3]=S [4]=H [5]=hd [6..8]=cos strides [9..11]=sin strides [12]=rows; f[0]=eps
+template <int VPL, bool BIAS, bool NORM, bool ROPE>
+void launch_head_prologue(const Step& s, hipStream_t st) {
+    HeadArgs a;
+    a.src = (const float*)s.in[0];
+    a.bias = (const float*)s.in[1];
+    a.w = (const float*)s.in[2];
+    a.cos = (const float*)s.in[3];
+    a.sin = (const float*)s.in[4];
+    a.out = (float*)s.out;
+    a.ld = s.i[0];
+    a.col0 = (int)s.i[1];
+    a.B = (int)s.i[2];
+    a.S = (int)s.i[3];
+    a.H = (int)s.i[4];
+    a.hd = (int)s.i[5];
+    for (int k = 0; k < 3; ++k) {
+        a.cst[k] = s.i[6 + k];
+        a.sst[k] = s.i[9 + k];
+    }
+    a.rows = s.i[12];
+    a.eps = s.f[0];
+    if (a.rows <= 0) return;
+    hipLaunchKernelGGL((head_prologue<VPL, BIAS, NORM, ROPE>), dim3((unsigned)((a.rows + 3) / 4)), dim3(256), 0, st,
+                       a);
+}
+
+template <int VPL, bool BIAS>
+step_fn pick_hp2(bool norm, bool rope) {
+    if (norm) return rope ? launch_head_prologue<VPL, BIAS, true, true> : launch_head_prologue<VPL, BIAS, true, false>;
+    return rope ? launch_head_prologue<VPL, BIAS, false, true> : launch_head_prologue<VPL, BIAS, false, false>;
+}
+
+template <int VPL>
+step_fn pick_hp(bool bias, bool norm, bool rope) {
+    return bias ? pick_hp2<VPL, true>(norm, rope) : pick_hp2<VPL, false>(norm, rope);
+}
+
+// ------------------------------------------------------------ matching
+
+struct Rng {
+    uintptr_t lo, hi;
+};
+
+bool overlap(Rng a, Rng b) { return a.lo < b.hi && b.lo < a.hi; }
+
+Rng out_rng(const OpNode* n) {
+    const uintptr_t p = (uintptr_t)n->output;
+    return {p, p + (uintptr_t)(node_total(n) * (n->elem_size > 0 ? n->elem_size : 4))};
+}
+
+Rng rng(const void* p, long long bytes) { return {(uintptr_t)p, (uintptr_t)p + (uintptr_t)bytes}; }
+
+bool contains(Rng r, const void* p) { return (uintptr_t)p >= r.lo && (uintptr_t)p < r.hi; }
+
+bool is_f32(const OpNode* n) { return n->elem_size == 4; }
+
+// inter minus w.
+void subtract(std::vector<Rng>* inter, Rng w) {
+    std::vector<Rng> rest;
+    for (const Rng& r : *inter) {
+        if (!overlap(r, w)) {
+            rest.push_back(r);
+            continue;
+        }
+        if (r.lo < w.lo) rest.push_back({r.lo, w.lo});
+        if (w.hi < r.hi) rest.push_back({w.hi, r.hi});
+    }
+    inter->swap(rest);
+}
+
+// Values the run [first, end) writes to `inter` are dead once the run is
+// over: the parts its own final outputs `outs` overwrite do not count;
+// walking the later nodes in order, no input pointer lands in a part not
+// yet overwritten, and what is left at the end overlaps no live-out range.
+bool dead_after(const OpNode* nodes, int n, int end, std::vector<Rng> inter, const std::vector<Rng>& outs,
+                const std::vector<Rng>& live) {
+    for (const Rng& o : outs) subtract(&inter, o);
+    for (int j = end; j < n && !inter.empty(); ++j) {
+        const OpNode* nd = &nodes[j];
+        // ATTENTION's trailing input is the planner's scratch slot (ops.py:437-459):
+        // written before it is read, so it is not a read of older values
+        const int reads = nd->op == OP_ATTENTION ? 3 + (nd->extra[3] != 0) : nd->n_inputs;
+        for (int k = 0; k < reads && k < nd->n_inputs && k < MAX_INPUTS; ++k)
+            for (const Rng& r : inter)
+                if (contains(r, nd->inputs[k])) return false;
+        subtract(&inter, out_rng(nd));
+    }
+    for (const Rng& r : inter)
+        for (const Rng& l : live)
+            if (overlap(r, l)) return false;
+    return true;
+}
+
+float extra_f(const OpNode* n, int i) { return node_extra_float(n, i); }
+
+struct Rope {
+    const void* cos;
+    const void* sin;
+    long long cst[3], sst[3];
+    const void* out;
+};
+
+// The 7-node rotate_half RoPE window (HF apply_rotary_pos_emb as exported:
+// q·cos, q[..., :half], q[..., half:], −, cat, ·sin, +) on x = [B, H, S, hd].
+bool match_rope(const OpNode* nodes, int n, int q, const void* x, int B, int H, int S, int hd, Rope* r,
+                std::vector<Rng>* inter) {
+    if (q + 7 > n || hd % 2) return false;
+    const int half = hd / 2;
+    const long long rows = (long long)B * H * S;
+    const OpNode* mc = &nodes[q];
+    const OpNode* s1 = &nodes[q + 1];
+    const OpNode* s2 = &nodes[q + 2];
+    const OpNode* ng = &nodes[q + 3];
+    const OpNode* ct = &nodes[q + 4];
+    const OpNode* ms = &nodes[q + 5];
+    const OpNode* ad = &nodes[q + 6];
+    for (int k = 0; k < 7; ++k)
+        if (!is_f32(&nodes[q + k])) return false;
+    const int shape[4] = {B, H, S, hd};
+    auto bcast_mul = [&](const OpNode* m, const void* a, long long* st) {
+        // SUB/MUL/DIV extras: [2 = broadcast, ndim, a strides, b strides, out shape]
+        if (m->op != OP_MUL || m->n_inputs < 2 || m->inputs[0] != a || m->n_dims != 4) return false;
+        if (m->extra[0] != 2 || m->extra[1] != 4) return false;
+        const long long full[4] = {(long long)H * S * hd, (long long)S * hd, hd, 1};
+        for (int d = 0; d < 4; ++d) {
+            if (m->out_shape[d] != shape[d] || m->extra[10 + d] != shape[d]) return false;
+            const long long as = m->extra[2 + d];
+            if (!(as == full[d] || (as == 0 && shape[d] == 1))) return false;
+        }
+        if (m->extra[6 + 3] != 1) return false;
+        for (int d = 0; d < 3; ++d) st[d] = shape[d] == 1 ? 0 : m->extra[6 + d];
+        return true;
+    };
+    if (!bcast_mul(mc, x, r->cst)) return false;
+    // SLICE extras [outer, orig, start, len, inner] along the last dim
+    if (s1->op != OP_SLICE || s1->inputs[0] != x || s1->extra[0] != rows || s1->extra[1] != hd ||
+        s1->extra[2] != 0 || s1->extra[3] != half || s1->extra[4] != 1)
+        return false;
+    if (s2->op != OP_SLICE || s2->inputs[0] != x || s2->extra[0] != rows || s2->extra[1] != hd ||
+        s2->extra[2] != half || s2->extra[3] != half || s2->extra[4] != 1)
+        return false;
+    if (ng->op != OP_NEG || ng->inputs[0] != s2->output || node_total(ng) != rows * half) return false;
+    // CAT extras [dim, sizes...]: cat(−x2, x1) on the last dim
+    if (ct->op != OP_CAT || ct->n_inputs != 2 || ct->inputs[0] != ng->output || ct->inputs[1] != s1->output ||
+        ct->n_dims != 4 || ct->extra[0] != 3 || ct->extra[1] != half || ct->extra[2] != half)
+        return false;
+    if (!bcast_mul(ms, ct->output, r->sst)) return false;
+    // ADD extras [1] = same shape
+    if (ad->op != OP_ADD || ad->n_inputs < 2 || ad->extra[0] != 1 || node_total(ad) != rows * hd) return false;
+    const bool ab = ad->inputs[0] == mc->output && ad->inputs[1] == ms->output;
+    const bool ba = ad->inputs[0] == ms->output && ad->inputs[1] == mc->output;
+    if (!ab && !ba) return false;
+    r->cos = mc->inputs[1];
+    r->sin = ms->inputs[1];
+    r->out = ad->output;
+    for (int k = 0; k < 6; ++k) inter->push_back(out_rng(&nodes[q + k]));
+    return true;
+}
+
+// SLICE(C, last dim) → [ADD bias row] → [RMSNORM] → TRANSPOSE(S,H) → [RoPE]
+// starting at node p.  C has `rows` rows of `ld` floats.
+struct HeadChain {
+    int first = 0, count = 0;
+    int col0 = 0, width = 0;
+    int B = 0, S = 0, H = 0, hd = 0;
+    const void* bias = nullptr;
+    const void* norm_w = nullptr;
+    float eps = 0.f;
+    bool rope = false;
+    Rope rp{};
+    const void* out = nullptr;
+    Rng out_r{};
+    std::vector<Rng> inter;   // values written by the chain other than `out`
+};
+
+bool match_head_chain(const OpNode* nodes, int n, int p, const void* C, long long rows, int ld, bool norm_rope,
+                      HeadChain* hc) {
+    const OpNode* sl = &nodes[p];
+    if (sl->op != OP_SLICE || sl->n_inputs < 1 || sl->inputs[0] != C || !is_f32(sl)) return false;
+    if (sl->extra[0] != rows || sl->extra[1] != ld || sl->extra[4] != 1) return false;
+    hc->first = p;
+    hc->col0 = sl->extra[2];
+    hc->width = sl->extra[3];
+    hc->inter.clear();
+    hc->inter.push_back(out_rng(sl));
+    const void* cur = sl->output;
+    int q = p + 1;
+    if (q < n && nodes[q].op == OP_ADD && nodes[q].n_inputs >= 2 && nodes[q].inputs[0] == cur &&
+        nodes[q].extra[0] == 0 && is_f32(&nodes[q]) && node_last_dim(&nodes[q]) == hc->width) {
+        hc->bias = nodes[q].inputs[1];
+        cur = nodes[q].output;
+        hc->inter.push_back(out_rng(&nodes[q]));
+        ++q;
+    }
+    int norm_hd = 0;
+    if (norm_rope && q < n && nodes[q].op == OP_RMSNORM && nodes[q].n_inputs >= 2 && nodes[q].inputs[0] == cur &&
+        is_f32(&nodes[q]) && nodes[q].n_dims >= 2) {
+        norm_hd = node_last_dim(&nodes[q]);
+        if (norm_hd <= 0 || hc->width % norm_hd) return false;
+        hc->norm_w = nodes[q].inputs[1];
+        hc->eps = extra_f(&nodes[q], 0);
+        cur = nodes[q].output;
+        hc->inter.push_back(out_rng(&nodes[q]));
+        ++q;
+    }
+    // N-D TRANSPOSE extras [outer, A, middle, B, inner]: [B, S, 1, H, hd]
+    if (q >= n) return false;
+    const OpNode* tr = &nodes[q];
+    if (tr->op != OP_TRANSPOSE || tr->n_inputs < 1 || tr->inputs[0] != cur || tr->n_dims != 4 || !is_f32(tr))
+        return false;
+    const int B = tr->extra[0], S = tr->extra[1], H = tr->extra[3], hd = tr->extra[4];
+    if (tr->extra[2] != 1 || (long long)B * S != rows || (long long)H * hd != hc->width) return false;
+    if (norm_hd && norm_hd != hd) return false;
+    if (tr->out_shape[0] != B || tr->out_shape[1] != H || tr->out_shape[2] != S || tr->out_shape[3] != hd)
+        return false;
+    hc->B = B;
+    hc->S = S;
+    hc->H = H;
+    hc->hd = hd;
+    cur = tr->output;
+    ++q;
+    hc->rope = false;
+    if (norm_rope) {
+        std::vector<Rng> ri;
+        Rope r{};
+        if (match_rope(nodes, n, q, cur, B, H, S, hd, &r, &ri)) {
+            hc->inter.push_back(out_rng(tr));
+            hc->inter.insert(hc->inter.end(), ri.begin(), ri.end());
+            hc->rope = true;
+            hc->rp = r;
+            cur = r.out;
+            q += 7;
+        }
+    }
+    hc->out = cur;
+    hc->out_r = out_rng(&nodes[q - 1]);
+    hc->count = q - p;
+    return true;
+}
+
+// Extent of a GEMM's inputs (A, B, bias) for the overlap test.
+void gemm_input_rngs(const OpNode* g, const Step& st, std::vector<Rng>* r) {
+    const long long M = st.i[0], N = st.i[1], K = st.i[2], batches = st.i[3];
+    const bool b2d = g->extra[2] != 0;
+    r->push_back(rng(g->inputs[0], M * K * batches * 4));
+    r->push_back(rng(g->inputs[1], N * K * (b2d ? 1 : batches) * 4));
+    if (g->op == OP_MATMUL_ADD) r->push_back(rng(g->inputs[2], N * 4));
+}
+
+bool any_overlap(Rng a, const std::vector<Rng>& v) {
+    for (const Rng& b : v)
+        if (overlap(a, b)) return true;
+    return false;
+}
+
+bool gemm_step(const OpNode* g, Step* st) {
+    if (g->op != OP_MATMUL && g->op != OP_MATMUL_ADD) return false;
+    *st = Step();
+    if (decode_matmul(g, st) != LBR_OK) {
+        lbr_set_error("");
+        return false;
+    }
+    return st->i[13] == 1;
+}
+
+}  // namespace
+
+// Find the fusable runs of `nodes` (in order, non-overlapping).
+int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, const size_t* live_bytes, int n_live,
+                     std::vector<FusedRun>* out) {
+    out->clear();
+    std::vector<Rng> live;
+    for (int k = 0; k < n_live; ++k) live.push_back(rng(live_ptr[k], (long long)live_bytes[k]));
+    int i = 0;
+    while (i < n) {
+        const OpNode* nd = &nodes[i];
+        Step gs;
+        if (gemm_step(nd, &gs)) {
+            std::vector<Rng> gin;
+            gemm_input_rngs(nd, gs, &gin);
+            const Rng c_r = out_rng(nd);
+            // GEMM_HEADS
+            if (gs.i[3] == 1 && i + 1 < n) {
+                const long long rows = gs.i[0];
+                const int N = (int)gs.i[1];
+                std::vector<HeadChain> chains;
+                int q = i + 1;
+                while (q < n && chains.size() < 4) {
+                    HeadChain hc;
+                    if (!match_head_chain(nodes, n, q, nd->output, rows, N, false, &hc)) break;
+                    q += hc.count;
+                    chains.push_back(hc);
+                }
+                bool ok = !chains.empty();
+                std::vector<Rng> inter{c_r}, outs, reads = gin;
+                for (const HeadChain& hc : chains) {
+                    inter.insert(inter.end(), hc.inter.begin(), hc.inter.end());
+                    if (hc.bias) reads.push_back(rng(hc.bias, (long long)hc.width * 4));
+                }
+                for (const HeadChain& hc : chains) {
+                    if (any_overlap(hc.out_r, reads) || any_overlap(hc.out_r, outs)) ok = false;
+                    outs.push_back(hc.out_r);
+                }
+                if (ok) ok = dead_after(nodes, n, q, inter, outs, live);
+                // splits must tile the columns they cover in order, with one head dim and S
+                for (size_t k = 1; ok && k < chains.size(); ++k)
+                    ok = chains[k].col0 == chains[k - 1].col0 + chains[k - 1].width &&
+                         chains[k].hd == chains[0].hd && chains[k].S == chains[0].S && chains[k].B == chains[0].B;
+                if (ok) {
+                    FusedRun f;
+                    f.first = i;
+                    f.count = q - i;
+                    f.kind = LBR_FUSE_GEMM_HEADS;
+                    f.n_split = (int)chains.size();
+                    for (size_t k = 0; k < chains.size(); ++k) {
+                        f.col_begin[k] = chains[k].col0;
+                        f.width[k] = chains[k].width;
+                        f.dst[k] = chains[k].out;
+                        f.sbias[k] = chains[k].bias;
+                        f.Hs[k] = chains[k].H;
+                    }
+                    f.hd = chains[0].hd;
+                    f.S = chains[0].S;
+                    f.B = chains[0].B;
+                    out->push_back(f);
+                    i = q;
+                    continue;
+                }
+            }
+            // GEMM_RESID
+            if (i + 1 < n) {
+                const OpNode* ad = &nodes[i + 1];
+                if (ad->op == OP_ADD && ad->n_inputs >= 2 && ad->extra[0] == 1 && is_f32(ad) && is_f32(nd) &&
+                    node_total(ad) == node_total(nd) && (ad->inputs[0] == nd->output) != (ad->inputs[1] == nd->output)) {
+                    const void* R = ad->inputs[0] == nd->output ? ad->inputs[1] : ad->inputs[0];
+                    const Rng y = out_rng(ad);
+                    const Rng r_r = rng(R, node_total(nd) * 4);
+                    bool ok = !any_overlap(y, gin) && (y.lo == r_r.lo || !overlap(y, r_r));
+                    if (ok) ok = dead_after(nodes, n, i + 2, {c_r}, {y}, live);
+                    if (ok) {
+                        FusedRun f;
+                        f.first = i;
+                        f.count = 2;
+                        f.kind = LBR_FUSE_GEMM_RESID;
+                        f.resid = R;
+                        f.out = ad->output;
+                        out->push_back(f);
+                        i += 2;
+                        continue;
+                    }
+                }
+            }
+            ++i;
+            continue;
+        }
+        // HEAD_PROLOGUE: a SLICE of a row-major [rows, ld] tensor
+        if (nd->op == OP_SLICE && nd->n_inputs >= 1 && nd->extra[4] == 1 && is_f32(nd)) {
+            HeadChain hc;
+            const long long rows = nd->extra[0];
+            const int ld = nd->extra[1];
+            if (match_head_chain(nodes, n, i, nd->inputs[0], rows, ld, true, &hc) &&
+                (hc.hd == 64 || hc.hd == 128 || hc.hd == 256)) {
+                std::vector<Rng> reads{rng(nd->inputs[0], rows * ld * 4)};
+                if (hc.bias) reads.push_back(rng(hc.bias, (long long)hc.width * 4));
+                if (hc.norm_w) reads.push_back(rng(hc.norm_w, (long long)hc.hd * 4));
+                bool ok = !any_overlap(hc.out_r, reads);
+                if (ok && hc.rope) {
+                    // the tables' extents follow from their strides
+                    auto ext = [&](const long long* st) {
+                        return ((long long)(hc.B - 1) * st[0] + (long long)(hc.H - 1) * st[1] +
+                                (long long)(hc.S - 1) * st[2] + hc.hd) * 4;
+                    };
+                    ok = !overlap(hc.out_r, rng(hc.rp.cos, ext(hc.rp.cst))) &&
+                         !overlap(hc.out_r, rng(hc.rp.sin, ext(hc.rp.sst)));
+                }
+                if (ok) ok = dead_after(nodes, n, i + hc.count, hc.inter, {hc.out_r}, live);
+                if (ok) {
+                    FusedRun f;
+                    f.first = i;
+                    f.count = hc.count;
+                    f.kind = LBR_FUSE_HEAD_PROLOGUE;
+                    f.src = nd->inputs[0];
+                    f.ld = ld;
+                    f.col_begin[0] = hc.col0;
+                    f.B = hc.B;
+                    f.S = hc.S;
+                    f.Hs[0] = hc.H;
+                    f.hd = hc.hd;
+                    f.sbias[0] = hc.bias;
+                    f.norm_w = hc.norm_w;
+                    f.eps = hc.eps;
+                    f.rope = hc.rope;
+                    if (hc.rope) {
+                        f.cos = hc.rp.cos;
+                        f.sin = hc.rp.sin;
+                        for (int k = 0; k < 3; ++k) {
+                            f.cst[k] = hc.rp.cst[k];
+                            f.sst[k] = hc.rp.sst[k];
+                        }
+                    }
+                    f.out = hc.out;
+                    out->push_back(f);
+                    i += hc.count;
+                    continue;
+                }
+            }
+        }
+        ++i;
+    }
+    return LBR_OK;
+}
+
+// Decoded launch record of a fused run.
+int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
+    *s = Step();
+    if (f.kind == LBR_FUSE_GEMM_RESID || f.kind == LBR_FUSE_GEMM_HEADS) {
+        int rc = decode_matmul(&nodes[f.first], s);
+        if (rc) return rc;
+        if (s->i[13] != 1) {
+            lbr_set_error("fusion: GEMM node %d is not on the MFMA path", f.first);
+            return LBR_ERR_INVALID;
+        }
+        if (f.kind == LBR_FUSE_GEMM_RESID) {
+            s->in[3] = f.resid;
+            s->out = (void*)f.out;
+            s->i[12] = s->i[12] && lbr_aligned(f.out, 16);
+            s->name = s->i[4] ? "gemm_mfma_f32_nt+resid" : "gemm_mfma_f32_nn+resid";
+        } else {
+            if (f.n_split < 1 || f.n_split > 4) {
+                lbr_set_error("fusion: %d head splits", f.n_split);
+                return LBR_ERR_INVALID;
+            }
+            s->i[19] = f.n_split;
+            for (int k = 0; k < f.n_split; ++k) {
+                s->i[20 + k] = f.col_begin[k];
+                s->in[4 + k] = (void*)f.dst[k];
+                s->in[8 + k] = f.sbias[k];
+                s->i[25 + k] = f.Hs[k];
+            }
+            s->i[20 + f.n_split] = f.col_begin[f.n_split - 1] + f.width[f.n_split - 1];
+            s->i[29] = f.hd;
+            s->i[30] = f.S;
+            s->name = s->i[4] ? "gemm_mfma_f32_nt+heads" : "gemm_mfma_f32_nn+heads";
+        }
+    } else {
+        s->in[0] = f.src;
+        s->in[1] = f.sbias[0];
+        s->in[2] = f.norm_w;
+        s->in[3] = f.cos;
+        s->in[4] = f.sin;
+        s->out = (void*)f.out;
+        s->i[0] = f.ld;
+        s->i[1] = f.col_begin[0];
+        s->i[2] = f.B;
+        s->i[3] = f.S;
+        s->i[4] = f.Hs[0];
+        s->i[5] = f.hd;
+        for (int k = 0; k < 3; ++k) {
+            s->i[6 + k] = f.cst[k];
+            s->i[9 + k] = f.sst[k];
+        }
+        s->i[12] = (long long)f.B * f.S * f.Hs[0];
+        s->f[0] = f.eps;
+        const bool bias = f.sbias[0] != nullptr, norm = f.norm_w != nullptr;
+        switch (f.hd / 64) {
+            case 1: s->run = pick_hp<1>(bias, norm, f.rope); break;
+            case 2: s->run = pick_hp<2>(bias, norm, f.rope); break;
+            default: s->run = pick_hp<4>(bias, norm, f.rope); break;
+        }
+        s->name = f.rope ? (norm ? "head_norm_rope" : "head_rope") : (norm ? "head_norm" : "head_transpose");
+    }
+    s->node_index = f.first;
+    s->n_nodes = f.count;
+    return LBR_OK;
+}

@@ -42,7 +42,33 @@ struct GemmArgs {
     int tiles_m, tiles_n;
     float* W;                 // split-K partial sums [ksplit][batches][M][N] (ksplit > 1)
     int ksplit, kchunk;       // number of K ranges, K per range (multiple of BK)
+    // Fused epilogues (set only by the plan's peephole fusion; all null/0 otherwise).
+    const float* resid;       // C += resid (same layout as C): a following same-shape ADD
+    int n_split;              // >0: C columns are scattered as attention heads, see epi_store
+    int col_begin[5];         // split k owns columns [col_begin[k], col_begin[k+1])
+    float* dst[4];            // split k's output, laid out [B, H, S, hd]
+    const float* sbias[4];    // split k's bias row (indexed by column - col_begin[k]) or null
+    int Hs[4], hd, S;         // heads of each split, head dim, rows per batch (M = B·S)
 };
+
+// Final store of one C element (row m, column n of batch bz) with the fused
+// epilogues applied in the order the unfused nodes would: v (already
+// alpha-scaled or bias-added) + resid, then the scattered split's bias.
+__device__ __forceinline__ void epi_store(const GemmArgs& g, long long bz, int m, int n, float v) {
+    if (g.resid) v = v + g.resid[bz * g.sC + (long long)m * g.N + n];
+    if (g.n_split == 0) {
+        g.C[bz * g.sC + (long long)m * g.N + n] = v;
+        return;
+    }
+    if (n < g.col_begin[0] || n >= g.col_begin[g.n_split]) return;   // columns no split reads
+    int k = 0;
+    while (k + 1 < g.n_split && n >= g.col_begin[k + 1]) ++k;
+    const int c = n - g.col_begin[k];
+    if (g.sbias[k]) v = v + g.sbias[k][c];
+    const int h = c / g.hd, d = c - h * g.hd;
+    const int b = m / g.S, s = m - b * g.S;
+    g.dst[k][(((long long)b * g.Hs[k] + h) * g.S + s) * g.hd + d] = v;
+}
 
 __device__ __forceinline__ void tile_coords(const GemmArgs& g, int& tm, int& tn) {
     // XCD-aware remap: hardware places workgroup id w on XCD w % 8.
@@ -247,6 +273,69 @@ __global__ __launch_bounds__(NT, 2) void gemm_mfma_f32(GemmArgs g) {
             }
         return;
     }
+    if (g.n_split) {
+        // Head scatter: the column fixes split, head, d and split bias; the
+        // row fixes (b, s) = divmod(m, S), stepped from the block's first row.
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = n0 + wn * 64 + j * 32 + lrow;
+            if (n >= g.N || n < g.col_begin[0] || n >= g.col_begin[g.n_split]) continue;
+            int k = 0;
+            while (k + 1 < g.n_split && n >= g.col_begin[k + 1]) ++k;
+            const int c = n - g.col_begin[k];
+            const int h = c / g.hd, d = c - h * g.hd;
+            const float bv = HAS_BIAS ? g.bias[n] : 0.f;
+            const float sb = g.sbias[k] ? g.sbias[k][c] : 0.f;
+            const bool has_sb = g.sbias[k] != nullptr;
+            float* __restrict__ col = g.dst[k] + ((long long)h * g.S) * g.hd + d;
+            const long long bstride = (long long)g.Hs[k] * g.S * g.hd;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int mb = m0 + wm * 64 + i * 32 + 4 * lhalf;
+                const int b0 = mb / g.S, s0 = mb - b0 * g.S;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int o = 8 * (r >> 2) + (r & 3);
+                    if (mb + o >= g.M) continue;
+                    int b = b0, s = s0 + o;
+                    while (s >= g.S) {   // o < 32: at most one step unless S < 32
+                        s -= g.S;
+                        ++b;
+                    }
+                    float v = HAS_BIAS ? (acc[i][j][r] + bv) : g.alpha * acc[i][j][r];
+                    if (has_sb) v = v + sb;
+                    col[b * bstride + (long long)s * g.hd] = v;
+                }
+            }
+        }
+        return;
+    }
+    if (g.resid) {
+        const float* __restrict__ R = g.resid + bz * g.sC;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = n0 + wn * 64 + j * 32 + lrow;
+                if (n >= g.N) continue;
+                const float bv = HAS_BIAS ? g.bias[n] : 0.f;
+                float rv[16];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {   // all loads first, then the adds and stores
+                    const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+                    rv[r] = m < g.M ? R[(long long)m * g.N + n] : 0.f;
+                }
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+                    if (m < g.M) {
+                        const float v = HAS_BIAS ? (acc[i][j][r] + bv) : g.alpha * acc[i][j][r];
+                        C[(long long)m * g.N + n] = v + rv[r];
+                    }
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -257,10 +346,7 @@ __global__ __launch_bounds__(NT, 2) void gemm_mfma_f32(GemmArgs g) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-                if (m < g.M) {
-                    const float v = acc[i][j][r];
-                    C[(long long)m * g.N + n] = HAS_BIAS ? (v + bv) : g.alpha * v;
-                }
+                if (m < g.M) C[(long long)m * g.N + n] = HAS_BIAS ? (acc[i][j][r] + bv) : g.alpha * acc[i][j][r];
             }
         }
 }
@@ -329,14 +415,29 @@ GemmArgs make_args(const Step& s) {
     g.ksplit = s.i[10] > 1 ? (int)s.i[10] : 1;
     g.kchunk = g.ksplit > 1 ? (int)s.i[11] : g.K;
     g.W = (float*)s.ws;
+    // fused epilogue: in[3] = resid; i[19] = n_split, i[20..24] = col_begin,
+    // in[4..7] = dst, in[8..11] = split biases, i[25..28] = heads per split,
+    // i[29] = hd, i[30] = S
+    g.resid = (const float*)s.in[3];
+    g.n_split = (int)s.i[19];
+    for (int k = 0; k < 5; ++k) g.col_begin[k] = (int)s.i[20 + k];
+    for (int k = 0; k < 4; ++k) {
+        g.dst[k] = (float*)s.in[4 + k];
+        g.sbias[k] = (const float*)s.in[8 + k];
+        g.Hs[k] = (int)s.i[25 + k];
+    }
+    g.hd = (int)s.i[29];
+    g.S = (int)s.i[30];
     return g;
 }
 
 // C[i] = alpha·Σ_ks W[ks][i] (MATMUL) or Σ_ks W[ks][i] + bias[i % N]
-// (MATMUL_ADD), summing the K ranges in increasing order.
+// (MATMUL_ADD), summing the K ranges in increasing order; then the fused
+// epilogue, if any (VEC only with no head scatter).
 template <bool HAS_BIAS, bool VEC>
-__global__ void splitk_reduce(const float* __restrict__ W, float* __restrict__ C, const float* __restrict__ bias,
-                              long long total, int N, int ksplit, float alpha) {
+__global__ void splitk_reduce(GemmArgs g, long long total) {
+    const float* __restrict__ W = g.W;
+    const int N = g.N, ksplit = g.ksplit;
     if (VEC) {
         const long long t4 = total / 4;
         for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < t4;
@@ -347,19 +448,26 @@ __global__ void splitk_reduce(const float* __restrict__ W, float* __restrict__ C
                 s.x += w.x; s.y += w.y; s.z += w.z; s.w += w.w;
             }
             if (HAS_BIAS) {
-                const float4 b = reinterpret_cast<const float4*>(bias)[(i * 4 % N) / 4];
+                const float4 b = reinterpret_cast<const float4*>(g.bias)[(i * 4 % N) / 4];
                 s.x += b.x; s.y += b.y; s.z += b.z; s.w += b.w;
             } else {
-                s.x *= alpha; s.y *= alpha; s.z *= alpha; s.w *= alpha;
+                s.x *= g.alpha; s.y *= g.alpha; s.z *= g.alpha; s.w *= g.alpha;
             }
-            reinterpret_cast<float4*>(C)[i] = s;
+            if (g.resid) {
+                const float4 r = reinterpret_cast<const float4*>(g.resid)[i];
+                s.x = s.x + r.x; s.y = s.y + r.y; s.z = s.z + r.z; s.w = s.w + r.w;
+            }
+            reinterpret_cast<float4*>(g.C)[i] = s;
         }
     } else {
+        const long long MN = (long long)g.M * N;
         for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
              i += (long long)gridDim.x * blockDim.x) {
             float s = W[i];
             for (int k = 1; k < ksplit; ++k) s += W[(long long)k * total + i];
-            C[i] = HAS_BIAS ? s + bias[i % N] : alpha * s;
+            s = HAS_BIAS ? s + g.bias[i % N] : g.alpha * s;
+            const long long bz = i / MN, r = i - bz * MN;
+            epi_store(g, bz, (int)(r / N), (int)(r % N), s);
         }
     }
 }
@@ -372,14 +480,12 @@ void launch_gemm_t(const Step& s, hipStream_t st) {
     hipLaunchKernelGGL((gemm_mfma_f32<TRANS_B, VEC, HAS_BIAS>), grid, dim3(NT), 0, st, g);
     if (g.ksplit > 1) {
         const long long total = (long long)g.M * g.N * s.i[3];
-        const bool v4 = s.i[12] != 0;
+        const bool v4 = s.i[12] != 0 && g.n_split == 0 && (!g.resid || lbr_aligned(g.resid, 16));
         const unsigned blocks = lbr_grid(v4 ? total / 4 : total, 256, 4096);
         if (v4)
-            hipLaunchKernelGGL((splitk_reduce<HAS_BIAS, true>), dim3(blocks), dim3(256), 0, st, g.W, g.C, g.bias,
-                               total, g.N, g.ksplit, g.alpha);
+            hipLaunchKernelGGL((splitk_reduce<HAS_BIAS, true>), dim3(blocks), dim3(256), 0, st, g, total);
         else
-            hipLaunchKernelGGL((splitk_reduce<HAS_BIAS, false>), dim3(blocks), dim3(256), 0, st, g.W, g.C, g.bias,
-                               total, g.N, g.ksplit, g.alpha);
+            hipLaunchKernelGGL((splitk_reduce<HAS_BIAS, false>), dim3(blocks), dim3(256), 0, st, g, total);
     }
 }
 
@@ -531,6 +637,7 @@ int decode_matmul(const OpNode* n, Step* s) {
         s->i[12] = (N % 4 == 0) && lbr_aligned(n->output, 16) && (!has_bias || lbr_aligned(n->inputs[2], 16));
         s->ws_bytes = ks > 1 ? (size_t)ks * batches * M * N * sizeof(float) : 0;
     }
+    s->i[13] = 1;   // MFMA path: takes the fused epilogues of Step::in[3..11], i[19..27]
     if (trans_b) {
         if (vec) s->run = has_bias ? launch_gemm_t<true, true, true> : launch_gemm_t<true, true, false>;
         else s->run = has_bias ? launch_gemm_t<true, false, true> : launch_gemm_t<true, false, false>;

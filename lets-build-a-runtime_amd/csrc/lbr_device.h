@@ -71,7 +71,9 @@ typedef void (*step_fn)(const Step&, hipStream_t);
 struct Step {
     step_fn run;
     const char* name;         // kernel name for reports
-    int node_index;
+    int node_index;           // first node this step executes
+    int n_nodes;              // nodes it covers (1, or the length of a fused run)
+    int fuse_kind;            // LBR_FUSE_* of a fused run
     const void* in[MAX_INPUTS];
     void* out;
     int n_in;

@@ -1,0 +1,39 @@
+// lbr_fusion.h — fused runs of consecutive OpNodes found at plan creation
+// (fusion.hip) and the decoded launch record that replaces each run.
+#pragma once
+
+#include <vector>
+
+#include "lbr_device.h"
+
+struct FusedRun {
+    int first = 0, count = 0, kind = LBR_FUSE_NONE;
+    // GEMM_HEADS: split k takes C columns [col_begin[k], col_begin[k] + width[k])
+    int n_split = 0;
+    int col_begin[5] = {0, 0, 0, 0, 0};
+    int width[4] = {0, 0, 0, 0};
+    const void* dst[4] = {nullptr, nullptr, nullptr, nullptr};
+    const void* sbias[4] = {nullptr, nullptr, nullptr, nullptr};   // [0] = HEAD_PROLOGUE bias
+    int Hs[4] = {0, 0, 0, 0};                                       // [0] = HEAD_PROLOGUE heads
+    int B = 0, S = 0, hd = 0;
+    // GEMM_RESID
+    const void* resid = nullptr;
+    const void* out = nullptr;
+    // HEAD_PROLOGUE
+    const void* src = nullptr;
+    long long ld = 0;
+    const void* norm_w = nullptr;
+    float eps = 0.f;
+    bool rope = false;
+    const void* cos = nullptr;
+    const void* sin = nullptr;
+    long long cst[3] = {0, 0, 0}, sst[3] = {0, 0, 0};
+};
+
+// Fusable runs of nodes[0..n) in stream order; live-out ranges are the
+// graph outputs the caller reads after the plan runs.
+int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, const size_t* live_bytes, int n_live,
+                     std::vector<FusedRun>* out);
+
+// Launch record of one fused run.
+int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s);

@@ -22,6 +22,7 @@ fallback: a missing library or GPU raises at compile.
 from __future__ import annotations
 
 import ctypes
+import os
 import time
 
 import numpy as np
@@ -29,7 +30,7 @@ import numpy as np
 from ..ir import Graph, OpType
 from ..planner import MemoryPlan
 from .common import Executor, OpTiming, RunProfile
-from .hip_lib import HipLibrary, load_library
+from .hip_lib import FUSE_KINDS, HipLibrary, live_arrays, load_library
 from .nodes import build_nodes, check_extents, dispatch_order
 
 _ALIGN = 256
@@ -82,9 +83,11 @@ class CompiledExecutor(Executor):
     """Plan → device OpNode array → hipGraph, replayed per run()."""
 
     def __init__(self, profile: bool = False, use_graph: bool = True, device: int = 0,
-                 weights: DeviceWeights | None = None) -> None:
+                 weights: DeviceWeights | None = None, fuse: bool | None = None) -> None:
         super().__init__(profile=profile)
         self._use_graph = use_graph
+        # peephole fusion in the device library (LBR_FUSE=0 turns it off)
+        self._fuse = os.environ.get("LBR_FUSE", "1") != "0" if fuse is None else fuse
         self._device = device
         self._lib: HipLibrary | None = None
         self._graph: Graph | None = None
@@ -162,9 +165,35 @@ class CompiledExecutor(Executor):
         self._nodes = arr
         self._order = order
         handle = ctypes.c_void_p()
-        lib.check(lib.lbr_plan_create(arr, len(order), 1 if self._use_graph else 0, ctypes.byref(handle)),
-                  "lbr_plan_create")
+        if self._fuse:
+            live = self.live_outs()
+            lp, lb = live_arrays(live)
+            lib.check(lib.lbr_plan_create_fused(arr, len(order), 1 if self._use_graph else 0, lp, lb, len(live),
+                                                ctypes.byref(handle)), "lbr_plan_create_fused")
+        else:
+            lib.check(lib.lbr_plan_create(arr, len(order), 1 if self._use_graph else 0, ctypes.byref(handle)),
+                      "lbr_plan_create")
         self._plan_handle = handle
+
+    def live_outs(self) -> list[tuple[int, int]]:
+        """(device address, bytes) of every graph output: what the caller reads after a launch."""
+        out = []
+        for name in self._graph.outputs:
+            t = self._graph.tensors[name]
+            out.append((self._addr[name], int(np.prod(t.shape)) * np.dtype(t.dtype).itemsize))
+        return out
+
+    def fused_runs(self) -> list[tuple[int, int, str]]:
+        """(first node, node count, kind) of every fused step of the compiled plan."""
+        runs = []
+        first, count, kind = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        for st in range(self._lib.lbr_plan_num_steps(self._plan_handle)):
+            self._lib.check(self._lib.lbr_plan_step_info(self._plan_handle, st, ctypes.byref(first),
+                                                         ctypes.byref(count), ctypes.byref(kind)),
+                            "lbr_plan_step_info")
+            if count.value > 1:
+                runs.append((first.value, count.value, FUSE_KINDS.get(kind.value, "?")))
+        return runs
 
     # ------------------------------------------------------------------ run
     def _upload_inputs(self, inputs: dict[str, np.ndarray]) -> None:

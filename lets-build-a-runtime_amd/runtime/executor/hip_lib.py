@@ -30,6 +30,14 @@ def library_path() -> Path:
     return Path(os.environ.get("LBR_EXECUTOR_LIB", _DEFAULT_LIB))
 
 
+class LbrWindow(ctypes.Structure):
+    """lbr_window: one fused run of consecutive nodes."""
+    _fields_ = [("first", ctypes.c_int), ("count", ctypes.c_int), ("kind", ctypes.c_int)]
+
+
+FUSE_KINDS = {0: "none", 1: "gemm_resid", 2: "gemm_heads", 3: "head_prologue"}
+
+
 class HipLibrary:
     """Loaded device library with typed entry points."""
 
@@ -59,6 +67,11 @@ class HipLibrary:
             "lbr_plan_time": ([c_vp, c_int, P(ctypes.c_float)], c_int),
             "lbr_plan_profile": ([c_vp, c_int, P(ctypes.c_float), c_int], c_int),
             "lbr_plan_node_kernel": ([c_vp, c_int, ctypes.c_char_p, c_int], c_int),
+            "lbr_fusion_windows": ([P(COpNode), c_int, P(c_vp), P(c_size), c_int, P(LbrWindow), c_int, P(c_int)],
+                                   c_int),
+            "lbr_plan_create_fused": ([P(COpNode), c_int, c_int, P(c_vp), P(c_size), c_int, P(c_vp)], c_int),
+            "lbr_plan_num_steps": ([c_vp], c_int),
+            "lbr_plan_step_info": ([c_vp, c_int, P(c_int), P(c_int), P(c_int)], c_int),
         }
         for name, (args, res) in sig.items():
             fn = getattr(lib, name)
@@ -97,11 +110,30 @@ class HipLibrary:
         self.check(self._lib.lbr_memcpy_d2h(ctypes.c_void_p(dst_ptr), ctypes.c_void_p(src), nbytes), "memcpy D2H")
 
 
+    def fusion_windows(self, nodes, n: int, live: list[tuple[int, int]]) -> list[tuple[int, int, str]]:
+        """(first, count, kind) of every run lbr_plan_create_fused would fuse; needs no device."""
+        lp, lb = live_arrays(live)
+        cap = max(n, 1)
+        out = (LbrWindow * cap)()
+        n_out = ctypes.c_int(0)
+        self.check(self._lib.lbr_fusion_windows(nodes, n, lp, lb, len(live), out, cap, ctypes.byref(n_out)),
+                   "lbr_fusion_windows")
+        return [(out[k].first, out[k].count, FUSE_KINDS.get(out[k].kind, "?")) for k in range(n_out.value)]
+
+
+def live_arrays(live: list[tuple[int, int]]):
+    """ctypes (pointer, byte count) arrays of live-out ranges."""
+    n = max(len(live), 1)
+    lp = (ctypes.c_void_p * n)(*[ctypes.c_void_p(p) for p, _ in live])
+    lb = (ctypes.c_size_t * n)(*[b for _, b in live])
+    return lp, lb
+
+
 _LIB: HipLibrary | None = None
 
 
-def load_library(device: int = 0) -> HipLibrary:
-    """Load (once) and initialise the device library; raises if it is absent or no gfx950 GPU is usable."""
+def open_library() -> HipLibrary:
+    """Load (once) the device library without touching a device."""
     global _LIB
     if _LIB is None:
         path = library_path()
@@ -109,8 +141,14 @@ def load_library(device: int = 0) -> HipLibrary:
             raise RuntimeError(f"HIP executor library not found at {path} — build it with "
                                "lets-build-a-runtime_amd/build_native.py first")
         _LIB = HipLibrary(path)
-    _LIB.check(_LIB.lbr_init(device), f"lbr_init({device})")
     return _LIB
+
+
+def load_library(device: int = 0) -> HipLibrary:
+    """Load (once) and initialise the device library; raises if it is absent or no gfx950 GPU is usable."""
+    lib = open_library()
+    lib.check(lib.lbr_init(device), f"lbr_init({device})")
+    return lib
 
 
 def loaded_library() -> HipLibrary | None:

@@ -1,0 +1,247 @@
+"""Peephole fusion matcher (lbr_fusion_windows) on the CPU: no device is
+touched, node pointers are fake addresses that are only compared.
+
+* the runs found on each BASELINE workload's real node stream (planner
+  offsets at S=64), and
+* every refusal rule on hand-built node arrays: a final output over memory
+  the fused kernel reads, an intermediate read later, an intermediate inside
+  a live-out range — each built so that the same array without the hazard
+  does fuse.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections import Counter
+
+import numpy as np
+import pytest
+
+from runtime.executor.common import COpNode
+from runtime.executor.hip_lib import open_library
+from runtime.ir import OpType
+
+ARENA, EXT = 1 << 40, 1 << 44
+
+
+def _lib():
+    try:
+        return open_library()
+    except RuntimeError as e:
+        pytest.skip(str(e))
+
+
+def _workload_nodes(key: str, seq: int):
+    from runtime.executor.nodes import build_nodes
+    from runtime.passes import run_pipeline
+    from runtime.planner import plan
+    from workloads import export_workload
+    _, _, g = export_workload(key, seq_len=seq)
+    run_pipeline(g, None)
+    mem = plan(g)
+    ext: dict[str, int] = {}
+
+    def addr(name):
+        if name in mem.offsets and name not in g.inputs and name not in g.constants:
+            return ARENA + mem.offsets[name]
+        if name not in ext:
+            ext[name] = EXT + len(ext) * (1 << 32)
+        return ext[name]
+
+    arr, order = build_nodes(mem, addr, lambda off, size: ARENA + off)
+    live = [(addr(n), int(np.prod(g.tensors[n].shape)) * 4) for n in g.outputs]
+    return arr, order, live
+
+
+EXPECTED = {
+    # merged QKV → three (slice, bias add, transpose) chains in the GEMM epilogue; the O-proj residual
+    # add writes over the GEMM's own A input (refused), the FFN2 one fuses
+    "toy": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1}),
+    "gpt2w": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1}),
+    "7b4k": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1}),
+    # c_attn is MATMUL_ADD (bias already in the GEMM): three (slice, transpose) chains per layer
+    "gpt2": Counter({("gemm_heads", 7): 2, ("gemm_resid", 2): 4}),
+    # q/k: slice → per-head RMSNorm → transpose → 7-node RoPE as one kernel; v's transpose lands
+    # over the QKV rows it reads at this size (refused)
+    "qwen3_4b": Counter({("head_prologue", 10): 4, ("gemm_resid", 2): 4}),
+}
+
+
+@pytest.mark.parametrize("key", list(EXPECTED))
+def test_workload_fusion_windows(key):
+    lib = _lib()
+    arr, order, live = _workload_nodes(key, 64)
+    wins = lib.fusion_windows(arr, len(order), live)
+    assert Counter((kind, count) for _, count, kind in wins) == EXPECTED[key]
+    # runs are disjoint, in order, inside the array
+    end = 0
+    for first, count, _ in wins:
+        assert first >= end and first + count <= len(order)
+        end = first + count
+    # no live-out declared → intermediates that are graph outputs are unknown; with an
+    # explicit empty list fusion still runs (the caller asserts nothing is read back)
+    assert len(lib.fusion_windows(arr, len(order), [])) >= len(wins)
+
+
+# ------------------------------------------------------------ hand-built arrays
+
+def _node(op, inputs, output, shape, extra=()):
+    n = COpNode()
+    n.op = op.value
+    n.n_inputs = len(inputs)
+    for i, p in enumerate(inputs):
+        n.inputs[i] = p
+    n.output = output
+    n.n_dims = len(shape)
+    for i, d in enumerate(shape):
+        n.out_shape[i] = d
+    n.elem_size = 4
+    for i, e in enumerate(extra):
+        n.extra[i] = e
+    return n
+
+
+def _array(nodes):
+    arr = (COpNode * len(nodes))()
+    for i, n in enumerate(nodes):
+        arr[i] = n
+    return arr
+
+
+M, K, N = 256, 128, 384          # GEMM rows, depth, columns
+A_, W_, R_ = EXT, EXT + (1 << 32), EXT + (2 << 32)
+MB = 1 << 20
+
+
+def _gemm_resid(c_off, y_off, a_ptr=A_, later=()):
+    """MATMUL A·Wᵀ → C, ADD(C, R) → Y, then `later` nodes."""
+    mm = _node(OpType.MATMUL, [a_ptr, W_], ARENA + c_off, (1, M, N), (K, 1, 1, 0))
+    ad = _node(OpType.ADD, [ARENA + c_off, R_], ARENA + y_off, (1, M, N), (1,))
+    return [mm, ad, *later]
+
+
+def _windows(nodes, live=()):
+    lib = _lib()
+    arr = _array(nodes)
+    return lib.fusion_windows(arr, len(nodes), list(live))
+
+
+def test_gemm_resid_fuses():
+    assert _windows(_gemm_resid(0, 4 * MB)) == [(0, 2, "gemm_resid")]
+    # Y over the dead C is fine: C is never written
+    assert _windows(_gemm_resid(0, 0)) == [(0, 2, "gemm_resid")]
+
+
+def test_gemm_resid_refuses_output_over_gemm_input():
+    # the GEMM reads A while other workgroups would already write Y over it
+    assert _windows(_gemm_resid(0, 4 * MB, a_ptr=ARENA + 4 * MB)) == []
+
+
+def test_gemm_resid_refuses_live_intermediate():
+    c_off = 0
+    reader = _node(OpType.RELU, [ARENA + c_off + 64], ARENA + 16 * MB, (16,))
+    assert _windows(_gemm_resid(c_off, 4 * MB, later=[reader])) == []
+    # ... unless the memory was overwritten before that read
+    writer = _node(OpType.RELU, [R_], ARENA + c_off, (1, M, N))
+    assert _windows(_gemm_resid(c_off, 4 * MB, later=[writer, reader])) == [(0, 2, "gemm_resid")]
+
+
+def test_gemm_resid_refuses_intermediate_in_live_out():
+    nodes = _gemm_resid(0, 4 * MB)
+    assert _windows(nodes, live=[(ARENA + 8, 4)]) == []
+    assert _windows(nodes, live=[(ARENA + 4 * MB, M * N * 4)]) == [(0, 2, "gemm_resid")]
+
+
+def _qkv(c_off, outs, heads=(4, 4, 4), hd=32, S=M, bias=True):
+    """MATMUL → C [1,S,Σ heads·hd]; per split: SLICE → [ADD bias] → TRANSPOSE(S,H)."""
+    width = [h * hd for h in heads]
+    ncol = sum(width)
+    nodes = [_node(OpType.MATMUL, [A_, W_], ARENA + c_off, (1, S, ncol), (K, 1, 1, 0))]
+    col = 0
+    for k, (h, w) in enumerate(zip(heads, width)):
+        tmp = ARENA + 32 * MB + k * MB
+        nodes.append(_node(OpType.SLICE, [ARENA + c_off], tmp, (1, S, w), (S, ncol, col, w, 1)))
+        src = tmp
+        if bias:
+            nodes.append(_node(OpType.ADD, [tmp, EXT + (3 + k << 32)], tmp, (1, S, w), (0,)))
+        nodes.append(_node(OpType.TRANSPOSE, [src], ARENA + outs[k], (1, h, S, hd), (1, S, 1, h, hd)))
+        col += w
+    return nodes
+
+
+def test_gemm_heads_fuses_with_gqa_splits():
+    nodes = _qkv(0, [8 * MB, 9 * MB, 10 * MB], heads=(8, 2, 2))
+    assert _windows(nodes) == [(0, 10, "gemm_heads")]
+    # an output inside the dead C is fine for the epilogue form (C is never written)
+    nodes = _qkv(0, [8 * MB, 9 * MB, 0], heads=(8, 2, 2), bias=False)
+    assert _windows(nodes) == [(0, 7, "gemm_heads")]
+
+
+def test_gemm_heads_refuses_when_C_is_read_later():
+    nodes = _qkv(0, [8 * MB, 9 * MB, 10 * MB])
+    nodes.append(_node(OpType.RELU, [ARENA + 4], ARENA + 40 * MB, (8,)))
+    wins = _windows(nodes)
+    assert all(kind != "gemm_heads" for _, _, kind in wins)
+
+
+def _rope_chain(src_off, out_off, S=64, H=4, hd=128, norm=True, rope=True):
+    """SLICE(C) → [RMSNORM] → TRANSPOSE → [RoPE 7 nodes] over C [1, S, H·hd + 64]."""
+    ld = H * hd + 64
+    C = ARENA + src_off
+    t = [ARENA + 40 * MB + k * MB for k in range(12)]
+    nodes = [_node(OpType.SLICE, [C], t[0], (1, S, H * hd), (S, ld, 0, H * hd, 1))]
+    cur = t[0]
+    if norm:
+        nodes.append(_node(OpType.RMSNORM, [cur, EXT + (5 << 32)], t[1], (1, S, H, hd), (0x358637BD,)))
+        cur = t[1]
+    nodes.append(_node(OpType.TRANSPOSE, [cur], t[2] if rope else ARENA + out_off, (1, H, S, hd),
+                       (1, S, 1, H, hd)))
+    if not rope:
+        return nodes
+    x = t[2]
+    cos, sin = EXT + (6 << 32), EXT + (7 << 32)
+    half = hd // 2
+    bc = (2, 4, 0, S * hd, hd, 1, 0, 0, hd, 1, 1, H, S, hd)
+    rows = H * S
+    nodes += [
+        _node(OpType.MUL, [x, cos], t[3], (1, H, S, hd), bc),
+        _node(OpType.SLICE, [x], t[4], (1, H, S, half), (rows, hd, 0, half, 1)),
+        _node(OpType.SLICE, [x], t[5], (1, H, S, half), (rows, hd, half, half, 1)),
+        _node(OpType.NEG, [t[5]], t[5], (1, H, S, half)),
+        _node(OpType.CAT, [t[5], t[4]], t[6], (1, H, S, hd), (3, half, half)),
+        _node(OpType.MUL, [t[6], sin], t[6], (1, H, S, hd), bc),
+        _node(OpType.ADD, [t[3], t[6]], ARENA + out_off, (1, H, S, hd), (1,)),
+    ]
+    return nodes
+
+
+def test_head_prologue_fuses_norm_and_rope():
+    assert _windows(_rope_chain(0, 8 * MB)) == [(0, 10, "head_prologue")]
+    assert _windows(_rope_chain(0, 8 * MB, norm=False)) == [(0, 9, "head_prologue")]
+    assert _windows(_rope_chain(0, 8 * MB, rope=False)) == [(0, 3, "head_prologue")]
+
+
+def test_head_prologue_refuses_output_over_its_source():
+    # out overlaps the rows of C the kernel reads (different index map)
+    assert _windows(_rope_chain(0, 4096)) == []
+
+
+def test_head_prologue_refuses_when_an_intermediate_is_read():
+    nodes = _rope_chain(0, 8 * MB)
+    # a later reader of the transposed (pre-RoPE) tensor keeps it live
+    nodes.append(_node(OpType.RELU, [ARENA + 42 * MB], ARENA + 60 * MB, (8,)))
+    assert _windows(nodes) == []
+
+
+def test_rope_tables_take_any_broadcast_strides():
+    # a sin table that also varies along heads is still RoPE: the kernel indexes it by strides
+    nodes = _rope_chain(0, 8 * MB)
+    nodes[8].extra[7] = 64 * 128
+    assert _windows(nodes) == [(0, 10, "head_prologue")]
+
+
+def test_not_rotate_half_is_not_rope():
+    # cat(x1, −x2) is not rotate_half: the chain stops at the transpose
+    nodes = _rope_chain(0, 8 * MB)
+    nodes[7].inputs[0], nodes[7].inputs[1] = nodes[7].inputs[1], nodes[7].inputs[0]
+    assert _windows(nodes) == [(0, 3, "head_prologue")]

@@ -46,6 +46,42 @@ def test_workload_parity(key, seq):
     assert e_go <= TOL
 
 
+@pytest.mark.parametrize("key,seq,kinds", [
+    ("toy", None, {"gemm_heads", "gemm_resid"}),
+    ("gpt2", None, {"gemm_heads", "gemm_resid"}),
+    ("qwen3_4b", None, {"head_prologue", "gemm_resid"}),
+    ("7b4k", 256, {"gemm_heads", "gemm_resid"}),
+])
+def test_fused_plan_matches_unfused(monkeypatch, key, seq, kinds):
+    """Peephole fusion changes launches, not results: the fused plan's outputs equal the
+    one-kernel-per-node plan's up to the RMSNorm sum order (GEMM epilogues and RoPE keep
+    every rounding step), and the expected runs were fused."""
+    import copy
+    from workloads import export_workload
+    from runtime.session import Session
+    _, x, graph = export_workload(key, seq_len=seq)
+    g2 = copy.deepcopy(graph)
+    fused = Session(graph)
+    fused.create()
+    runs = fused.executor.fused_runs()
+    print(key, [(f, c, k) for f, c, k in runs])
+    assert kinds <= {k for _, _, k in runs}
+    y = fused.run({graph.inputs[0]: x})[graph.outputs[0]]
+    fused.close()
+    monkeypatch.setenv("LBR_FUSE", "0")
+    plain = Session(g2)
+    plain.create()
+    assert plain.executor.fused_runs() == []
+    z = plain.run({g2.inputs[0]: x})[g2.outputs[0]]
+    plain.close()
+    e = normwise_rel(y, z)
+    print(f"{key}: fused-vs-unfused rel {e:.2e} abs {np.abs(y - z).max():.2e}")
+    if "head_prologue" in kinds:
+        assert e <= 1e-5
+    else:
+        np.testing.assert_array_equal(y, z)
+
+
 def test_graph_replay_matches_eager_and_reruns():
     """hipGraph replay == eager launches, and repeated runs with new inputs stay correct."""
     from workloads import export_workload, WORKLOADS
