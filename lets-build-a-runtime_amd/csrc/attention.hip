@@ -31,6 +31,8 @@
 #include <float.h>
 #include <math.h>
 
+#include <algorithm>
+
 namespace {
 
 constexpr int AT_NT = 256;       // 4 waves
@@ -47,6 +49,11 @@ struct AttnArgs {
     int S, D, group_size, n_qblocks;
     float scale_log2;            // (1/√hd)·log2(e)
     int fold;                    // causal: workgroup j also runs query block j (16x16 kernel)
+    int ch, n_items;             // key-range split (16x16 kernel): tiles per chunk, work items per head
+    int n_bh;                    // heads × batch (split: the grid is 1-D)
+    float* part;                 // split partials Σ p·V: [bh][n_items][128 rows][D]
+    float* ml;                   // split running max and Σ p: [bh][n_items][128 rows][2]
+    int* queue;                  // split work counter, reset before every launch
 };
 
 // One K/V tile (AT_KB keys × DP) staged through registers: thread t holds the
@@ -244,11 +251,20 @@ constexpr int A16_NT = 512;      // 8 waves
 constexpr int A16_QB = 128;      // query rows per workgroup (16 per wave)
 constexpr int A16_KB = 32;       // keys per tile
 
-// One 128-row query block of one head: streams the key tiles it needs
-// through Ks/Vs and writes its output rows.
-template <int DP, bool CAUSAL, bool HAS_MASK>
-__device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int qblk, float (*Ks)[DP + 4],
-                                              float (*Vs)[DP + 4]) {
+// Key tiles query block `qblk` needs: all of them, or (causal) up to the one
+// holding its last row's diagonal.
+__device__ __forceinline__ int attn16_tiles(const AttnArgs& g, int qblk, bool causal) {
+    const int nt = (g.S + A16_KB - 1) / A16_KB;
+    return causal ? min(nt, min(g.S - 1, qblk * A16_QB + A16_QB - 1) / A16_KB + 1) : nt;
+}
+
+// One 128-row query block of one head over key tiles [t0, t1): streams them
+// through Ks/Vs.  slot < 0: the range is the whole row, write O.  slot >= 0:
+// write the unnormalised partial (Σ p·V, running max m, Σ p) of this key
+// range to the split workspace for attn_split_merge.
+template <int DP, bool CAUSAL, bool HAS_MASK, bool SPLIT>
+__device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qblk, int t0_, int t1, long long slot,
+                                              float (*Ks)[DP + 4], float (*Vs)[DP + 4]) {
     constexpr int NCH = DP / 16;     // 16-wide d chunks (S reduction) and d blocks (O)
     constexpr int W = NCH < 4 ? NCH : 4;
     typedef float VW __attribute__((ext_vector_type(W)));
@@ -257,7 +273,9 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int qblk, float
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
-    const long long bh = blockIdx.y;
+    // without a split the head is the grid's y index and the range starts at tile 0
+    const long long bh = SPLIT ? (long long)bhi : (long long)blockIdx.y;
+    const int t0 = SPLIT ? t0_ : 0;
     const long long kvh = bh / g.group_size;
     const int S = g.S, D = g.D;
     const float* __restrict__ Qb = g.Q + bh * (long long)S * D;
@@ -286,9 +304,6 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int qblk, float
     for (int b = 0; b < NCH; ++b) oacc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
     float m_run = -FLT_MAX, l_run = 0.f;
 
-    int n_tiles = (S + A16_KB - 1) / A16_KB;
-    if (CAUSAL) n_tiles = min(n_tiles, min(S - 1, qblk * A16_QB + A16_QB - 1) / A16_KB + 1);
-
     float4 kr[PER], vr[PER];
     auto load = [&](int k0) {
 #pragma unroll
@@ -313,13 +328,13 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int qblk, float
         }
     };
 
-    load(0);
+    load(t0 * A16_KB);
     store();
     __syncthreads();
 
-    for (int kt = 0; kt < n_tiles; ++kt) {
+    for (int kt = t0; kt < t1; ++kt) {
         const int k0 = kt * A16_KB;
-        if (kt + 1 < n_tiles) load(k0 + A16_KB);
+        if (kt + 1 < t1) load(k0 + A16_KB);
 
         if (!CAUSAL || k0 <= q_wave0 + 15) {
             // Sᵀ for two 16-key blocks; register r of block b = key k0 + 16b + 4g + r
@@ -385,7 +400,7 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int qblk, float
                 }
         }
         __syncthreads();
-        if (kt + 1 < n_tiles) {
+        if (kt + 1 < t1) {
             store();
             __syncthreads();
         }
@@ -394,8 +409,14 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int qblk, float
     // O[q][d] = Oᵀ[d][q] / l; register r of block W·h + w holds row i = 4g + r,
     // i.e. d = 16W·h + W·(4g + r) + w: W consecutive floats per (h, r)
     if (q < S) {
-        const float inv_l = 1.0f / l_run;
-        float* __restrict__ Ob = g.O + bh * (long long)S * D + (long long)q * D;
+        const bool part = SPLIT && slot >= 0;
+        const long long prow = slot * A16_QB + (q - qblk * A16_QB);   // partial row in the workspace
+        const float inv_l = part ? 1.0f : 1.0f / l_run;
+        float* __restrict__ Ob = part ? g.part + prow * D : g.O + bh * (long long)S * D + (long long)q * D;
+        if (part && lg == 0) {
+            g.ml[2 * prow] = m_run;
+            g.ml[2 * prow + 1] = l_run;
+        }
 #pragma unroll
         for (int h = 0; h < NCH / W; ++h)
 #pragma unroll
@@ -416,20 +437,106 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int qblk, float
 // one-block-per-workgroup grid leaves some CUs with only the longest blocks.
 // With g.fold set, workgroup j runs block n-1-j and then block j: every
 // workgroup carries the same number of key tiles.
+//
+// Key-range split (g.ch > 0, small grids): work item = (query block q, chunk
+// c of g.ch key tiles), numbered q = n-1 .. 0 (heaviest first); a persistent
+// grid takes (item, head) pairs from the counter g.queue in the order item,
+// then head, so every CU stays busy until the last chunk.  Blocks with one
+// chunk write O; the others write partials to slot (head, item).  Every
+// workgroup leaves the loop once the counter passes the last pair.
 template <int DP, bool CAUSAL, bool HAS_MASK>
 __global__ __launch_bounds__(A16_NT, 4) void attn_fwd_mfma16(AttnArgs g) {
     __shared__ float Ks[A16_KB][DP + 4];
     __shared__ float Vs[A16_KB][DP + 4];
     const int j = blockIdx.x, last = g.n_qblocks - 1 - j;
     if (!CAUSAL) {
-        attn16_qblock<DP, CAUSAL, HAS_MASK>(g, j, Ks, Vs);
+        attn16_qblock<DP, CAUSAL, HAS_MASK, false>(g, 0, j, 0, attn16_tiles(g, j, false), -1, Ks, Vs);
         return;
     }
-    attn16_qblock<DP, CAUSAL, HAS_MASK>(g, last, Ks, Vs);
-    if (g.fold && j < last) {
+    attn16_qblock<DP, CAUSAL, HAS_MASK, false>(g, 0, last, 0, attn16_tiles(g, last, true), -1, Ks, Vs);
+    if (g.fold && j < last) {   // folded second block: query block j
         __syncthreads();
-        attn16_qblock<DP, CAUSAL, HAS_MASK>(g, j, Ks, Vs);
+        attn16_qblock<DP, CAUSAL, HAS_MASK, false>(g, 0, j, 0, attn16_tiles(g, j, true), -1, Ks, Vs);
     }
+}
+
+template <int DP, bool CAUSAL, bool HAS_MASK>
+__global__ __launch_bounds__(A16_NT, 4) void attn_fwd_mfma16_split(AttnArgs g) {
+    __shared__ float Ks[A16_KB][DP + 4];
+    __shared__ float Vs[A16_KB][DP + 4];
+    __shared__ int next_work;
+    const long long total = (long long)g.n_items * g.n_bh;
+    for (;;) {
+        if (threadIdx.x == 0) next_work = atomicAdd(g.queue, 1);
+        __syncthreads();
+        const long long idx = next_work;
+        __syncthreads();
+        if (idx >= total) break;
+        int item = (int)(idx / g.n_bh);
+        const int bhi = (int)(idx - (long long)item * g.n_bh);
+        const int it0 = item;
+        int qb = g.n_qblocks - 1;
+        for (; qb > 0; --qb) {
+            const int nc = (attn16_tiles(g, qb, CAUSAL) + g.ch - 1) / g.ch;
+            if (item < nc) break;
+            item -= nc;
+        }
+        const int nt = attn16_tiles(g, qb, CAUSAL);
+        const int nc = (nt + g.ch - 1) / g.ch;
+        const int t0 = item * g.ch, t1 = min(nt, t0 + g.ch);
+        const long long slot = nc > 1 ? (long long)bhi * g.n_items + it0 : -1;
+        attn16_qblock<DP, CAUSAL, HAS_MASK, true>(g, bhi, qb, t0, t1, slot, Ks, Vs);
+    }
+}
+
+__global__ void attn_queue_reset(int* queue) {
+    if (threadIdx.x == 0) *queue = 0;
+}
+
+// Combine the key-range partials of every query row whose block was split:
+// O = Σ_c 2^(m_c − M)·acc_c / Σ_c 2^(m_c − M)·l_c, M = max_c m_c, chunks
+// summed in order.  One wavefront per row; rows of unsplit blocks return.
+// Thread t of a row handles d = 4t .. 4t+3 (D % 4 == 0 on this path), so a
+// row of hd = 128 takes 32 threads and every load and store is a float4.
+__global__ __launch_bounds__(256) void attn_split_merge(AttnArgs g, int causal) {
+    const int tpr = g.D / 4;                                    // threads per row
+    const long long t = blockIdx.x * 256LL + threadIdx.x;
+    const long long row = t / tpr;
+    const int d = (int)(t - row * tpr) * 4;
+    const long long bh = blockIdx.y;
+    if (row >= g.S) return;
+    const int qb = (int)(row / A16_QB);
+    int first = 0, nc = 0;
+    for (int b = g.n_qblocks - 1; b >= 0; --b) {
+        const int n = (attn16_tiles(g, b, causal != 0) + g.ch - 1) / g.ch;
+        if (b == qb) {
+            nc = n;
+            break;
+        }
+        first += n;
+    }
+    if (nc <= 1) return;
+    const long long r0 = (bh * g.n_items + first) * A16_QB + (row - (long long)qb * A16_QB);
+    float M = -FLT_MAX;
+    for (int c = 0; c < nc; ++c) M = fmaxf(M, g.ml[2 * (r0 + (long long)c * A16_QB)]);
+    float L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int c = 0; c < nc; ++c) {
+        const long long pr = r0 + (long long)c * A16_QB;
+        const float w = __builtin_amdgcn_exp2f(g.ml[2 * pr] - M);
+        L += w * g.ml[2 * pr + 1];
+        const float4 p = *reinterpret_cast<const float4*>(g.part + pr * g.D + d);
+        acc.x += w * p.x;
+        acc.y += w * p.y;
+        acc.z += w * p.z;
+        acc.w += w * p.w;
+    }
+    const float inv_l = 1.0f / L;
+    acc.x *= inv_l;
+    acc.y *= inv_l;
+    acc.z *= inv_l;
+    acc.w *= inv_l;
+    *reinterpret_cast<float4*>(g.O + (bh * g.S + row) * (long long)g.D + d) = acc;
 }
 
 // Fallback for head dims the MFMA kernel does not take (hd % 8 != 0 or
@@ -473,6 +580,7 @@ __global__ __launch_bounds__(256) void attn_fwd_rows(AttnArgs g, int causal) {
 }
 
 // Step::i: [0]=bh [1]=S [2]=D [3]=causal [4]=group [5]=DP (0 = row fallback)
+//          [6]=fold [7]=split chunk tiles (0 = none) [8]=split work items per head
 AttnArgs make_args(const Step& s) {
     AttnArgs g;
     g.Q = (const float*)s.in[0];
@@ -510,8 +618,39 @@ void launch_attn16(const Step& s, hipStream_t st) {
     if (g.S <= 0 || s.i[0] <= 0) return;
     g.n_qblocks = (g.S + A16_QB - 1) / A16_QB;
     g.fold = CAUSAL && s.i[6] != 0;
+    g.ch = (int)s.i[7];
+    g.n_items = (int)s.i[8];
+    g.n_bh = (int)s.i[0];
+    if (g.ch > 0) {
+        // workspace: partials, then (m, l) pairs, then the work counter
+        const long long rows = (long long)g.n_items * s.i[0] * A16_QB;
+        g.part = (float*)s.ws;
+        g.ml = g.part + rows * g.D;
+        g.queue = (int*)(g.ml + rows * 2);
+        const long long total = (long long)g.n_items * s.i[0];
+        const long long slots = 2LL * (lbr_device_cus() > 0 ? lbr_device_cus() : 256);
+        hipLaunchKernelGGL(attn_queue_reset, dim3(1), dim3(64), 0, st, g.queue);
+        hipLaunchKernelGGL((attn_fwd_mfma16_split<DP, CAUSAL, HAS_MASK>), dim3((unsigned)std::min(total, slots), 1),
+                           dim3(A16_NT), 0, st, g);
+        hipLaunchKernelGGL(attn_split_merge, dim3((unsigned)(((long long)g.S * (g.D / 4) + 255) / 256), (unsigned)s.i[0]),
+                           dim3(256), 0, st, g, (int)CAUSAL);
+        return;
+    }
+    g.part = g.ml = nullptr;
+    g.queue = nullptr;
     const unsigned gx = g.fold ? (unsigned)(g.n_qblocks + 1) / 2 : (unsigned)g.n_qblocks;
     hipLaunchKernelGGL((attn_fwd_mfma16<DP, CAUSAL, HAS_MASK>), dim3(gx, (unsigned)s.i[0]), dim3(A16_NT), 0, st, g);
+}
+
+// Work items of a key-range split with `ch` tiles per chunk (one head).
+long long attn16_items(int S, bool causal, int ch) {
+    const int nt = (S + A16_KB - 1) / A16_KB, nq = (S + A16_QB - 1) / A16_QB;
+    long long items = 0;
+    for (int q = 0; q < nq; ++q) {
+        const int t = causal ? std::min(nt, std::min(S - 1, q * A16_QB + A16_QB - 1) / A16_KB + 1) : nt;
+        items += (t + ch - 1) / ch;
+    }
+    return items;
 }
 
 template <int DP>
@@ -577,6 +716,27 @@ int decode_attention(const OpNode* n, Step* s) {
             s->i[6] = causal && (nq + 1) / 2 * bh >= cus;
             const char* fold = getenv("LBR_ATTN_FOLD");
             if (fold) s->i[6] = causal && atoi(fold) != 0;
+            // Grids that leave CUs idle (fewer than two 8-wavefront workgroups per
+            // CU, not folded) split each query block's key range into chunks of
+            // 8 tiles (256 keys; 4 when that still leaves fewer work items than
+            // CUs), fed to a persistent grid through a work counter, when that
+            // gives at least half again as many work items as blocks.  Measured
+            // on Qwen3 and GPT-2 S=1024, 8 beat 1, 2, 4 and 16: smaller chunks
+            // pay the per-item Q load, first-tile latency and larger partials.
+            // LBR_ATTN_SPLIT=<ch> forces a chunk size (0: no split).
+            int ch = 0;
+            if (!s->i[6] && nq * bh < 2LL * cus) {
+                const int c = attn16_items(seq, causal, 8) * bh >= cus ? 8 : 4;
+                if (attn16_items(seq, causal, c) * 2 >= 3 * nq) ch = c;
+            }
+            const char* split = getenv("LBR_ATTN_SPLIT");
+            if (split) ch = std::max(0, atoi(split));
+            if (ch > 0 && !s->i[6]) {
+                const long long items = attn16_items(seq, causal, ch);
+                s->i[7] = ch;
+                s->i[8] = items;
+                s->ws_bytes = (size_t)(items * bh * A16_QB) * (size_t)(hd + 2) * sizeof(float) + 256;
+            }
             switch (dp) {
                 case 32: s->run = pick16<32>(causal, has_mask); break;
                 case 64: s->run = pick16<64>(causal, has_mask); break;

@@ -127,8 +127,15 @@ def test_attention(B, H, S, hd, causal, group):
 
 # Kernel-selection overrides read when the plan is built: LBR_ATTN_FOLD=1
 # forces the paired causal schedule (workgroup j runs query blocks n-1-j and
-# j; odd n leaves the middle block alone), LBR_ATTN_TILE=32 the 32x32 kernel.
-@pytest.mark.parametrize("env", [{"LBR_ATTN_FOLD": "1"}, {"LBR_ATTN_TILE": "32"}], ids=["fold", "tile32"])
+# j; odd n leaves the middle block alone), LBR_ATTN_TILE=32 the 32x32 kernel,
+# LBR_ATTN_SPLIT=c the key-range split with c tiles (32 keys) per chunk plus
+# the merge kernel (c=1: every tile its own chunk; c=3: chunks that do not
+# divide a block's tile count).
+@pytest.mark.parametrize("env", [{"LBR_ATTN_FOLD": "1"}, {"LBR_ATTN_TILE": "32"},
+                                 {"LBR_ATTN_SPLIT": "1", "LBR_ATTN_FOLD": "0"},
+                                 {"LBR_ATTN_SPLIT": "3", "LBR_ATTN_FOLD": "0"},
+                                 {"LBR_ATTN_SPLIT": "8", "LBR_ATTN_FOLD": "0"}],
+                         ids=["fold", "tile32", "split1", "split3", "split8"])
 @pytest.mark.parametrize("B,H,S,hd,causal,group", [
     (1, 4, 257, 128, True, 1),      # 3 query blocks: pair (2, 0) and the middle block 1 alone
     (1, 8, 512, 64, True, 2),       # 4 query blocks: pairs (3, 0), (2, 1)
@@ -142,7 +149,9 @@ def test_attention_schedules(monkeypatch, env, B, H, S, hd, causal, group):
 
 
 @pytest.mark.parametrize("S", [16, 300])
-def test_attention_mask(S):
+@pytest.mark.parametrize("split", ["0", "2"])
+def test_attention_mask(monkeypatch, S, split):
+    monkeypatch.setenv("LBR_ATTN_SPLIT", split)
     r = rng(S)
     B, H, hd = 1, 2, 64
     q, k, v = randn(r, B, H, S, hd), randn(r, B, H, S, hd), randn(r, B, H, S, hd)
