@@ -161,6 +161,8 @@ int lbr_plan_node_kernel(const lbr_plan* plan, int index, char* name_out,
                                      the epilogue writes each column range as [B, H, S, hd]     */
 #define LBR_FUSE_HEAD_PROLOGUE 3  /* SLICE → [ADD bias] → [RMSNORM] → TRANSPOSE(S,H) → [RoPE]
                                      (7-node rotate-half window) as one kernel                  */
+#define LBR_FUSE_ATTN_TRANSPOSE 4 /* ATTENTION → TRANSPOSE(H,S): the attention kernel writes
+                                     its output as [B, S, H, hd]                                */
 
 typedef struct {
     int first;   /* index of the run's first node */

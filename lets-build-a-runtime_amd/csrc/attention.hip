@@ -54,7 +54,18 @@ struct AttnArgs {
     float* part;                 // split partials Σ p·V: [bh][n_items][128 rows][D]
     float* ml;                   // split running max and Σ p: [bh][n_items][128 rows][2]
     int* queue;                  // split work counter, reset before every launch
+    int o_heads;                 // 0: O is [bh, S, D]; H > 0: O is [B, S, H, D] (fused transpose)
 };
+
+// Row q of head bh in the output: [bh][S][D], or [B][S][H][D] when the
+// following TRANSPOSE(1, 2) is fused (16x16 kernel only).
+__device__ __forceinline__ float* attn_out_row(const AttnArgs& g, long long bh, long long q) {
+    if (g.o_heads) {
+        const long long b = bh / g.o_heads, h = bh - b * g.o_heads;
+        return g.O + ((b * g.S + q) * g.o_heads + h) * (long long)g.D;
+    }
+    return g.O + (bh * g.S + q) * (long long)g.D;
+}
 
 // One K/V tile (AT_KB keys × DP) staged through registers: thread t holds the
 // float4 granules idx = t + i·AT_NT of each tile in row-major order.  Keys
@@ -412,7 +423,7 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
         const bool part = SPLIT && slot >= 0;
         const long long prow = slot * A16_QB + (q - qblk * A16_QB);   // partial row in the workspace
         const float inv_l = part ? 1.0f : 1.0f / l_run;
-        float* __restrict__ Ob = part ? g.part + prow * D : g.O + bh * (long long)S * D + (long long)q * D;
+        float* __restrict__ Ob = part ? g.part + prow * D : attn_out_row(g, bh, q);
         if (part && lg == 0) {
             g.ml[2 * prow] = m_run;
             g.ml[2 * prow + 1] = l_run;
@@ -536,7 +547,7 @@ __global__ __launch_bounds__(256) void attn_split_merge(AttnArgs g, int causal) 
     acc.y *= inv_l;
     acc.z *= inv_l;
     acc.w *= inv_l;
-    *reinterpret_cast<float4*>(g.O + (bh * g.S + row) * (long long)g.D + d) = acc;
+    *reinterpret_cast<float4*>(attn_out_row(g, bh, row) + d) = acc;
 }
 
 // Fallback for head dims the MFMA kernel does not take (hd % 8 != 0 or
@@ -581,6 +592,7 @@ __global__ __launch_bounds__(256) void attn_fwd_rows(AttnArgs g, int causal) {
 
 // Step::i: [0]=bh [1]=S [2]=D [3]=causal [4]=group [5]=DP (0 = row fallback)
 //          [6]=fold [7]=split chunk tiles (0 = none) [8]=split work items per head
+//          [9]=heads of a fused output transpose (0 = none) [10]=16x16 kernel (transpose fusable)
 AttnArgs make_args(const Step& s) {
     AttnArgs g;
     g.Q = (const float*)s.in[0];
@@ -594,6 +606,7 @@ AttnArgs make_args(const Step& s) {
     g.n_qblocks = (g.S + AT_QB - 1) / AT_QB;
     g.scale_log2 = s.f[0] * LOG2E;
     g.fold = 0;
+    g.o_heads = 0;
     return g;
 }
 
@@ -618,6 +631,7 @@ void launch_attn16(const Step& s, hipStream_t st) {
     if (g.S <= 0 || s.i[0] <= 0) return;
     g.n_qblocks = (g.S + A16_QB - 1) / A16_QB;
     g.fold = CAUSAL && s.i[6] != 0;
+    g.o_heads = (int)s.i[9];
     g.ch = (int)s.i[7];
     g.n_items = (int)s.i[8];
     g.n_bh = (int)s.i[0];
@@ -743,6 +757,7 @@ int decode_attention(const OpNode* n, Step* s) {
                 default: s->run = pick16<128>(causal, has_mask); break;
             }
             s->name = "attn_fwd_mfma16_f32";
+            s->i[10] = 1;   // can write O as [B, S, H, D] (i[9] = H) for a fused transpose
             return LBR_OK;
         }
         switch (dp) {

@@ -26,6 +26,8 @@
 //   HEAD_PROLOGUE  SLICE last dim → [ADD bias row] → [RMSNORM over hd] →
 //               TRANSPOSE(S,H) → [RoPE: MUL cos, SLICE, SLICE, NEG, CAT,
 //               MUL sin, ADD]: one wavefront per (token, head) row.
+//   ATTN_TRANSPOSE  ATTENTION → TRANSPOSE(H,S): the attention kernel stores
+//               its rows straight into [B, S, H, hd].
 #include "lbr_device.h"
 
 #include <math.h>
@@ -457,6 +459,36 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
             ++i;
             continue;
         }
+        // ATTN_TRANSPOSE: attention output [B, H, S, hd] transposed to [B, S, H, hd]
+        if (nd->op == OP_ATTENTION && i + 1 < n && is_f32(nd) && nd->n_dims == 4) {
+            const OpNode* tr = &nodes[i + 1];
+            Step as = Step();
+            const int B = nd->out_shape[0], H = nd->out_shape[1], S = nd->out_shape[2], hd = nd->out_shape[3];
+            if (tr->op == OP_TRANSPOSE && tr->n_inputs >= 1 && tr->inputs[0] == nd->output && is_f32(tr) &&
+                tr->n_dims == 4 && tr->extra[0] == B && tr->extra[1] == H && tr->extra[2] == 1 &&
+                tr->extra[3] == S && tr->extra[4] == hd && decode_attention(nd, &as) == LBR_OK && as.i[10] == 1) {
+                // the kernel reads Q, K, V (and the mask) while it writes the transposed output
+                const bool mask = nd->extra[3] != 0;
+                const long long qkv = (long long)B * H * S * hd * 4;
+                const int group = nd->extra[4] > 0 ? nd->extra[4] : 1;
+                std::vector<Rng> reads{rng(nd->inputs[0], qkv), rng(nd->inputs[1], qkv / group),
+                                       rng(nd->inputs[2], qkv / group)};
+                if (mask) reads.push_back(rng(nd->inputs[3], (long long)B * H * S * S * 4));
+                const Rng y = out_rng(tr);
+                if (!any_overlap(y, reads) && dead_after(nodes, n, i + 2, {out_rng(nd)}, {y}, live)) {
+                    FusedRun f;
+                    f.first = i;
+                    f.count = 2;
+                    f.kind = LBR_FUSE_ATTN_TRANSPOSE;
+                    f.out = tr->output;
+                    f.Hs[0] = H;
+                    out->push_back(f);
+                    i += 2;
+                    continue;
+                }
+            }
+            lbr_set_error("");
+        }
         // HEAD_PROLOGUE: a SLICE of a row-major [rows, ld] tensor
         if (nd->op == OP_SLICE && nd->n_inputs >= 1 && nd->extra[4] == 1 && is_f32(nd)) {
             HeadChain hc;
@@ -517,7 +549,17 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
 // Decoded launch record of a fused run.
 int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
     *s = Step();
-    if (f.kind == LBR_FUSE_GEMM_RESID || f.kind == LBR_FUSE_GEMM_HEADS) {
+    if (f.kind == LBR_FUSE_ATTN_TRANSPOSE) {
+        int rc = decode_attention(&nodes[f.first], s);
+        if (rc) return rc;
+        if (s->i[10] != 1) {
+            lbr_set_error("fusion: attention node %d cannot write a transposed output", f.first);
+            return LBR_ERR_INVALID;
+        }
+        s->out = (void*)f.out;
+        s->i[9] = f.Hs[0];
+        s->name = "attn_fwd_mfma16_f32+transpose";
+    } else if (f.kind == LBR_FUSE_GEMM_RESID || f.kind == LBR_FUSE_GEMM_HEADS) {
         int rc = decode_matmul(&nodes[f.first], s);
         if (rc) return rc;
         if (s->i[13] != 1) {

@@ -62,8 +62,9 @@ EXPECTED = {
     # c_attn is MATMUL_ADD (bias already in the GEMM): three (slice, transpose) chains per layer
     "gpt2": Counter({("gemm_heads", 7): 2, ("gemm_resid", 2): 4}),
     # q/k: slice → per-head RMSNorm → transpose → 7-node RoPE as one kernel; v's transpose lands
-    # over the QKV rows it reads at this size (refused)
-    "qwen3_4b": Counter({("head_prologue", 10): 4, ("gemm_resid", 2): 4}),
+    # over the QKV rows it reads at this size (refused); the attention output transpose is fused
+    # here, while in the other workloads the planner places it over the dead V (refused)
+    "qwen3_4b": Counter({("head_prologue", 10): 4, ("gemm_resid", 2): 4, ("attn_transpose", 2): 2}),
 }
 
 
@@ -245,3 +246,27 @@ def test_not_rotate_half_is_not_rope():
     nodes = _rope_chain(0, 8 * MB)
     nodes[7].inputs[0], nodes[7].inputs[1] = nodes[7].inputs[1], nodes[7].inputs[0]
     assert _windows(nodes) == [(0, 3, "head_prologue")]
+
+
+def _attn_transpose(out_off, v_off=20 * MB, B=1, H=4, S=128, hd=64):
+    q, k, v = ARENA + 16 * MB, ARENA + 18 * MB, ARENA + v_off
+    att = _node(OpType.ATTENTION, [q, k, v, ARENA + 30 * MB], ARENA + 24 * MB, (B, H, S, hd), (S, hd, 1, 0, 1))
+    att.n_inputs = 4          # Q, K, V + the planner's scratch slot
+    tr = _node(OpType.TRANSPOSE, [ARENA + 24 * MB], ARENA + out_off, (B, S, H, hd), (B, H, 1, S, hd))
+    return [att, tr]
+
+
+def test_attention_transpose_fuses():
+    assert _windows(_attn_transpose(26 * MB)) == [(0, 2, "attn_transpose")]
+    # the dead attention output's own memory is fine
+    assert _windows(_attn_transpose(24 * MB)) == [(0, 2, "attn_transpose")]
+
+
+def test_attention_transpose_refuses_output_over_v():
+    # the planner may reuse V's memory once attention is done; one fused kernel still reads V
+    assert _windows(_attn_transpose(20 * MB)) == []
+
+
+def test_attention_transpose_needs_the_16x16_kernel():
+    # head dim 256 runs the 32x32 kernel, which writes [bh, S, hd] only
+    assert _windows(_attn_transpose(40 * MB, hd=256)) == []
