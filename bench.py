@@ -210,9 +210,20 @@ def main() -> int:
     ap.add_argument("--nodes", action="store_true", help="log every node's device time and roofline fraction")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run the library's copy kernel over MIB MiB, 5 times (reference for HBM counters)")
+    ap.add_argument("--save-graph", metavar="STEM",
+                    help="only export the --config workload and write STEM.json + STEM.weights")
+    ap.add_argument("--graph", metavar="STEM",
+                    help="run a saved graph (STEM.json + STEM.weights) instead of exporting --config")
     args = ap.parse_args()
     if args.calibrate_copy:
         return calibrate_copy(args.calibrate_copy)
+    if args.save_graph:
+        from workloads import export_workload
+        _, _, graph = export_workload(args.config)
+        graph.save(args.save_graph)
+        log(f"[bench] wrote {args.save_graph}.json/.weights ({len(graph.nodes)} nodes, {len(graph.constants)} "
+            f"constants) for workload {args.config}")
+        return 0
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
@@ -223,10 +234,19 @@ def main() -> int:
     from runtime.session import Session
     from workloads import WORKLOADS, export_workload
 
-    wl = WORKLOADS[args.config]
     t0 = time.time()
-    model, x, graph = export_workload(args.config)
-    del model
+    if args.graph:
+        # a saved graph: seeded N(0,1) input of the graph's input shape
+        from runtime.ir import Graph
+        graph = Graph.load(args.graph)
+        shape = tuple(graph.tensors[graph.inputs[0]].shape)
+        x = np.random.default_rng(0).standard_normal(shape).astype(np.float32)
+        wl = type("SavedGraph", (), {"title": f"saved graph {Path(args.graph).name}"})()
+        args.config = Path(args.graph).name
+    else:
+        wl = WORKLOADS[args.config]
+        model, x, graph = export_workload(args.config)
+        del model
     sess = Session(graph)
     sess.create(use_graph=not args.eager)
     ex = sess.executor

@@ -82,6 +82,29 @@ def test_fused_plan_matches_unfused(monkeypatch, key, seq, kinds):
         np.testing.assert_array_equal(y, z)
 
 
+def test_saved_reference_graph_runs():
+    """A graph file written by the reference's Graph.save runs through Session on the GPU."""
+    import importlib.util
+    from pathlib import Path
+    import torch
+    from runtime.ir import Graph
+    from oracle.host_exec import OracleRun
+    golden = Path(__file__).resolve().parent / "golden"
+    spec = importlib.util.spec_from_file_location("make_graph_fixture", golden / "make_graph_fixture.py")
+    fx = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(fx)
+    graph = Graph.load(golden / "graph_tiny")
+    x = fx.tiny_input()
+    y, sess = _session_run(graph, x)
+    o = OracleRun(sess.memory_plan).run({graph.inputs[0]: x})[graph.outputs[0]]
+    sess.close()
+    with torch.no_grad():
+        ref = fx.tiny_model().double()(torch.from_numpy(x).double()).numpy()
+    e_gpu, e_go = normwise_rel(y, ref), normwise_rel(y, o)
+    print(f"graph_tiny: gpu-vs-torch64 {e_gpu:.2e}, gpu-vs-oracle {e_go:.2e}")
+    assert e_gpu <= TOL and e_go <= TOL
+
+
 def test_graph_replay_matches_eager_and_reruns():
     """hipGraph replay == eager launches, and repeated runs with new inputs stay correct."""
     from workloads import export_workload, WORKLOADS
