@@ -85,6 +85,9 @@ def node_work(node, graph) -> tuple[float, float]:
         s, hd = q[-2], q[-1]
         flops = 4.0 * bh * s * s * hd * (0.5 if node.attrs.get("causal") else 1.0)
         return flops, float(sum(nbytes(t) for t in node.inputs[:3]) + out_b)
+    if op == OpType.EMBEDDING:
+        # a gather: the ids, the table rows it reads (as many bytes as it writes) and the output
+        return 0.0, float(nbytes(node.inputs[0]) + 2 * out_b)
     return 0.0, float(sum(nbytes(t) for t in node.inputs) + out_b)
 
 
@@ -326,9 +329,11 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded N(0,1) input, random-init N(0,0.02) weights)",
+        "data": ("synthetic (seeded uniform token ids" if x.dtype.kind == "i" else
+                 "synthetic (seeded N(0,1) input") + ", random-init N(0,0.02) weights)",
         "config": {"workload": args.config, "title": wl.title, "batch": int(x.shape[0]),
-                   "seq_len": int(x.shape[1]), "d_model": int(x.shape[2]),
+                   "seq_len": int(x.shape[1]),
+                   "d_model": int(x.shape[2]) if x.ndim == 3 else int(getattr(wl, "d_model", 0)),
                    "graph": "hipGraph replay" if not args.eager else "eager launches",
                    "nodes_per_step": len(ex.dispatch_order), "kernels_per_step": len(units),
                    "fused_runs": len(runs)},

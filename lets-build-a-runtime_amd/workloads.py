@@ -121,6 +121,45 @@ def init_weights(model: nn.Module, seed: int = 0) -> nn.Module:
     return model.eval()
 
 
+class CausalLM(nn.Module):
+    """A HuggingFace causal LM returning logits for token ids — the reference's
+    full-model benchmark wrapper (ablation/bench_transformer_ablation.py:186-208)."""
+
+    def __init__(self, lm: nn.Module) -> None:
+        super().__init__()
+        self.lm = lm
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        return self.lm(ids, use_cache=False).logits
+
+
+def gpt2_lm(n_layer: int = 2, n_head: int = 12, n_embd: int = 768, vocab: int = 50257) -> nn.Module:
+    """GPT2LMHeadModel as the reference builds it (bench_transformer_ablation.py:170-183): tied LM head."""
+    from transformers import GPT2Config, GPT2LMHeadModel
+    cfg = GPT2Config(n_layer=n_layer, n_head=n_head, n_embd=n_embd, vocab_size=vocab, attn_pdrop=0.0,
+                     resid_pdrop=0.0, embd_pdrop=0.0)
+    cfg._attn_implementation = "sdpa"
+    m = GPT2LMHeadModel(cfg)
+    m.config.use_cache = False
+    return CausalLM(m)
+
+
+def qwen3_lm(hidden: int = 2560, n_layer: int = 2, n_heads: int = 32, n_kv: int = 8, head_dim: int = 128,
+             ffn: int = 9728, vocab: int = 151936, eps: float = 1e-6, theta: float = 1e6) -> nn.Module:
+    """Qwen3ForCausalLM with Qwen3-4B's shape, two layers and tied embeddings (the reference
+    loads the same config from the hub, bench_transformer_ablation.py:196-208; no network here)."""
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    cfg = Qwen3Config(hidden_size=hidden, intermediate_size=ffn, num_hidden_layers=n_layer,
+                      num_attention_heads=n_heads, num_key_value_heads=n_kv, head_dim=head_dim,
+                      rms_norm_eps=eps, vocab_size=vocab, max_position_embeddings=40960,
+                      rope_parameters={"rope_type": "default", "rope_theta": theta}, attention_bias=False,
+                      tie_word_embeddings=True)
+    cfg._attn_implementation = "sdpa"
+    m = Qwen3ForCausalLM(cfg)
+    m.config.use_cache = False
+    return CausalLM(m)
+
+
 @dataclass(frozen=True)
 class Workload:
     key: str
@@ -129,13 +168,17 @@ class Workload:
     d_model: int
     build: Callable[[], nn.Module]
     causal: bool = True
+    vocab: int = 0               # > 0: the model takes int64 token ids [1, S] in [0, vocab)
 
     def model(self, seed: int = 0) -> nn.Module:
         return init_weights(self.build(), seed)
 
     def input(self, seed: int = 0, seq_len: int | None = None) -> np.ndarray:
         s = self.seq_len if seq_len is None else seq_len
-        return np.random.default_rng(seed).standard_normal((1, s, self.d_model)).astype(np.float32)
+        rng = np.random.default_rng(seed)
+        if self.vocab:
+            return rng.integers(0, self.vocab, (1, s), dtype=np.int64)
+        return rng.standard_normal((1, s, self.d_model)).astype(np.float32)
 
 
 WORKLOADS: dict[str, Workload] = {
@@ -146,6 +189,11 @@ WORKLOADS: dict[str, Workload] = {
     "7b4k": Workload("7b4k", "7B-shaped block S4096 D4096 H32", 4096, 4096, lambda: CausalGeluBlock(4096, 32)),
     "qwen3_4b": Workload("qwen3_4b", "Qwen3-4B-shaped body 2 layers S1024 D2560 GQA 32/8", 1024, 2560,
                          lambda: Qwen3Body()),
+    # the reference's published full-model rows (README.md:41-57): embeddings + 2 layers + LM head
+    "gpt2_lm": Workload("gpt2_lm", "GPT-2 LM 2 layers S1024 D768 vocab 50257 (token ids in, logits out)", 1024,
+                        768, lambda: gpt2_lm(), vocab=50257),
+    "qwen3_4b_lm": Workload("qwen3_4b_lm", "Qwen3-4B-shaped LM 2 layers S1024 D2560 vocab 151936 (ids in, logits out)",
+                            1024, 2560, lambda: qwen3_lm(), vocab=151936),
 }
 
 # BASELINE.json configs[i] → workload key
@@ -166,8 +214,9 @@ def reference_forward(model: nn.Module, x: np.ndarray, dtype=torch.float64) -> n
     """PyTorch eager forward on the CPU in ``dtype`` (float64 by default)."""
     with torch.no_grad():
         m = model.to(dtype)
+        xt = torch.from_numpy(x)
         try:
-            y = m(torch.from_numpy(x).to(dtype))
+            y = m(xt if not xt.is_floating_point() else xt.to(dtype))   # token ids stay int64
         finally:
             model.to(torch.float32)
     return y.to(torch.float64).numpy()

@@ -28,7 +28,7 @@ def _session_run(graph, x, **create_kw):
 
 
 @pytest.mark.parametrize("key,seq", [("toy", None), ("gpt2w", None), ("gpt2", None), ("qwen3_4b", None),
-                                     ("7b4k", 256)])
+                                     ("7b4k", 256), ("gpt2_lm", 128), ("qwen3_4b_lm", 64)])
 def test_workload_parity(key, seq):
     from workloads import export_workload, reference_forward
     from oracle.host_exec import OracleRun

@@ -15,7 +15,7 @@ from pathlib import Path
 import pytest
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
-KEYS = ["toy", "gpt2w", "gpt2", "7b4k", "qwen3_4b"]
+KEYS = ["toy", "gpt2w", "gpt2", "7b4k", "qwen3_4b", "gpt2_lm", "qwen3_4b_lm"]
 
 
 def _jsonable(v):
