@@ -95,9 +95,10 @@ class CompiledExecutor(Executor):
         self._nodes = None
         self._order = []
         self._arena = 0
-        # weights handed over by a previous executor (Session.rebind) become ours
+        # weights passed in (Session's shared block) are borrowed: used when they cover the
+        # graph's constants, never freed here; weights this executor uploads itself it owns
         self._weights: DeviceWeights | None = weights
-        self._owns_weights = True
+        self._owns_weights = weights is None
         self._inputs: dict[str, tuple[int, int]] = {}   # name -> (device ptr, nbytes)
         self._addr: dict[str, int] = {}
 
@@ -303,7 +304,8 @@ class CompiledExecutor(Executor):
             self._weights = None
 
     def release_weights(self) -> DeviceWeights | None:
-        """Hand the resident weights to another executor (Session.rebind); this one stops owning them."""
+        """Hand the resident weights to the caller (Session, which shares them between cached
+        plans and frees them); this executor stops owning them."""
         self._owns_weights = False
         return self._weights
 

@@ -12,9 +12,16 @@ Same API as the reference (runtime/session.py:79-229):
 resident across ``rebind`` calls when the constants are unchanged.
 ``execution_mode="interpreted"`` (the reference's per-node CPU debug path)
 is not provided by this backend and raises.
+
+``rebind`` keeps the last ``plan_cache`` compiled plans (arena, node array,
+hipGraph) keyed by their bindings: returning to a shape seen before switches
+to its plan without re-planning or re-capturing.  All cached plans share one
+device copy of the weights.
 """
 
 from __future__ import annotations
+
+from collections import OrderedDict
 
 import numpy as np
 
@@ -38,6 +45,20 @@ class Session:
         self._backend = "hip"
         self._profile = False
         self._memory_plan = None
+        # rebind cache: bindings key → (executor, resolved graph, memory plan), least recent first
+        self._plans: OrderedDict = OrderedDict()
+        self._plan_cache = 8
+        self._key = None
+        self._weights: list = []      # device weight blocks shared by the cached executors
+
+    @staticmethod
+    def _bindings_key(bindings: dict[str, int] | None):
+        return tuple(sorted((bindings or {}).items()))
+
+    @property
+    def cached_plans(self) -> list:
+        """Bindings of the compiled plans kept for rebind, least recently used first."""
+        return [dict(k) for k in self._plans]
 
     @property
     def graph(self) -> Graph:
@@ -70,17 +91,20 @@ class Session:
     def create(self, execution_mode: str = "compiled", backend: str = "hip", optimization: str = "default",
                pipeline: list[Pass] | None = None, verbose: bool = False, profile: bool = False,
                bindings: dict[str, int] | None = None, validation: str = "normal",
-               use_graph: bool = True) -> None:
+               use_graph: bool = True, plan_cache: int = 8) -> None:
         """Optimise (once), resolve ``bindings``, plan, validate and compile.
 
         optimization: "none" | "default" (pipeline once) | "aggressive" (until stable)
         validation:   "strict" (fail on warnings) | "normal" (fail on errors) | "none"
         use_graph:    capture the launch sequence into a hipGraph (default) or launch eagerly
+        plan_cache:   compiled plans kept for rebind (≥ 1)
         """
+        self.close()
         self._execution_mode = execution_mode
         self._backend = backend
         self._profile = profile
         self._use_graph = use_graph
+        self._plan_cache = max(1, int(plan_cache))
         fail_on = _validation_severity(validation)
         self._check_mode(execution_mode)
 
@@ -118,20 +142,29 @@ class Session:
 
         ex = self._make_executor(execution_mode, backend, profile)
         ex.compile(mem)
-        self._replace_executor(ex)
+        self._adopt(self._bindings_key(bindings), ex)
 
     def rebind(self, bindings: dict[str, int]) -> None:
-        """Re-resolve, re-plan and re-compile for new symbol values (passes are not re-run)."""
+        """Switch to new symbol values (passes are not re-run): the cached plan for these
+        bindings if there is one, else re-resolve, re-plan and re-compile (session.py:187-207
+        of the reference), sharing the resident weights."""
+        key = self._bindings_key(bindings)
+        if key == self._key and self._executor is not None:
+            return
+        if key in self._plans:
+            self._plans.move_to_end(key)
+            self._executor, self._resolved, self._memory_plan = self._plans[key]
+            self._plan_stats = self._memory_plan.stats
+            self._key = key
+            return
         self._resolved = resolve_graph(self._graph, bindings)
         mem = plan(self._resolved)
         self._memory_plan = mem
         self._plan_stats = mem.stats
-        weights = None
-        if self._executor is not None and hasattr(self._executor, "release_weights"):
-            weights = self._executor.release_weights()
-        ex = self._make_executor(self._execution_mode, self._backend, self._profile, weights=weights)
+        ex = self._make_executor(self._execution_mode, self._backend, self._profile,
+                                 weights=self._weights[-1] if self._weights else None)
         ex.compile(mem)
-        self._replace_executor(ex)
+        self._adopt(key, ex)
 
     def run(self, inputs: dict[str, np.ndarray], profile: bool = False) -> dict[str, np.ndarray]:
         if self._executor is None:
@@ -145,17 +178,37 @@ class Session:
                 self._executor._profile = self._profile
 
     def close(self) -> None:
-        """Free the executor's device memory now (otherwise freed when the session is collected)."""
-        if self._executor is not None and hasattr(self._executor, "close"):
-            self._executor.close()
+        """Free every cached plan's device memory and the weights now (otherwise freed when
+        the session is collected)."""
+        execs = [e for e, _, _ in self._plans.values()]
+        if self._executor is not None and all(self._executor is not e for e in execs):
+            execs.append(self._executor)
+        for e in execs:
+            if hasattr(e, "close"):
+                e.close()
+        for w in self._weights:
+            w.free()
+        self._plans.clear()
+        self._weights = []
         self._executor = None
+        self._key = None
 
     # ------------------------------------------------------------------ internals
-    def _replace_executor(self, ex: Executor) -> None:
-        old = self._executor
+    def _adopt(self, key, ex: Executor) -> None:
+        """Make `ex` current and cache it under `key`; the session takes over its weights
+        (shared with later plans) and evicts the least recently used plan beyond the cache size."""
+        if hasattr(ex, "release_weights"):
+            w = ex.release_weights()
+            if w is not None and all(w is not v for v in self._weights):
+                self._weights.append(w)
         self._executor = ex
-        if old is not None and old is not ex and hasattr(old, "close"):
-            old.close()
+        self._key = key
+        self._plans[key] = (ex, self._resolved, self._memory_plan)
+        self._plans.move_to_end(key)
+        while len(self._plans) > self._plan_cache:
+            _, (old, _, _) = self._plans.popitem(last=False)
+            if old is not ex and hasattr(old, "close"):
+                old.close()
 
     @staticmethod
     def _check_mode(execution_mode: str) -> None:

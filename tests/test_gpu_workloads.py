@@ -105,6 +105,42 @@ def test_saved_reference_graph_runs():
     assert e_gpu <= TOL and e_go <= TOL
 
 
+def test_rebind_plan_cache():
+    """Dynamic sequence length (the reference's decode loop rebinds every step, run_gpt2.py:95-99):
+    each length runs correctly; a length seen before reuses its compiled plan; the least recently
+    used plan is evicted; every plan shares one device copy of the weights."""
+    import torch
+    from runtime.exporter import export_model
+    from runtime.session import Session
+    from oracle.host_exec import OracleRun
+    from workloads import CausalGeluBlock, init_weights
+    m = init_weights(CausalGeluBlock(64, 4), seed=3)
+    g = export_model(m, (torch.randn(1, 16, 64),), dynamic_dims={"L": [("x", 1)]})
+    s = Session(g)
+    s.create(bindings={"L": 16}, plan_cache=2)
+    seen = {}
+    for L in (16, 40, 16, 96, 40):
+        s.rebind({"L": L})
+        if L == 16 and 16 in seen:
+            assert s.executor is seen[16], "rebind to a cached length must reuse its plan"
+        seen.setdefault(L, s.executor)
+        x = np.random.default_rng(L).standard_normal((1, L, 64)).astype(np.float32)
+        y = s.run({g.inputs[0]: x})[g.outputs[0]]
+        with torch.no_grad():
+            ref = m.double()(torch.from_numpy(x).double()).numpy()
+            m.float()
+        o = OracleRun(s.memory_plan).run({g.inputs[0]: x})[g.outputs[0]]
+        assert y.shape == (1, L, 64)
+        assert normwise_rel(y, ref) <= TOL and normwise_rel(y, o) <= TOL
+    # cache of 2 after 16, 40, 16, 96, 40: 16 was refreshed, then 96 evicted 40, then 40 evicted 16
+    assert s.cached_plans == [{"L": 96}, {"L": 40}]
+    assert s.executor is not seen[40]
+    w = {id(e.weights) for e, _, _ in s._plans.values()}
+    assert len(w) == 1
+    s.close()
+    assert s.cached_plans == [] and s.executor is None
+
+
 def test_graph_replay_matches_eager_and_reruns():
     """hipGraph replay == eager launches, and repeated runs with new inputs stay correct."""
     from workloads import export_workload, WORKLOADS
