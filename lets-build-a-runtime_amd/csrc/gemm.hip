@@ -1,4 +1,4 @@
-// gemm.hip — fp32 GEMM on the gfx950 matrix cores (v_mfma_f32_32x32x2_f32).
+// gemm.hip — fp32 GEMM on the gfx950 matrix cores.
 //
 // Replaces kernel_matmul_ab / kernel_matmul_gemv (csrc/ops/matmul.c:19-79,
 // cblas_sgemm / cblas_sgemv) behind MATMUL and MATMUL_ADD
@@ -8,7 +8,13 @@
 //               reference hard-codes alpha = 1 on this path, executor.c:341/344)
 // op(B) = Bᵀ when trans_b (B stored [N, K], nn.Linear layout) else B ([K, N]).
 //
-// Tiling: a 256-thread workgroup (4 wavefronts, 2×2) owns a 128×128 tile of
+// Two kernels: gemm_dma_f32 (below the register-staged one) takes every
+// trans_b GEMM with K a multiple of 32 — all the Linear layers of the
+// workloads — with v_mfma_f32_16x16x4_f32, direct-to-LDS loads and a tile
+// shape chosen per GEMM; gemm_mfma_f32 (v_mfma_f32_32x32x2_f32) takes the
+// rest (B stored [K, N], ragged K, unaligned operands).
+//
+// gemm_mfma_f32 tiling: a 256-thread workgroup (4 wavefronts, 2×2) owns a 128×128 tile of
 // C; each wavefront owns 64×64 = 2×2 MFMA blocks of 32×32 (64 accumulator
 // registers per lane).  K advances in steps of 32: the next A/B tiles are
 // fetched from global memory into registers while the current ones are
@@ -23,6 +29,9 @@
 // gives each XCD a contiguous range of tiles so neighbouring tiles (which
 // reuse the same A and B panels) hit the same L2.
 #include "lbr_device.h"
+
+#include <cstdlib>
+#include <cstring>
 
 namespace {
 
@@ -351,6 +360,258 @@ __global__ __launch_bounds__(NT, 2) void gemm_mfma_f32(GemmArgs g) {
         }
 }
 
+// ---------------------------------------------------------------- DMA GEMM (trans_b)
+// C = A · Bᵀ with A [M, K] and B [N, K] both K-contiguous, K a multiple of
+// DBK: the 16-byte direct-to-LDS form of buffer loads streams each K step
+// of the A and B tiles into LDS without passing through registers, into a
+// second LDS stage while the first is consumed (one barrier per K step).
+//
+// LDS layout of a stage: the A tile's TM rows, then the B tile's TN rows,
+// DBK floats (8 chunks of 16 bytes) per row, chunk c of row r stored at
+// position c ^ (r & 7) so the 16-byte fragment reads of 8 consecutive rows
+// hit 8 different bank groups.  One DMA instruction fills 1 KB = 8 rows:
+// lane l lands at byte 16·l, i.e. row l/8, position l%8, so it fetches the
+// logical chunk (l%8) ^ row.
+//
+// Math: v_mfma_f32_16x16x4_f32, a WGM×WGN grid of wavefronts each owning a
+// (TM/WGM)×(TN/WGN) block of C.  Lane (kq, i) = (l/16, l%16) reads 4
+// consecutive k of row i of a 16-row block; component q feeds MFMA q, which
+// reduces over k = 4·kq + q of the 16-wide chunk — the four MFMAs cover the
+// chunk exactly once (a reordering of the K sum).  Accumulator register r of
+// lane l holds row 4·(l/16) + r, column l%16 of the 16×16 block.
+//
+// Software pipeline: the fragments of the next 16-wide K chunk are read
+// while the MFMAs of the current one issue; at the last chunk of a K step
+// the workgroup synchronises once (the next stage has landed and the
+// current one is free), starts the DMA two steps ahead into the freed stage
+// and reads the next step's first fragments.  sched_group_barrier pairs
+// every DMA issue and fragment read with one MFMA so the matrix pipe keeps
+// issuing.
+constexpr int DBK = 32;
+
+// 16-byte DMA into LDS: lane l's dword4 at r + voff + soff lands at lds + 16·l.
+// (A plain device function: the builtin has no host-side form inside kernel templates.)
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, float* lds, unsigned voff, unsigned soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, soff, 0, 0);
+}
+
+template <int NV, int ND, int NM>
+__device__ __forceinline__ void chunk_schedule() {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // one VMEM read (DMA)
+    }
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NM - NV - ND, 0);
+}
+
+template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS>
+__global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) {
+    constexpr int NW = WGM * WGN;
+    constexpr int CH = DBK / 4;                 // 16-byte chunks per tile row
+    constexpr int RPI = 64 / CH;                // tile rows per DMA instruction
+    constexpr int FM = TM / WGM / 16, FN = TN / WGN / 16;
+    constexpr int IA = TM / NW / RPI, IB = TN / NW / RPI;
+    static_assert(IA * NW * RPI == TM && IB * NW * RPI == TN, "tile rows must split evenly over the waves");
+    static_assert(CH == 8 && FM * 16 * WGM == TM && FN * 16 * WGN == TN, "tile shape");
+    constexpr int STAGE = (TM + TN) * DBK;
+    constexpr int NCC = CH / 4;                 // 16-wide K chunks per step
+    __shared__ __attribute__((aligned(1024))) float lds[2 * STAGE];
+
+    int tm, tn;
+    tile_coords(g, tm, tn);
+    const int m0 = tm * TM, n0 = tn * TN;
+    const long long bz = blockIdx.z;
+    const int M = g.M, N = g.N, K = g.K;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    // DMA sources: row clamped to the matrix (rows past the edge are never stored)
+    const int dr = lane / CH, dp = lane % CH;
+    unsigned offA[IA], offB[IB];
+#pragma unroll
+    for (int t = 0; t < IA; ++t) {
+        const int row = wave * (TM / NW) + t * RPI + dr;
+        offA[t] = (unsigned)(min(m0 + row, M - 1) * K + ((dp ^ dr) * 4)) * 4u;
+    }
+#pragma unroll
+    for (int t = 0; t < IB; ++t) {
+        const int row = wave * (TN / NW) + t * RPI + dr;
+        offB[t] = (unsigned)(min(n0 + row, N - 1) * K + ((dp ^ dr) * 4)) * 4u;
+    }
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(g.A + bz * g.sA), (short)0, M * K * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(g.B + bz * g.sB), (short)0, N * K * 4, 0x00020000);
+    auto issue = [&](int k0, float* st) {
+        float* la = st + wave * (TM / NW) * DBK;
+        float* lb = st + TM * DBK + wave * (TN / NW) * DBK;
+#pragma unroll
+        for (int t = 0; t < IA; ++t) dma16(ra, la + t * RPI * DBK, offA[t], (unsigned)k0 * 4u);
+#pragma unroll
+        for (int t = 0; t < IB; ++t) dma16(rb, lb + t * RPI * DBK, offB[t], (unsigned)k0 * 4u);
+    };
+
+    floatx4 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // fragment reads: the swizzle depends on the row only through fi (blocks start at multiples of 16)
+    const int fi = lane & 15, kq = lane >> 4;
+    int rdA[NCC], rdB[NCC];
+#pragma unroll
+    for (int cc = 0; cc < NCC; ++cc) {
+        const int o = fi * DBK + (((cc * 4 + kq) ^ (fi & 7)) * 4);
+        rdA[cc] = wm * (TM / WGM) * DBK + o;
+        rdB[cc] = TM * DBK + wn * (TN / WGN) * DBK + o;
+    }
+    floatx4 fa[2][FM], fb[2][FN];
+    auto frags = [&](const float* st, int cc, floatx4* a, floatx4* b) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const floatx4*>(st + rdA[cc] + i * 16 * DBK);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const floatx4*>(st + rdB[cc] + j * 16 * DBK);
+    };
+    auto mma = [&](const floatx4* a, const floatx4* b) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
+    };
+
+    // K range of this workgroup (split ks of ksplit; kchunk is a multiple of DBK)
+    const int ks = blockIdx.y;
+    const int kbeg = ks * g.kchunk;
+    const int nk = (min(K, kbeg + g.kchunk) - kbeg) / DBK;
+    if (nk > 0) {
+        issue(kbeg, lds);
+        __builtin_amdgcn_s_waitcnt(0x3F70);   // vmcnt(0)
+        __syncthreads();
+        if (nk > 1) issue(kbeg + DBK, lds + STAGE);
+        frags(lds, 0, fa[0], fb[0]);
+        for (int kt = 0; kt < nk - 1; ++kt) {
+            const int cur = (kt & 1) * STAGE;
+#pragma unroll
+            for (int cc = 0; cc < NCC; ++cc) {
+                if (cc + 1 < NCC) {
+                    frags(lds + cur, cc + 1, fa[(cc + 1) & 1], fb[(cc + 1) & 1]);
+                } else {
+                    __builtin_amdgcn_sched_barrier(0);
+                    __builtin_amdgcn_s_waitcnt(0x3F70);   // step kt+1 landed (this wave's DMA) ...
+                    __syncthreads();                      // ... and every wave's; stage cur fully read
+                    // two steps ahead, clamped to the last step (re-fetched into a stage not read again)
+                    issue(kbeg + min(kt + 2, nk - 1) * DBK, lds + cur);
+                    frags(lds + (STAGE - cur), 0, fa[0], fb[0]);
+                }
+                mma(fa[cc & 1], fb[cc & 1]);
+                if (cc + 1 < NCC) chunk_schedule<0, FM + FN, 4 * FM * FN>();
+                else chunk_schedule<IA + IB, FM + FN, 4 * FM * FN>();
+            }
+        }
+        const int cur = ((nk - 1) & 1) * STAGE;
+#pragma unroll
+        for (int cc = 0; cc < NCC; ++cc) {
+            if (cc + 1 < NCC) frags(lds + cur, cc + 1, fa[(cc + 1) & 1], fb[(cc + 1) & 1]);
+            mma(fa[cc & 1], fb[cc & 1]);
+            if (cc + 1 < NCC) chunk_schedule<0, FM + FN, 4 * FM * FN>();
+        }
+        __builtin_amdgcn_s_waitcnt(0x3F70);   // no DMA may still target this workgroup's LDS at exit
+    }
+
+    const int rq = (lane >> 4) * 4, cl = lane & 15;
+    const int mw = m0 + wm * (TM / WGM), nw = n0 + wn * (TN / WGN);
+    if (g.ksplit > 1) {
+        float* __restrict__ Wp = g.W + ((long long)ks * gridDim.z + bz) * (long long)M * N;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int n = nw + j * 16 + cl;
+            if (n >= N) continue;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = mw + i * 16 + rq + r;
+                    if (m < M) Wp[(long long)m * N + n] = acc[i][j][r];
+                }
+        }
+        return;
+    }
+    if (g.n_split) {
+        // head scatter: the column fixes split, head, d and split bias; the
+        // row fixes (b, s) = divmod(m, S), stepped from each 4-row group's first row
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int n = nw + j * 16 + cl;
+            if (n >= N || n < g.col_begin[0] || n >= g.col_begin[g.n_split]) continue;
+            int k = 0;
+            while (k + 1 < g.n_split && n >= g.col_begin[k + 1]) ++k;
+            const int c = n - g.col_begin[k];
+            const int h = c / g.hd, d = c - h * g.hd;
+            const float bv = HAS_BIAS ? g.bias[n] : 0.f;
+            const bool has_sb = g.sbias[k] != nullptr;
+            const float sb = has_sb ? g.sbias[k][c] : 0.f;
+            float* __restrict__ col = g.dst[k] + ((long long)h * g.S) * g.hd + d;
+            const long long bstride = (long long)g.Hs[k] * g.S * g.hd;
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                const int mb = mw + i * 16 + rq;
+                const int b0 = mb / g.S, s0 = mb - b0 * g.S;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (mb + r >= M) continue;
+                    int b = b0, s = s0 + r;
+                    while (s >= g.S) {   // r < 4: at most one step unless S < 4
+                        s -= g.S;
+                        ++b;
+                    }
+                    float v = HAS_BIAS ? (acc[i][j][r] + bv) : g.alpha * acc[i][j][r];
+                    if (has_sb) v = v + sb;
+                    col[b * bstride + (long long)s * g.hd] = v;
+                }
+            }
+        }
+        return;
+    }
+    float* __restrict__ C = g.C + bz * g.sC;
+    const float* __restrict__ R = g.resid ? g.resid + bz * g.sC : nullptr;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int n = nw + j * 16 + cl;
+        if (n >= N) continue;
+        const float bv = HAS_BIAS ? g.bias[n] : 0.f;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            float rv[4] = {0.f, 0.f, 0.f, 0.f};
+            if (R) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = mw + i * 16 + rq + r;
+                    if (m < M) rv[r] = R[(long long)m * N + n];
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = mw + i * 16 + rq + r;
+                if (m >= M) continue;
+                float v = HAS_BIAS ? (acc[i][j][r] + bv) : g.alpha * acc[i][j][r];
+                if (R) v = v + rv[r];
+                C[(long long)m * N + n] = v;
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- GEMV
 // M == 1 (decode): the reference switches to sgemv here (executor.c:217).
 // trans_b: one wavefront per output column, lanes stride over K.
@@ -472,20 +733,99 @@ __global__ void splitk_reduce(GemmArgs g, long long total) {
     }
 }
 
+template <bool HAS_BIAS>
+void launch_splitk_reduce(const Step& s, const GemmArgs& g, hipStream_t st) {
+    const long long total = (long long)g.M * g.N * s.i[3];
+    const bool v4 = s.i[12] != 0 && g.n_split == 0 && (!g.resid || lbr_aligned(g.resid, 16));
+    const unsigned blocks = lbr_grid(v4 ? total / 4 : total, 256, 4096);
+    if (v4)
+        hipLaunchKernelGGL((splitk_reduce<HAS_BIAS, true>), dim3(blocks), dim3(256), 0, st, g, total);
+    else
+        hipLaunchKernelGGL((splitk_reduce<HAS_BIAS, false>), dim3(blocks), dim3(256), 0, st, g, total);
+}
+
 template <bool TRANS_B, bool VEC, bool HAS_BIAS>
 void launch_gemm_t(const Step& s, hipStream_t st) {
     GemmArgs g = make_args(s);
     if (g.M <= 0 || g.N <= 0) return;
     dim3 grid(g.tiles_m * g.tiles_n, g.ksplit, (unsigned)s.i[3]);
     hipLaunchKernelGGL((gemm_mfma_f32<TRANS_B, VEC, HAS_BIAS>), grid, dim3(NT), 0, st, g);
-    if (g.ksplit > 1) {
-        const long long total = (long long)g.M * g.N * s.i[3];
-        const bool v4 = s.i[12] != 0 && g.n_split == 0 && (!g.resid || lbr_aligned(g.resid, 16));
-        const unsigned blocks = lbr_grid(v4 ? total / 4 : total, 256, 4096);
-        if (v4)
-            hipLaunchKernelGGL((splitk_reduce<HAS_BIAS, true>), dim3(blocks), dim3(256), 0, st, g, total);
-        else
-            hipLaunchKernelGGL((splitk_reduce<HAS_BIAS, false>), dim3(blocks), dim3(256), 0, st, g, total);
+    if (g.ksplit > 1) launch_splitk_reduce<HAS_BIAS>(s, g, st);
+}
+
+template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS>
+void launch_gemm_dma(const Step& s, hipStream_t st) {
+    GemmArgs g = make_args(s);
+    if (g.M <= 0 || g.N <= 0) return;
+    g.tiles_m = (g.M + TM - 1) / TM;
+    g.tiles_n = (g.N + TN - 1) / TN;
+    dim3 grid(g.tiles_m * g.tiles_n, g.ksplit, (unsigned)s.i[3]);
+    hipLaunchKernelGGL((gemm_dma_f32<TM, TN, WGM, WGN, OCC, HAS_BIAS>), grid, dim3(64 * WGM * WGN), 0, st, g);
+    if (g.ksplit > 1) launch_splitk_reduce<HAS_BIAS>(s, g, st);
+}
+
+// Tile shapes of the DMA GEMM: (TM, TN), workgroups resident per CU (LDS
+// and registers), and measured steady-state fraction of the fp32 MFMA peak.
+struct DmaTile {
+    int tm, tn, occ;
+    double eff;
+    const char* name;
+};
+constexpr DmaTile kDmaTiles[] = {
+    {256, 256, 1, 0.94, "256x256"},   // 8 wavefronts (4×2), 128 KB LDS
+    {128, 128, 2, 0.92, "128x128"},   // 4 wavefronts (2×2), 64 KB LDS
+    {128, 64, 3, 0.90, "128x64"},     // 4 wavefronts (2×2), 48 KB LDS
+    {64, 128, 3, 0.90, "64x128"},
+};
+constexpr int kNumDmaTiles = sizeof(kDmaTiles) / sizeof(kDmaTiles[0]);
+
+// Tile shape and number of K ranges for the DMA GEMM.  Time model: the
+// busiest CU runs ceil(items / CUs) workgroups of TM·TN·kchunk MACs each
+// at the tile's efficiency; a K split adds writing and re-reading the
+// partial sums at ~5 TB/s plus a reduction launch.  LBR_GEMM_TILE (a tile
+// name) and LBR_GEMM_KSPLIT override the choice.
+void choose_dma(long long M, long long N, int K, long long batches, int cus, int* tile, int* ksplit, int* kchunk) {
+    const double peak_cu = 157.3e12 / 256.0;
+    const char* force_tile = getenv("LBR_GEMM_TILE");
+    const char* force_ks = getenv("LBR_GEMM_KSPLIT");
+    double best = 1e30;
+    *tile = 1;
+    *ksplit = 1;
+    *kchunk = K;
+    if (cus <= 0) cus = 256;
+    for (int t = 0; t < kNumDmaTiles; ++t) {
+        const DmaTile& d = kDmaTiles[t];
+        if (force_tile && strcmp(force_tile, d.name) != 0) continue;
+        const long long tiles = ((M + d.tm - 1) / d.tm) * ((N + d.tn - 1) / d.tn) * batches;
+        for (int s = 1; s <= 16; ++s) {
+            const int chunk = ((K + s - 1) / s + DBK - 1) / DBK * DBK;
+            const int s_eff = (K + chunk - 1) / chunk;
+            if (force_ks) {
+                if (s != atoi(force_ks) || s_eff != s) continue;
+            } else if (s > 1 && (chunk < 256 || s_eff != s)) {
+                continue;
+            }
+            const long long per_cu = (tiles * s_eff + cus - 1) / cus;
+            double t_s = (double)per_cu * 2.0 * d.tm * d.tn * chunk / (d.eff * peak_cu);
+            if (s_eff > 1) t_s += (2.0 * s_eff + 1.0) * M * N * batches * 4.0 / 5e12 + 4e-6;
+            if (s_eff > 1 && !force_ks) t_s *= 1.05;   // split only for a clear gain
+            if (t_s < best) {
+                best = t_s;
+                *tile = t;
+                *ksplit = s_eff;
+                *kchunk = s_eff > 1 ? chunk : K;
+            }
+        }
+    }
+}
+
+template <bool HAS_BIAS>
+step_fn dma_launcher(int tile) {
+    switch (tile) {
+        case 0: return launch_gemm_dma<256, 256, 4, 2, 1, HAS_BIAS>;
+        case 1: return launch_gemm_dma<128, 128, 2, 2, 2, HAS_BIAS>;
+        case 2: return launch_gemm_dma<128, 64, 2, 2, 3, HAS_BIAS>;
+        default: return launch_gemm_dma<64, 128, 2, 2, 3, HAS_BIAS>;
     }
 }
 
@@ -628,16 +968,31 @@ int decode_matmul(const OpNode* n, Step* s) {
     }
     const bool vec = lbr_aligned(n->inputs[0], 16) && lbr_aligned(n->inputs[1], 16) && K % 4 == 0 &&
                      (trans_b || N % 4 == 0);
+    s->i[12] = (N % 4 == 0) && lbr_aligned(n->output, 16) && (!has_bias || lbr_aligned(n->inputs[2], 16));
+    s->i[13] = 1;   // MFMA path: takes the fused epilogues of Step::in[3..11], i[19..27]
+    // DMA kernel: B [N, K], K a multiple of its K step, 16-byte aligned rows, and
+    // each batch's A and B addressable with 31-bit byte offsets.
+    const char* force_tile = getenv("LBR_GEMM_TILE");
+    const bool legacy = force_tile && strcmp(force_tile, "legacy") == 0;
+    if (!legacy && trans_b && vec && K % DBK == 0 && M * K * 4 < (1LL << 31) && (long long)N * K * 4 < (1LL << 31)) {
+        int tile = 1, ks = 1, kchunk = K;
+        choose_dma(M, N, K, batches, lbr_device_cus(), &tile, &ks, &kchunk);
+        s->i[10] = ks;
+        s->i[11] = kchunk;
+        s->i[14] = tile + 1;
+        s->ws_bytes = ks > 1 ? (size_t)ks * batches * M * N * sizeof(float) : 0;
+        s->run = has_bias ? dma_launcher<true>(tile) : dma_launcher<false>(tile);
+        s->name = "gemm_dma_f32_nt";
+        return LBR_OK;
+    }
     {
         const long long tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN) * batches;
         int kchunk = K;
         const int ks = choose_ksplit(tiles, K, M * (long long)N, lbr_device_cus(), &kchunk);
         s->i[10] = ks;
         s->i[11] = kchunk;
-        s->i[12] = (N % 4 == 0) && lbr_aligned(n->output, 16) && (!has_bias || lbr_aligned(n->inputs[2], 16));
         s->ws_bytes = ks > 1 ? (size_t)ks * batches * M * N * sizeof(float) : 0;
     }
-    s->i[13] = 1;   // MFMA path: takes the fused epilogues of Step::in[3..11], i[19..27]
     if (trans_b) {
         if (vec) s->run = has_bias ? launch_gemm_t<true, true, true> : launch_gemm_t<true, true, false>;
         else s->run = has_bias ? launch_gemm_t<true, false, true> : launch_gemm_t<true, false, false>;

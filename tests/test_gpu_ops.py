@@ -47,9 +47,48 @@ GEMM_CASES = [
 ]
 
 
+# Kernel-selection overrides read when the plan is built: LBR_GEMM_TILE=legacy
+# keeps the register-staged 32x32 kernel, a tile name (256x256, 128x128,
+# 128x64, 64x128) forces that DMA tile, LBR_GEMM_KSPLIT=n forces n K ranges.
+@pytest.mark.parametrize("kernel", ["auto", "legacy"])
 @pytest.mark.parametrize("M,N,K,trans_b,batches,b2d", GEMM_CASES)
 @pytest.mark.parametrize("with_bias", [False, True])
-def test_gemm(M, N, K, trans_b, batches, b2d, with_bias):
+def test_gemm(monkeypatch, kernel, M, N, K, trans_b, batches, b2d, with_bias):
+    if kernel == "legacy":
+        monkeypatch.setenv("LBR_GEMM_TILE", "legacy")
+    name = _gemm_case(M, N, K, trans_b, batches, b2d, with_bias)
+    if kernel == "legacy":
+        assert "dma" not in name
+
+
+DMA_CASES = [
+    # (M, N, K, batches, b_is_2d)
+    (300, 520, 96, 1, True),      # ragged M and N edges, 3 K steps
+    (513, 257, 64, 1, True),
+    (64, 64, 32, 1, True),        # a single K step
+    (96, 200, 160, 3, False),     # batched, B [batches, N, K]
+]
+
+
+@pytest.mark.parametrize("tile", ["256x256", "128x128", "128x64", "64x128"])
+@pytest.mark.parametrize("M,N,K,batches,b2d", DMA_CASES)
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_gemm_dma_tiles(monkeypatch, tile, M, N, K, batches, b2d, with_bias):
+    monkeypatch.setenv("LBR_GEMM_TILE", tile)
+    monkeypatch.setenv("LBR_GEMM_KSPLIT", "1")
+    assert _gemm_case(M, N, K, True, batches, b2d, with_bias) == "gemm_dma_f32_nt"
+
+
+@pytest.mark.parametrize("tile,ks,M,N,K,batches", [("128x128", 3, 200, 300, 3072, 1), ("256x256", 5, 70, 90, 800, 2),
+                                                   ("64x128", 2, 130, 260, 64, 1)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_gemm_dma_ksplit(monkeypatch, tile, ks, M, N, K, batches, with_bias):
+    monkeypatch.setenv("LBR_GEMM_TILE", tile)
+    monkeypatch.setenv("LBR_GEMM_KSPLIT", str(ks))
+    assert _gemm_case(M, N, K, True, batches, batches == 1, with_bias) == "gemm_dma_f32_nt"
+
+
+def _gemm_case(M, N, K, trans_b, batches, b2d, with_bias):
     r = rng(M * 7 + N + K)
     if b2d:
         a = randn(r, 1, M, K)
@@ -75,6 +114,19 @@ def test_gemm(M, N, K, trans_b, batches, b2d, with_bias):
         ref = ref * alpha
     g = one_node_graph(op, {"a": a}, out_shape, attrs, consts)
     _check(g, {"a": a}, ref, 1e-4)
+    return _kernel_of(g)
+
+
+def _kernel_of(graph) -> str:
+    """Kernel the plan of a one-node graph launches (kernel selection happens at plan build)."""
+    from runtime.executor.compiled import CompiledExecutor
+    from runtime.planner import plan
+    ex = CompiledExecutor()
+    ex.compile(plan(graph))
+    try:
+        return ex.kernel_names()[0]
+    finally:
+        ex.close()
 
 
 def test_matmul_add_ignores_alpha():
