@@ -570,7 +570,7 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
             s->in[3] = f.resid;
             s->out = (void*)f.out;
             s->i[12] = s->i[12] && lbr_aligned(f.out, 16);
-            s->name = s->i[4] ? "gemm_mfma_f32_nt+resid" : "gemm_mfma_f32_nn+resid";
+            s->name = s->i[14] ? "gemm_dma_f32_nt+resid" : s->i[4] ? "gemm_mfma_f32_nt+resid" : "gemm_mfma_f32_nn+resid";
         } else {
             if (f.n_split < 1 || f.n_split > 4) {
                 lbr_set_error("fusion: %d head splits", f.n_split);
@@ -586,7 +586,7 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
             s->i[20 + f.n_split] = f.col_begin[f.n_split - 1] + f.width[f.n_split - 1];
             s->i[29] = f.hd;
             s->i[30] = f.S;
-            s->name = s->i[4] ? "gemm_mfma_f32_nt+heads" : "gemm_mfma_f32_nn+heads";
+            s->name = s->i[14] ? "gemm_dma_f32_nt+heads" : s->i[4] ? "gemm_mfma_f32_nt+heads" : "gemm_mfma_f32_nn+heads";
         }
     } else {
         s->in[0] = f.src;

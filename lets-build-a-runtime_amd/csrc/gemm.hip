@@ -657,7 +657,8 @@ __global__ __launch_bounds__(256) void gemv_n(GemmArgs g) {
 }
 
 // Step::i: [0]=M [1]=N [2]=K [3]=batches [4]=trans_b [5]=vec [6]=has_bias
-//          [7]=sA [8]=sB [9]=sC ; f[0] = alpha
+//          [7]=sA [8]=sB [9]=sC [10]=ksplit [11]=kchunk [12]=float4 reduce
+//          [13]=1 (takes fused epilogues) [14]=DMA tile + 1 (0: gemm_mfma_f32) ; f[0] = alpha
 GemmArgs make_args(const Step& s) {
     GemmArgs g;
     g.A = (const float*)s.in[0];
