@@ -49,11 +49,15 @@ struct AttnArgs {
     int S, D, group_size, n_qblocks;
     float scale_log2;            // (1/√hd)·log2(e)
     int fold;                    // causal: workgroup j also runs query block j (16x16 kernel)
-    int ch, n_items;             // key-range split (16x16 kernel): tiles per chunk, work items per head
-    int n_bh;                    // heads × batch (split: the grid is 1-D)
-    float* part;                 // split partials Σ p·V: [bh][n_items][128 rows][D]
-    float* ml;                   // split running max and Σ p: [bh][n_items][128 rows][2]
-    int* queue;                  // split work counter, reset before every launch
+    // Key-range split (16x16 kernel, small grids): the key tiles of all
+    // (head, query block) pairs, numbered head-major then block then tile,
+    // are cut into sk_wg contiguous equal shares, one per workgroup.
+    int sk_wg;                   // workgroups of the split grid (0: no split)
+    int sk_maxseg;               // partial slots per (head, query block)
+    long long sk_tiles;          // key tiles of all heads
+    int sk_head_tiles;           // key tiles of one head
+    float* part;                 // split partials Σ p·V: [bh][query block][sk_maxseg][128 rows][D]
+    float* ml;                   // split running max and Σ p, same slots: [..][128 rows][2]
     int o_heads;                 // 0: O is [bh, S, D]; H > 0: O is [B, S, H, D] (fused transpose)
 };
 
@@ -449,12 +453,35 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
 // With g.fold set, workgroup j runs block n-1-j and then block j: every
 // workgroup carries the same number of key tiles.
 //
-// Key-range split (g.ch > 0, small grids): work item = (query block q, chunk
-// c of g.ch key tiles), numbered q = n-1 .. 0 (heaviest first); a persistent
-// grid takes (item, head) pairs from the counter g.queue in the order item,
-// then head, so every CU stays busy until the last chunk.  Blocks with one
-// chunk write O; the others write partials to slot (head, item).  Every
-// workgroup leaves the loop once the counter passes the last pair.
+// Key-range split (g.sk_wg > 0, small grids): the key tiles of every (head,
+// query block) pair in order — head, then block 0 .. n-1, then tile — form
+// one sequence of sk_tiles tiles; workgroup w takes tiles
+// [sk_bound(w), sk_bound(w+1)), an equal share, so every CU carries the same
+// number of tiles whatever the causal block lengths.  A query block inside
+// one share writes O; a block cut by share boundaries is computed in
+// segments, segment j by the j-th workgroup that touches it, each writing
+// its partial to slot (head, block, j) for attn_split_merge.
+
+// First tile of workgroup w's share (sk_bound(sk_wg) = sk_tiles).
+__device__ __forceinline__ long long sk_bound(const AttnArgs& g, long long w) {
+    return w * g.sk_tiles / g.sk_wg;
+}
+
+// Workgroup whose share holds tile G.
+__device__ __forceinline__ long long sk_owner(const AttnArgs& g, long long G) {
+    long long w = G * g.sk_wg / g.sk_tiles;
+    while (w + 1 < g.sk_wg && sk_bound(g, w + 1) <= G) ++w;
+    while (w > 0 && sk_bound(g, w) > G) --w;
+    return w;
+}
+
+// First tile of query block qb within its head.
+__device__ __forceinline__ int sk_block_start(const AttnArgs& g, int qb, bool causal) {
+    int t = 0;
+    for (int b = 0; b < qb; ++b) t += attn16_tiles(g, b, causal);
+    return t;
+}
+
 template <int DP, bool CAUSAL, bool HAS_MASK>
 __global__ __launch_bounds__(A16_NT, 4) void attn_fwd_mfma16(AttnArgs g) {
     __shared__ float Ks[A16_KB][DP + 4];
@@ -475,40 +502,31 @@ template <int DP, bool CAUSAL, bool HAS_MASK>
 __global__ __launch_bounds__(A16_NT, 4) void attn_fwd_mfma16_split(AttnArgs g) {
     __shared__ float Ks[A16_KB][DP + 4];
     __shared__ float Vs[A16_KB][DP + 4];
-    __shared__ int next_work;
-    const long long total = (long long)g.n_items * g.n_bh;
-    for (;;) {
-        if (threadIdx.x == 0) next_work = atomicAdd(g.queue, 1);
-        __syncthreads();
-        const long long idx = next_work;
-        __syncthreads();
-        if (idx >= total) break;
-        int item = (int)(idx / g.n_bh);
-        const int bhi = (int)(idx - (long long)item * g.n_bh);
-        const int it0 = item;
-        int qb = g.n_qblocks - 1;
-        for (; qb > 0; --qb) {
-            const int nc = (attn16_tiles(g, qb, CAUSAL) + g.ch - 1) / g.ch;
-            if (item < nc) break;
-            item -= nc;
+    const long long w = blockIdx.x;
+    const long long end = sk_bound(g, w + 1);
+    long long G = sk_bound(g, w);
+    while (G < end) {
+        const long long bh = G / g.sk_head_tiles;
+        int t0 = (int)(G - bh * g.sk_head_tiles);
+        int qb = 0, nt = attn16_tiles(g, 0, CAUSAL);
+        while (t0 >= nt) {
+            t0 -= nt;
+            nt = attn16_tiles(g, ++qb, CAUSAL);
         }
-        const int nt = attn16_tiles(g, qb, CAUSAL);
-        const int nc = (nt + g.ch - 1) / g.ch;
-        const int t0 = item * g.ch, t1 = min(nt, t0 + g.ch);
-        const long long slot = nc > 1 ? (long long)bhi * g.n_items + it0 : -1;
-        attn16_qblock<DP, CAUSAL, HAS_MASK, true>(g, bhi, qb, t0, t1, slot, Ks, Vs);
+        const int t1 = (int)min((long long)nt, t0 + (end - G));
+        // a block cut by a share boundary: segment index = this workgroup − the owner of its first tile
+        const long long slot =
+            (t0 > 0 || t1 < nt) ? (bh * g.n_qblocks + qb) * g.sk_maxseg + (w - sk_owner(g, G - t0)) : -1;
+        attn16_qblock<DP, CAUSAL, HAS_MASK, true>(g, (int)bh, qb, t0, t1, slot, Ks, Vs);
+        G += t1 - t0;
     }
 }
 
-__global__ void attn_queue_reset(int* queue) {
-    if (threadIdx.x == 0) *queue = 0;
-}
-
 // Combine the key-range partials of every query row whose block was split:
-// O = Σ_c 2^(m_c − M)·acc_c / Σ_c 2^(m_c − M)·l_c, M = max_c m_c, chunks
-// summed in order.  One wavefront per row; rows of unsplit blocks return.
-// Thread t of a row handles d = 4t .. 4t+3 (D % 4 == 0 on this path), so a
-// row of hd = 128 takes 32 threads and every load and store is a float4.
+// O = Σ_c 2^(m_c − M)·acc_c / Σ_c 2^(m_c − M)·l_c, M = max_c m_c, segments
+// summed in key order.  Rows of unsplit blocks return.  Thread t of a row
+// handles d = 4t .. 4t+3 (D % 4 == 0 on this path), so a row of hd = 128
+// takes 32 threads and every load and store is a float4.
 __global__ __launch_bounds__(256) void attn_split_merge(AttnArgs g, int causal) {
     const int tpr = g.D / 4;                                    // threads per row
     const long long t = blockIdx.x * 256LL + threadIdx.x;
@@ -517,17 +535,11 @@ __global__ __launch_bounds__(256) void attn_split_merge(AttnArgs g, int causal) 
     const long long bh = blockIdx.y;
     if (row >= g.S) return;
     const int qb = (int)(row / A16_QB);
-    int first = 0, nc = 0;
-    for (int b = g.n_qblocks - 1; b >= 0; --b) {
-        const int n = (attn16_tiles(g, b, causal != 0) + g.ch - 1) / g.ch;
-        if (b == qb) {
-            nc = n;
-            break;
-        }
-        first += n;
-    }
+    const long long G0 = bh * g.sk_head_tiles + sk_block_start(g, qb, causal != 0);
+    const long long G1 = G0 + attn16_tiles(g, qb, causal != 0);
+    const int nc = (int)(sk_owner(g, G1 - 1) - sk_owner(g, G0)) + 1;
     if (nc <= 1) return;
-    const long long r0 = (bh * g.n_items + first) * A16_QB + (row - (long long)qb * A16_QB);
+    const long long r0 = (bh * g.n_qblocks + qb) * g.sk_maxseg * A16_QB + (row - (long long)qb * A16_QB);
     float M = -FLT_MAX;
     for (int c = 0; c < nc; ++c) M = fmaxf(M, g.ml[2 * (r0 + (long long)c * A16_QB)]);
     float L = 0.f;
@@ -591,8 +603,9 @@ __global__ __launch_bounds__(256) void attn_fwd_rows(AttnArgs g, int causal) {
 }
 
 // Step::i: [0]=bh [1]=S [2]=D [3]=causal [4]=group [5]=DP (0 = row fallback)
-//          [6]=fold [7]=split chunk tiles (0 = none) [8]=split work items per head
+//          [6]=fold [7]=split workgroups (0 = none) [8]=split partial slots per (head, block)
 //          [9]=heads of a fused output transpose (0 = none) [10]=16x16 kernel (transpose fusable)
+//          [11]=key tiles per head (split)
 AttnArgs make_args(const Step& s) {
     AttnArgs g;
     g.Q = (const float*)s.in[0];
@@ -632,39 +645,56 @@ void launch_attn16(const Step& s, hipStream_t st) {
     g.n_qblocks = (g.S + A16_QB - 1) / A16_QB;
     g.fold = CAUSAL && s.i[6] != 0;
     g.o_heads = (int)s.i[9];
-    g.ch = (int)s.i[7];
-    g.n_items = (int)s.i[8];
-    g.n_bh = (int)s.i[0];
-    if (g.ch > 0) {
-        // workspace: partials, then (m, l) pairs, then the work counter
-        const long long rows = (long long)g.n_items * s.i[0] * A16_QB;
+    g.sk_wg = (int)s.i[7];
+    g.sk_maxseg = (int)s.i[8];
+    g.sk_head_tiles = (int)s.i[11];
+    g.sk_tiles = s.i[11] * s.i[0];
+    if (g.sk_wg > 0) {
+        // workspace: partials, then (m, l) pairs
+        const long long rows = s.i[0] * g.n_qblocks * (long long)g.sk_maxseg * A16_QB;
         g.part = (float*)s.ws;
         g.ml = g.part + rows * g.D;
-        g.queue = (int*)(g.ml + rows * 2);
-        const long long total = (long long)g.n_items * s.i[0];
-        const long long slots = 2LL * (lbr_device_cus() > 0 ? lbr_device_cus() : 256);
-        hipLaunchKernelGGL(attn_queue_reset, dim3(1), dim3(64), 0, st, g.queue);
-        hipLaunchKernelGGL((attn_fwd_mfma16_split<DP, CAUSAL, HAS_MASK>), dim3((unsigned)std::min(total, slots), 1),
-                           dim3(A16_NT), 0, st, g);
+        hipLaunchKernelGGL((attn_fwd_mfma16_split<DP, CAUSAL, HAS_MASK>), dim3((unsigned)g.sk_wg), dim3(A16_NT), 0, st,
+                           g);
         hipLaunchKernelGGL(attn_split_merge, dim3((unsigned)(((long long)g.S * (g.D / 4) + 255) / 256), (unsigned)s.i[0]),
                            dim3(256), 0, st, g, (int)CAUSAL);
         return;
     }
     g.part = g.ml = nullptr;
-    g.queue = nullptr;
     const unsigned gx = g.fold ? (unsigned)(g.n_qblocks + 1) / 2 : (unsigned)g.n_qblocks;
     hipLaunchKernelGGL((attn_fwd_mfma16<DP, CAUSAL, HAS_MASK>), dim3(gx, (unsigned)s.i[0]), dim3(A16_NT), 0, st, g);
 }
 
-// Work items of a key-range split with `ch` tiles per chunk (one head).
-long long attn16_items(int S, bool causal, int ch) {
-    const int nt = (S + A16_KB - 1) / A16_KB, nq = (S + A16_QB - 1) / A16_QB;
-    long long items = 0;
-    for (int q = 0; q < nq; ++q) {
-        const int t = causal ? std::min(nt, std::min(S - 1, q * A16_QB + A16_QB - 1) / A16_KB + 1) : nt;
-        items += (t + ch - 1) / ch;
+// Key tiles of query block q (host mirror of attn16_tiles).
+int attn16_block_tiles(int S, bool causal, int q) {
+    const int nt = (S + A16_KB - 1) / A16_KB;
+    return causal ? std::min(nt, std::min(S - 1, q * A16_QB + A16_QB - 1) / A16_KB + 1) : nt;
+}
+
+// Key-range split of `bh` heads over `wg` workgroups (host mirror of
+// sk_bound / sk_owner): the largest number of segments any (head, query
+// block) is cut into, i.e. the partial slots each pair needs.
+int attn16_max_segments(int S, bool causal, long long bh, long long wg) {
+    const int nq = (S + A16_QB - 1) / A16_QB;
+    long long head = 0;
+    for (int q = 0; q < nq; ++q) head += attn16_block_tiles(S, causal, q);
+    const long long total = head * bh;
+    auto owner = [&](long long G) {
+        long long w = G * wg / total;
+        while (w + 1 < wg && (w + 1) * total / wg <= G) ++w;
+        while (w > 0 && w * total / wg > G) --w;
+        return w;
+    };
+    long long best = 1;
+    for (long long h = 0; h < bh; ++h) {
+        long long G = h * head;
+        for (int q = 0; q < nq; ++q) {
+            const int t = attn16_block_tiles(S, causal, q);
+            best = std::max(best, owner(G + t - 1) - owner(G) + 1);
+            G += t;
+        }
     }
-    return items;
+    return (int)best;
 }
 
 template <int DP>
@@ -731,25 +761,33 @@ int decode_attention(const OpNode* n, Step* s) {
             const char* fold = getenv("LBR_ATTN_FOLD");
             if (fold) s->i[6] = causal && atoi(fold) != 0;
             // Grids that leave CUs idle (fewer than two 8-wavefront workgroups per
-            // CU, not folded) split each query block's key range into chunks of
-            // 8 tiles (256 keys; 4 when that still leaves fewer work items than
-            // CUs), fed to a persistent grid through a work counter, when that
-            // gives at least half again as many work items as blocks.  Measured
-            // on Qwen3 and GPT-2 S=1024, 8 beat 1, 2, 4 and 16: smaller chunks
-            // pay the per-item Q load, first-tile latency and larger partials.
-            // LBR_ATTN_SPLIT=<ch> forces a chunk size (0: no split).
-            int ch = 0;
+            // CU, not folded) take the key-range split: two workgroups per CU with
+            // equal shares of all key tiles, shares of at least 8 tiles (4 for
+            // hd <= 64) since every segment pays a Q load, the first tile's
+            // latency and, when cut, a partial; no split when that gives no more
+            // workgroups than the plain grid.  LBR_ATTN_SPLIT=<n> forces shares
+            // of n tiles (0: no split).
+            long long head_tiles = 0;
+            for (int q = 0; q < nq; ++q) head_tiles += attn16_block_tiles(seq, causal != 0, q);
+            const long long total = head_tiles * bh;
+            long long wg = 0;
             if (!s->i[6] && nq * bh < 2LL * cus) {
-                const int c = attn16_items(seq, causal, 8) * bh >= cus ? 8 : 4;
-                if (attn16_items(seq, causal, c) * 2 >= 3 * nq) ch = c;
+                const int min_share = hd <= 64 ? 4 : 8;
+                wg = std::min(2LL * cus, total / min_share);
+                if (wg <= nq * bh) wg = 0;
             }
             const char* split = getenv("LBR_ATTN_SPLIT");
-            if (split) ch = std::max(0, atoi(split));
-            if (ch > 0 && !s->i[6]) {
-                const long long items = attn16_items(seq, causal, ch);
-                s->i[7] = ch;
-                s->i[8] = items;
-                s->ws_bytes = (size_t)(items * bh * A16_QB) * (size_t)(hd + 2) * sizeof(float) + 256;
+            if (split) {
+                const long long n = atoi(split);
+                wg = n > 0 ? (total + n - 1) / n : 0;
+            }
+            wg = std::min(wg, total);   // every share holds at least one tile
+            if (wg > 0 && !s->i[6]) {
+                const int maxseg = attn16_max_segments(seq, causal != 0, bh, wg);
+                s->i[7] = wg;
+                s->i[8] = maxseg;
+                s->i[11] = head_tiles;
+                s->ws_bytes = (size_t)(bh * nq * maxseg * A16_QB) * (size_t)(hd + 2) * sizeof(float) + 256;
             }
             switch (dp) {
                 case 32: s->run = pick16<32>(causal, has_mask); break;

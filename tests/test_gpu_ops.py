@@ -156,6 +156,8 @@ ATTN_CASES = [
     (1, 2, 33, 12, False, 1),       # hd % 8 != 0 → row fallback kernel
     (1, 2, 200, 256, True, 1),      # hd > 128 → 32x32 MFMA kernel
     (1, 3, 70, 160, False, 1),      # hd > 128, padded to 256
+    (1, 32, 1024, 128, True, 4),    # Qwen3-4B attention: small grid → key-range split
+    (1, 12, 1024, 64, True, 1),     # GPT-2 attention: split with 4-tile shares
 ]
 
 
@@ -180,14 +182,16 @@ def test_attention(B, H, S, hd, causal, group):
 # Kernel-selection overrides read when the plan is built: LBR_ATTN_FOLD=1
 # forces the paired causal schedule (workgroup j runs query blocks n-1-j and
 # j; odd n leaves the middle block alone), LBR_ATTN_TILE=32 the 32x32 kernel,
-# LBR_ATTN_SPLIT=c the key-range split with c tiles (32 keys) per chunk plus
-# the merge kernel (c=1: every tile its own chunk; c=3: chunks that do not
-# divide a block's tile count).
+# LBR_ATTN_SPLIT=c the key-range split: every workgroup an equal share of c
+# key tiles (32 keys) of the whole (head, query block, tile) sequence, plus
+# the merge kernel (c=1: every tile its own segment; c=3, 7: shares that cut
+# blocks at varying offsets and span several blocks and heads).
 @pytest.mark.parametrize("env", [{"LBR_ATTN_FOLD": "1"}, {"LBR_ATTN_TILE": "32"},
                                  {"LBR_ATTN_SPLIT": "1", "LBR_ATTN_FOLD": "0"},
                                  {"LBR_ATTN_SPLIT": "3", "LBR_ATTN_FOLD": "0"},
+                                 {"LBR_ATTN_SPLIT": "7", "LBR_ATTN_FOLD": "0"},
                                  {"LBR_ATTN_SPLIT": "8", "LBR_ATTN_FOLD": "0"}],
-                         ids=["fold", "tile32", "split1", "split3", "split8"])
+                         ids=["fold", "tile32", "split1", "split3", "split7", "split8"])
 @pytest.mark.parametrize("B,H,S,hd,causal,group", [
     (1, 4, 257, 128, True, 1),      # 3 query blocks: pair (2, 0) and the middle block 1 alone
     (1, 8, 512, 64, True, 2),       # 4 query blocks: pairs (3, 0), (2, 1)
