@@ -163,6 +163,11 @@ int lbr_plan_node_kernel(const lbr_plan* plan, int index, char* name_out,
                                      (7-node rotate-half window) as one kernel                  */
 #define LBR_FUSE_ATTN_TRANSPOSE 4 /* ATTENTION → TRANSPOSE(H,S): the attention kernel writes
                                      its output as [B, S, H, hd]                                */
+#define LBR_FUSE_GEMM_ACT      5  /* MATMUL[_ADD] → RELU | GELU | SILU: the activation is
+                                     applied in the GEMM epilogue                               */
+#define LBR_FUSE_GEMM_GATED    6  /* MATMUL[_ADD] (N = 2F) → SLICE [0,F) → SLICE [F,2F) →
+                                     GATED_ACT: the GEMM pairs gate and up columns in each tile
+                                     and writes act(gate)·up as [M, F]                           */
 
 typedef struct {
     int first;   /* index of the run's first node */

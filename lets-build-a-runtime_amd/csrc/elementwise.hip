@@ -18,12 +18,9 @@ namespace {
 
 enum UnaryKind { U_RELU, U_EXP, U_TANH, U_POW, U_GELU, U_RSQRT, U_SILU, U_NEG, U_COS, U_SIN };
 
-__device__ __forceinline__ float gelu_tanh(float x) {
-    // 0.5·x·(1 + tanh(√(2/π)·(x + 0.044715·x³)))  (elementwise.c:185-190)
-    return 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
-}
+__device__ __forceinline__ float gelu_tanh(float x) { return lbr_gelu_tanh(x); }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float silu(float x) { return lbr_silu(x); }
 
 template <int K>
 __device__ __forceinline__ float unary_apply(float x, float s) {

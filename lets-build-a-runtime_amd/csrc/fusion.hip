@@ -28,6 +28,14 @@
 //               MUL sin, ADD]: one wavefront per (token, head) row.
 //   ATTN_TRANSPOSE  ATTENTION → TRANSPOSE(H,S): the attention kernel stores
 //               its rows straight into [B, S, H, hd].
+//   GEMM_ACT    MATMUL[_ADD] → RELU | GELU | SILU: the activation runs in the
+//               GEMM epilogue (the FFN's first projection).
+//   GEMM_GATED  MATMUL[_ADD] with 2F columns → SLICE [0,F) and SLICE [F,2F)
+//               → GATED_ACT(gate, [bias], up): the GEMM fetches gate and up
+//               weight rows interleaved in blocks of 16 columns, so each lane
+//               holds both values of an output element, and writes
+//               act(gate)·up as [M, F] (the merged gate/up projection of a
+//               SiLU-gated FFN).
 #include "lbr_device.h"
 
 #include <math.h>
@@ -433,6 +441,75 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
                     continue;
                 }
             }
+            // GEMM_GATED: C [rows, 2F] → SLICE(C, last dim) × 2 → GATED_ACT(gate, [bias], up), one
+            // slice the column half [0, F) and the other [F, 2F); DMA kernel, one batch, no K split
+            if (gs.i[14] && gs.i[3] == 1 && gs.i[10] <= 1 && gs.i[1] % 2 == 0 && i + 3 < n && is_f32(nd)) {
+                const long long rows = gs.i[0];
+                const int N = (int)gs.i[1], F = N / 2;
+                const OpNode* s1 = &nodes[i + 1];
+                const OpNode* s2 = &nodes[i + 2];
+                const OpNode* ga = &nodes[i + 3];
+                auto half = [&](const OpNode* sl) {   // column offset of a half slice of C, or -1
+                    if (sl->op != OP_SLICE || sl->n_inputs < 1 || sl->inputs[0] != nd->output || !is_f32(sl) ||
+                        sl->extra[0] != rows || sl->extra[1] != N || sl->extra[3] != F || sl->extra[4] != 1)
+                        return -1;
+                    return (sl->extra[2] == 0 || sl->extra[2] == F) ? sl->extra[2] : -1;
+                };
+                const int h1 = half(s1), h2 = half(s2);
+                if (h1 >= 0 && h2 >= 0 && h1 != h2 && ga->op == OP_GATED_ACT && is_f32(ga) && ga->n_inputs >= 2 &&
+                    node_total(ga) == rows * F && (ga->extra[1] == 0 || ga->extra[1] == 1)) {
+                    const bool hb = ga->extra[0] != 0;
+                    const void* x = ga->inputs[0];
+                    const void* up = hb ? ga->inputs[2] : ga->inputs[1];
+                    const void* gb = hb ? ga->inputs[1] : nullptr;
+                    int gate_base = -1;
+                    if (x == s1->output && up == s2->output) gate_base = h1;
+                    if (x == s2->output && up == s1->output) gate_base = h2;
+                    if (gate_base >= 0 && !(hb && ga->n_inputs < 3)) {
+                        const Rng y = out_rng(ga);
+                        std::vector<Rng> reads = gin;
+                        if (gb) reads.push_back(rng(gb, (long long)F * 4));
+                        bool ok = !any_overlap(y, reads);
+                        if (ok) ok = dead_after(nodes, n, i + 4, {c_r, out_rng(s1), out_rng(s2)}, {y}, live);
+                        if (ok) {
+                            FusedRun f;
+                            f.first = i;
+                            f.count = 4;
+                            f.kind = LBR_FUSE_GEMM_GATED;
+                            f.gF = F;
+                            f.gate_base = gate_base;
+                            f.gact = ga->extra[1];
+                            f.gbias = gb;
+                            f.out = ga->output;
+                            out->push_back(f);
+                            i += 4;
+                            continue;
+                        }
+                    }
+                }
+            }
+            // GEMM_ACT: C → RELU | GELU | SILU (DMA kernel)
+            if (gs.i[14] && i + 1 < n) {
+                const OpNode* ac = &nodes[i + 1];
+                const int act = ac->op == OP_RELU ? LBR_ACT_RELU
+                              : ac->op == OP_GELU ? LBR_ACT_GELU
+                              : ac->op == OP_SILU ? LBR_ACT_SILU : LBR_ACT_NONE;
+                if (act != LBR_ACT_NONE && ac->n_inputs >= 1 && ac->inputs[0] == nd->output && is_f32(ac) &&
+                    is_f32(nd) && node_total(ac) == node_total(nd)) {
+                    const Rng y = out_rng(ac);
+                    if (!any_overlap(y, gin) && dead_after(nodes, n, i + 2, {c_r}, {y}, live)) {
+                        FusedRun f;
+                        f.first = i;
+                        f.count = 2;
+                        f.kind = LBR_FUSE_GEMM_ACT;
+                        f.act = act;
+                        f.out = ac->output;
+                        out->push_back(f);
+                        i += 2;
+                        continue;
+                    }
+                }
+            }
             // GEMM_RESID
             if (i + 1 < n) {
                 const OpNode* ad = &nodes[i + 1];
@@ -559,6 +636,25 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
         s->out = (void*)f.out;
         s->i[9] = f.Hs[0];
         s->name = "attn_fwd_mfma16_f32+transpose";
+    } else if (f.kind == LBR_FUSE_GEMM_ACT || f.kind == LBR_FUSE_GEMM_GATED) {
+        int rc = decode_matmul(&nodes[f.first], s);
+        if (rc) return rc;
+        if (!s->i[14] || (f.kind == LBR_FUSE_GEMM_GATED && (s->i[10] > 1 || s->i[3] != 1))) {
+            lbr_set_error("fusion: GEMM node %d is not on the DMA path without a K split", f.first);
+            return LBR_ERR_INVALID;
+        }
+        s->out = (void*)f.out;
+        if (f.kind == LBR_FUSE_GEMM_ACT) {
+            s->i[31] = f.act;
+            s->i[12] = s->i[12] && lbr_aligned(f.out, 16);
+            s->name = "gemm_dma_f32_nt+act";
+        } else {
+            s->i[32] = f.gF;
+            s->i[33] = f.gact;
+            s->i[34] = f.gate_base;
+            s->in[3] = f.gbias;
+            s->name = "gemm_dma_f32_nt+gated";
+        }
     } else if (f.kind == LBR_FUSE_GEMM_RESID || f.kind == LBR_FUSE_GEMM_HEADS) {
         int rc = decode_matmul(&nodes[f.first], s);
         if (rc) return rc;

@@ -58,6 +58,14 @@ struct GemmArgs {
     float* dst[4];            // split k's output, laid out [B, H, S, hd]
     const float* sbias[4];    // split k's bias row (indexed by column - col_begin[k]) or null
     int Hs[4], hd, S;         // heads of each split, head dim, rows per batch (M = B·S)
+    int act;                  // LBR_ACT_*: a following RELU / GELU / SILU applied to C (DMA kernel)
+    // Gated pair (DMA kernel): the GEMM's columns hold a gate half and an up half
+    // of gF columns each; the kernel writes out[m][j] = act(gate[m][j] (+ gbias[j]))·up[m][j]
+    // to C as [M, gF]
+    int gF;                   // 0: off
+    int gbase;                // first column of the gate half (0 or gF; up is the other half)
+    int gact;                 // 0: SiLU, 1: GELU (GATED_ACT extras[1])
+    const float* gbias;       // GATED_ACT bias (applied to gate) or null
 };
 
 // Final store of one C element (row m, column n of batch bz) with the fused
@@ -443,7 +451,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
 #pragma unroll
     for (int t = 0; t < IB; ++t) {
         const int row = wave * (TN / NW) + t * RPI + dr;
-        offB[t] = (unsigned)(min(n0 + row, N - 1) * K + ((dp ^ dr) * 4)) * 4u;
+        int brow = min(n0 + row, N - 1);
+        if (g.gF) {
+            // gated pair: tile column blocks of 16 alternate gate, up for the same
+            // TN/2 output columns starting at tn·TN/2 (clamped to the last one)
+            const int jb = row >> 4;
+            const int o = min(tn * (TN / 2) + (jb >> 1) * 16 + (row & 15), g.gF - 1);
+            brow = (jb & 1) ? (g.gbase ? 0 : g.gF) + o : g.gbase + o;
+        }
+        offB[t] = (unsigned)(brow * K + ((dp ^ dr) * 4)) * 4u;
     }
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(g.A + bz * g.sA), (short)0, M * K * 4, 0x00020000);
@@ -583,6 +599,34 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
         }
         return;
     }
+    if (g.gF) {
+        // gated pair: blocks j (gate) and j+1 (up) of this wave hold the same 16
+        // output columns; out = act(gate (+ gated bias))·up, rounded like the
+        // unfused GEMM → SLICE → GATED_ACT chain
+        const int F = g.gF;
+        float* __restrict__ C = g.C + bz * (long long)M * F;
+#pragma unroll
+        for (int j = 0; j < FN; j += 2) {
+            const int o = tn * (TN / 2) + ((wn * FN + j) >> 1) * 16 + cl;
+            if (o >= F) continue;
+            const float bg = HAS_BIAS ? g.bias[g.gbase + o] : 0.f;
+            const float bu = HAS_BIAS ? g.bias[(g.gbase ? 0 : F) + o] : 0.f;
+            const float gb = g.gbias ? g.gbias[o] : 0.f;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = mw + i * 16 + rq + r;
+                    if (m >= M) continue;
+                    float x = HAS_BIAS ? (acc[i][j][r] + bg) : g.alpha * acc[i][j][r];
+                    const float u = HAS_BIAS ? (acc[i][j + 1][r] + bu) : g.alpha * acc[i][j + 1][r];
+                    if (g.gbias) x = x + gb;
+                    const float a = g.gact == 0 ? lbr_silu(x) : lbr_gelu_tanh(x);
+                    C[(long long)m * F + o] = a * u;
+                }
+        }
+        return;
+    }
     float* __restrict__ C = g.C + bz * g.sC;
     const float* __restrict__ R = g.resid ? g.resid + bz * g.sC : nullptr;
 #pragma unroll
@@ -606,7 +650,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
                 if (m >= M) continue;
                 float v = HAS_BIAS ? (acc[i][j][r] + bv) : g.alpha * acc[i][j][r];
                 if (R) v = v + rv[r];
-                C[(long long)m * N + n] = v;
+                C[(long long)m * N + n] = lbr_act(g.act, v);   // a fused activation never comes with resid
             }
         }
     }
@@ -658,7 +702,8 @@ __global__ __launch_bounds__(256) void gemv_n(GemmArgs g) {
 
 // Step::i: [0]=M [1]=N [2]=K [3]=batches [4]=trans_b [5]=vec [6]=has_bias
 //          [7]=sA [8]=sB [9]=sC [10]=ksplit [11]=kchunk [12]=float4 reduce
-//          [13]=1 (takes fused epilogues) [14]=DMA tile + 1 (0: gemm_mfma_f32) ; f[0] = alpha
+//          [13]=1 (takes fused epilogues) [14]=DMA tile + 1 (0: gemm_mfma_f32)
+//          [19..30] head scatter, [31] activation, [32..34] gated pair (see below) ; f[0] = alpha
 GemmArgs make_args(const Step& s) {
     GemmArgs g;
     g.A = (const float*)s.in[0];
@@ -677,10 +722,15 @@ GemmArgs make_args(const Step& s) {
     g.ksplit = s.i[10] > 1 ? (int)s.i[10] : 1;
     g.kchunk = g.ksplit > 1 ? (int)s.i[11] : g.K;
     g.W = (float*)s.ws;
-    // fused epilogue: in[3] = resid; i[19] = n_split, i[20..24] = col_begin,
-    // in[4..7] = dst, in[8..11] = split biases, i[25..28] = heads per split,
-    // i[29] = hd, i[30] = S
-    g.resid = (const float*)s.in[3];
+    // fused epilogue: in[3] = resid (gated pair: the GATED_ACT bias);
+    // i[19] = n_split, i[20..24] = col_begin, in[4..7] = dst, in[8..11] =
+    // split biases, i[25..28] = heads per split, i[29] = hd, i[30] = S;
+    // i[31] = act; i[32] = gated F, i[33] = gated act, i[34] = gate half's first column
+    g.gF = (int)s.i[32];
+    g.gact = (int)s.i[33];
+    g.gbase = (int)s.i[34];
+    g.resid = g.gF ? nullptr : (const float*)s.in[3];
+    g.gbias = g.gF ? (const float*)s.in[3] : nullptr;
     g.n_split = (int)s.i[19];
     for (int k = 0; k < 5; ++k) g.col_begin[k] = (int)s.i[20 + k];
     for (int k = 0; k < 4; ++k) {
@@ -690,6 +740,7 @@ GemmArgs make_args(const Step& s) {
     }
     g.hd = (int)s.i[29];
     g.S = (int)s.i[30];
+    g.act = (int)s.i[31];
     return g;
 }
 
@@ -715,6 +766,10 @@ __global__ void splitk_reduce(GemmArgs g, long long total) {
             } else {
                 s.x *= g.alpha; s.y *= g.alpha; s.z *= g.alpha; s.w *= g.alpha;
             }
+            if (g.act) {
+                s.x = lbr_act(g.act, s.x); s.y = lbr_act(g.act, s.y);
+                s.z = lbr_act(g.act, s.z); s.w = lbr_act(g.act, s.w);
+            }
             if (g.resid) {
                 const float4 r = reinterpret_cast<const float4*>(g.resid)[i];
                 s.x = s.x + r.x; s.y = s.y + r.y; s.z = s.z + r.z; s.w = s.w + r.w;
@@ -727,7 +782,7 @@ __global__ void splitk_reduce(GemmArgs g, long long total) {
              i += (long long)gridDim.x * blockDim.x) {
             float s = W[i];
             for (int k = 1; k < ksplit; ++k) s += W[(long long)k * total + i];
-            s = HAS_BIAS ? s + g.bias[i % N] : g.alpha * s;
+            s = lbr_act(g.act, HAS_BIAS ? s + g.bias[i % N] : g.alpha * s);
             const long long bz = i / MN, r = i - bz * MN;
             epi_store(g, bz, (int)(r / N), (int)(r % N), s);
         }
@@ -759,7 +814,8 @@ void launch_gemm_dma(const Step& s, hipStream_t st) {
     GemmArgs g = make_args(s);
     if (g.M <= 0 || g.N <= 0) return;
     g.tiles_m = (g.M + TM - 1) / TM;
-    g.tiles_n = (g.N + TN - 1) / TN;
+    // a gated pair's tile covers TN/2 output columns (TN/2 gate + TN/2 up columns of C)
+    g.tiles_n = g.gF ? (g.gF + TN / 2 - 1) / (TN / 2) : (g.N + TN - 1) / TN;
     dim3 grid(g.tiles_m * g.tiles_n, g.ksplit, (unsigned)s.i[3]);
     hipLaunchKernelGGL((gemm_dma_f32<TM, TN, WGM, WGN, OCC, HAS_BIAS>), grid, dim3(64 * WGM * WGN), 0, st, g);
     if (g.ksplit > 1) launch_splitk_reduce<HAS_BIAS>(s, g, st);

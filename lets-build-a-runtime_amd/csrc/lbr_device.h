@@ -16,6 +16,39 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 // ---------------------------------------------------------------------------
+// Activations, shared by the element-wise kernels and the GEMM epilogues so
+// a fused epilogue rounds exactly like the separate node would.
+// ---------------------------------------------------------------------------
+
+// 0.5·x·(1 + tanh(z)), z = √(2/π)·(x + 0.044715·x³)  (elementwise.c:185-190),
+// evaluated in its sigmoid form: 0.5·(1 + tanh(z)) = 1/(1 + e^(−2z)), so
+// GELU(x) = x / (1 + e^(−2z)) — the hardware exp2 and reciprocal (about 1
+// ulp each) instead of a tanh; e^(−2z) overflowing to inf gives ∓0,
+// underflowing to 0 gives x.
+__device__ __forceinline__ float lbr_gelu_tanh(float x) {
+    const float z = 0.7978845608f * (x + 0.044715f * x * x * x);
+    return x * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * z));
+}
+
+// x·σ(x) = x / (1 + e^(−x)), same evaluation
+__device__ __forceinline__ float lbr_silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+// GEMM epilogue activation codes (fused MATMUL → RELU / GELU / SILU)
+#define LBR_ACT_NONE 0
+#define LBR_ACT_RELU 1
+#define LBR_ACT_GELU 2
+#define LBR_ACT_SILU 3
+
+__device__ __forceinline__ float lbr_act(int act, float v) {
+    switch (act) {
+        case LBR_ACT_RELU: return v > 0.0f ? v : 0.0f;
+        case LBR_ACT_GELU: return lbr_gelu_tanh(v);
+        case LBR_ACT_SILU: return lbr_silu(v);
+        default: return v;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Wave / block reductions (64-lane wavefronts)
 // ---------------------------------------------------------------------------
 

@@ -28,6 +28,12 @@ struct FusedRun {
     const void* cos = nullptr;
     const void* sin = nullptr;
     long long cst[3] = {0, 0, 0}, sst[3] = {0, 0, 0};
+    // GEMM_ACT: LBR_ACT_* applied to C
+    int act = 0;
+    // GEMM_GATED: F output columns, gate half at columns [gate_base, gate_base + F),
+    // GATED_ACT's act code and bias (`out` is the GATED_ACT output)
+    int gF = 0, gate_base = 0, gact = 0;
+    const void* gbias = nullptr;
 };
 
 // Fusable runs of nodes[0..n) in stream order; live-out ranges are the

@@ -35,7 +35,8 @@ class LbrWindow(ctypes.Structure):
     _fields_ = [("first", ctypes.c_int), ("count", ctypes.c_int), ("kind", ctypes.c_int)]
 
 
-FUSE_KINDS = {0: "none", 1: "gemm_resid", 2: "gemm_heads", 3: "head_prologue", 4: "attn_transpose"}
+FUSE_KINDS = {0: "none", 1: "gemm_resid", 2: "gemm_heads", 3: "head_prologue", 4: "attn_transpose",
+              5: "gemm_act", 6: "gemm_gated"}
 
 
 class HipLibrary:

@@ -56,22 +56,28 @@ def _workload_nodes(key: str, seq: int):
 EXPECTED = {
     # merged QKV → three (slice, bias add, transpose) chains in the GEMM epilogue; the O-proj residual
     # add writes over the GEMM's own A input (refused), the FFN2 one fuses
-    "toy": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1}),
-    "gpt2w": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1}),
-    "7b4k": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1}),
+    # FFN1 → GELU runs in the GEMM epilogue
+    "toy": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1}),
+    "gpt2w": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1}),
+    "7b4k": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1}),
     # c_attn is MATMUL_ADD (bias already in the GEMM): three (slice, transpose) chains per layer
-    "gpt2": Counter({("gemm_heads", 7): 2, ("gemm_resid", 2): 4}),
+    "gpt2": Counter({("gemm_heads", 7): 2, ("gemm_resid", 2): 4, ("gemm_act", 2): 2}),
     # q/k: slice → per-head RMSNorm → transpose → 7-node RoPE as one kernel; v's transpose lands
     # over the QKV rows it reads at this size (refused); the attention output transpose is fused
-    # here, while in the other workloads the planner places it over the dead V (refused)
+    # here, while in the other workloads the planner places it over the dead V (refused); at
+    # S=64 the gated FFN output lands over the gate/up GEMM's input (refused)
     "qwen3_4b": Counter({("head_prologue", 10): 4, ("gemm_resid", 2): 4, ("attn_transpose", 2): 2}),
+    # at the benchmark length the merged gate/up GEMM → two half slices → SiLU gate is one GEMM
+    "qwen3_4b@1024": Counter({("head_prologue", 10): 4, ("gemm_resid", 2): 4, ("attn_transpose", 2): 2,
+                              ("gemm_gated", 4): 2}),
 }
 
 
 @pytest.mark.parametrize("key", list(EXPECTED))
 def test_workload_fusion_windows(key):
     lib = _lib()
-    arr, order, live = _workload_nodes(key, 64)
+    name, _, seq = key.partition("@")
+    arr, order, live = _workload_nodes(name, int(seq) if seq else 64)
     wins = lib.fusion_windows(arr, len(order), live)
     assert Counter((kind, count) for _, count, kind in wins) == EXPECTED[key]
     # runs are disjoint, in order, inside the array
@@ -270,3 +276,71 @@ def test_attention_transpose_refuses_output_over_v():
 def test_attention_transpose_needs_the_16x16_kernel():
     # head dim 256 runs the 32x32 kernel, which writes [bh, S, hd] only
     assert _windows(_attn_transpose(40 * MB, hd=256)) == []
+
+
+# ------------------------------------------------------------ activation epilogues
+
+def _gemm_act(c_off, y_off, a_ptr=A_, op=OpType.GELU, k=K, later=()):
+    """MATMUL A·Wᵀ → C, activation(C) → Y, then `later` nodes."""
+    mm = _node(OpType.MATMUL, [a_ptr, W_], ARENA + c_off, (1, M, N), (k, 1, 1, 0))
+    ac = _node(op, [ARENA + c_off], ARENA + y_off, (1, M, N))
+    return [mm, ac, *later]
+
+
+def test_gemm_act_fuses():
+    for op in (OpType.RELU, OpType.GELU, OpType.SILU):
+        assert _windows(_gemm_act(0, 4 * MB, op=op)) == [(0, 2, "gemm_act")]
+    # in place over the dead C
+    assert _windows(_gemm_act(0, 0)) == [(0, 2, "gemm_act")]
+    # only RELU, GELU and SILU have an epilogue form
+    assert _windows(_gemm_act(0, 4 * MB, op=OpType.TANH)) == []
+
+
+def test_gemm_act_refusals():
+    # Y over the GEMM's A input
+    assert _windows(_gemm_act(0, 4 * MB, a_ptr=ARENA + 4 * MB)) == []
+    # C read by a later node, or C a graph output
+    reader = _node(OpType.RELU, [ARENA + 64], ARENA + 16 * MB, (16,))
+    assert _windows(_gemm_act(0, 4 * MB, later=[reader])) == []
+    assert _windows(_gemm_act(0, 4 * MB), live=[(ARENA, 4)]) == []
+    # K % 32 != 0 keeps the register-staged kernel, which has no activation epilogue
+    assert _windows(_gemm_act(0, 4 * MB, k=K + 4)) == []
+
+
+F = 192   # gated pair: output columns
+
+
+def _gated(y_off, order=(0, 1), a_ptr=A_, bias=False, act=0, later=(), halves=(0, F)):
+    """MATMUL → C [1, M, 2F]; SLICE(C) at columns halves[0] and halves[1]; GATED_ACT(x, [b], up)
+    with x, up the slices picked by `order`."""
+    C = ARENA
+    mm = _node(OpType.MATMUL, [a_ptr, W_], C, (1, M, 2 * F), (K, 1, 1, 0))
+    s = [_node(OpType.SLICE, [C], ARENA + (8 + k) * MB, (1, M, F), (M, 2 * F, halves[k], F, 1)) for k in (0, 1)]
+    x, up = s[order[0]].output, s[order[1]].output
+    ins = [x, EXT + (6 << 32), up] if bias else [x, up]
+    ga = _node(OpType.GATED_ACT, ins, ARENA + y_off, (1, M, F), (int(bias), act))
+    return [mm, s[0], s[1], ga, *later]
+
+
+def test_gemm_gated_fuses():
+    assert _windows(_gated(16 * MB)) == [(0, 4, "gemm_gated")]
+    # the gate is the upper half
+    assert _windows(_gated(16 * MB, order=(1, 0))) == [(0, 4, "gemm_gated")]
+    assert _windows(_gated(16 * MB, bias=True, act=1)) == [(0, 4, "gemm_gated")]
+    # output over the dead C and slices
+    assert _windows(_gated(0)) == [(0, 4, "gemm_gated")]
+
+
+def test_gemm_gated_refusals():
+    # output over the GEMM's A input (the Qwen3 LM plan places it there)
+    assert _windows(_gated(16 * MB, a_ptr=ARENA + 16 * MB)) == []
+    # a slice read by a later node, or a graph output
+    reader = _node(OpType.RELU, [ARENA + 8 * MB], ARENA + 40 * MB, (16,))
+    assert _windows(_gated(16 * MB, later=[reader])) == []
+    assert _windows(_gated(16 * MB), live=[(ARENA + 9 * MB, 4)]) == []
+    # slices that are not the two halves of C
+    assert _windows(_gated(16 * MB, halves=(0, 64))) == []
+    # output over the gated bias
+    nodes = _gated(16 * MB, bias=True)
+    nodes[3].inputs[1] = ARENA + 16 * MB + 64
+    assert _windows(nodes) == []

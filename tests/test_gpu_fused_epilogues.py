@@ -1,0 +1,123 @@
+"""Fused GEMM epilogues on the GPU, through the compiled executor:
+
+* MATMUL[_ADD] → RELU / GELU / SILU, the activation applied in the GEMM
+  epilogue (or in the split-K reduction), and
+* the gated pair MATMUL[_ADD] with 2F columns → SLICE [0,F) and [F,2F) →
+  GATED_ACT(gate, [bias], up), computed by one GEMM whose tiles pair gate
+  and up columns,
+
+each against the float64 closed form, the CPU oracle, and the same graph run
+node by node (fusion off): the bits must be identical, since the epilogue
+rounds every step in the order the separate nodes do.
+"""
+
+import numpy as np
+import pytest
+
+from conftest import normwise_rel
+from helpers import cf_gelu_tanh, cf_silu, randn, rng, run_oracle
+from runtime.ir import Graph, OpType
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+def _run(graph, inputs, fuse):
+    from runtime.executor.compiled import CompiledExecutor
+    from runtime.planner import plan
+    ex = CompiledExecutor(fuse=fuse)
+    ex.compile(plan(graph))
+    try:
+        y = ex.run(inputs)[graph.outputs[0]]
+        return y, [kind for _, _, kind in ex.fused_runs()]
+    finally:
+        ex.close()
+
+
+def _check(graph, inputs, ref, kind):
+    y, runs = _run(graph, inputs, True)
+    z, plain = _run(graph, inputs, False)
+    o = run_oracle(graph, inputs)
+    print(f"{kind}: fused runs {runs}; gpu-vs-ref {normwise_rel(y, ref):.2e} oracle-vs-ref {normwise_rel(o, ref):.2e}")
+    assert runs == [kind] and plain == []
+    np.testing.assert_array_equal(y, z)
+    assert normwise_rel(o, ref) <= TOL
+    assert normwise_rel(y, ref) <= TOL
+    assert normwise_rel(y, o) <= TOL
+
+
+def _gemm_graph(g, r, M, N, K, bias):
+    """a [1, M, K] input, w [N, K] (and b [N]) constants, c = a·wᵀ (+ b); returns a, c64."""
+    a = randn(r, 1, M, K)
+    w = randn(r, N, K)
+    g.add_tensor("a", (1, M, K))
+    g.inputs.append("a")
+    g.add_tensor("w", (N, K)).buffer = w
+    g.constants.append("w")
+    ins = ["a", "w"]
+    c = a.astype(np.float64) @ w.T.astype(np.float64)
+    if bias:
+        b = randn(r, N)
+        g.add_tensor("b", (N,)).buffer = b
+        g.constants.append("b")
+        ins.append("b")
+        c = c + b
+    g.add_tensor("c", (1, M, N))
+    g.add_node(OpType.MATMUL_ADD if bias else OpType.MATMUL, ins, "c", {"transpose_b": True})
+    return a, c
+
+
+ACTS = {OpType.RELU: lambda v: np.maximum(v, 0.0), OpType.GELU: cf_gelu_tanh, OpType.SILU: cf_silu}
+
+
+# Kernel-selection overrides (read when the plan is built): LBR_GEMM_TILE forces
+# a DMA tile, LBR_GEMM_KSPLIT the number of K ranges (the activation then runs
+# in the split-K reduction).
+@pytest.mark.parametrize("op", list(ACTS), ids=lambda o: o.name)
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("tile,ks,M,N,K", [(None, None, 300, 520, 96), ("256x256", "1", 300, 520, 96),
+                                           ("64x128", "1", 70, 130, 64), ("128x128", "3", 200, 300, 3072)])
+def test_gemm_activation_epilogue(monkeypatch, op, bias, tile, ks, M, N, K):
+    if tile:
+        monkeypatch.setenv("LBR_GEMM_TILE", tile)
+        monkeypatch.setenv("LBR_GEMM_KSPLIT", ks)
+    r = rng(M + N + K)
+    g = Graph()
+    a, c = _gemm_graph(g, r, M, N, K, bias)
+    g.add_tensor("y", (1, M, N))
+    g.add_node(op, ["c"], "y", {})
+    g.outputs.append("y")
+    _check(g, {"a": a}, ACTS[op](c), "gemm_act")
+
+
+@pytest.mark.parametrize("tile", [None, "256x256", "128x128", "128x64", "64x128"])
+@pytest.mark.parametrize("act,gbias,order,mm_bias", [("silu", False, 0, False), ("gelu", True, 1, True),
+                                                      ("silu", True, 0, True), ("gelu", False, 1, False)])
+def test_gemm_gated_epilogue(monkeypatch, tile, act, gbias, order, mm_bias):
+    """gate = the half picked by `order` (0: columns [0, F)), F ragged against the 16-column
+    blocks and the tiles."""
+    if tile:
+        monkeypatch.setenv("LBR_GEMM_TILE", tile)
+        monkeypatch.setenv("LBR_GEMM_KSPLIT", "1")
+    M, F, K = 300, 200, 96
+    r = rng(M + F + K + order)
+    g = Graph()
+    a, c = _gemm_graph(g, r, M, 2 * F, K, mm_bias)
+    for k, (lo, hi) in enumerate([(0, F), (F, 2 * F)]):
+        g.add_tensor(f"s{k}", (1, M, F))
+        g.add_node(OpType.SLICE, ["c"], f"s{k}", {"dim": 2, "start": lo, "end": hi})
+    halves = [c[..., :F], c[..., F:]]
+    x, up = (halves[0], halves[1]) if order == 0 else (halves[1], halves[0])
+    ins = ["s0", "s1"] if order == 0 else ["s1", "s0"]
+    if gbias:
+        gb = randn(r, F)
+        g.add_tensor("gb", (F,)).buffer = gb
+        g.constants.append("gb")
+        ins.insert(1, "gb")
+        x = x + gb
+    g.add_tensor("y", (1, M, F))
+    g.add_node(OpType.GATED_ACT, ins, "y", {"has_bias": gbias, "act": act})
+    g.outputs.append("y")
+    ref = (cf_silu(x) if act == "silu" else cf_gelu_tanh(x)) * up
+    _check(g, {"a": a}, ref, "gemm_gated")

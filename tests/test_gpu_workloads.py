@@ -47,10 +47,10 @@ def test_workload_parity(key, seq):
 
 
 @pytest.mark.parametrize("key,seq,kinds", [
-    ("toy", None, {"gemm_heads", "gemm_resid"}),
-    ("gpt2", None, {"gemm_heads", "gemm_resid"}),
-    ("qwen3_4b", None, {"head_prologue", "gemm_resid"}),
-    ("7b4k", 256, {"gemm_heads", "gemm_resid"}),
+    ("toy", None, {"gemm_heads", "gemm_resid", "gemm_act"}),
+    ("gpt2", None, {"gemm_heads", "gemm_resid", "gemm_act"}),
+    ("qwen3_4b", None, {"head_prologue", "gemm_resid", "gemm_gated", "attn_transpose"}),
+    ("7b4k", 256, {"gemm_heads", "gemm_resid", "gemm_act"}),
 ])
 def test_fused_plan_matches_unfused(monkeypatch, key, seq, kinds):
     """Peephole fusion changes launches, not results: the fused plan's outputs equal the
