@@ -129,10 +129,13 @@ def step_units(names, order, graph, ms, runs):
 
 
 def kernel_table(units):
-    """Aggregate per-step device times by kernel name."""
+    """Aggregate per-step device times by device kernel: a fused step is named
+    `<kernel>+<epilogue>` and runs `<kernel>`, so it counts under `<kernel>`
+    (the grouping rocprofv3 reports, by kernel function)."""
     agg: dict[str, dict] = {}
     for u in units:
-        a = agg.setdefault(u["name"], {"kernel": u["name"], "launches": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0})
+        base = u["name"].split("+")[0]
+        a = agg.setdefault(base, {"kernel": base, "launches": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0})
         a["launches"] += 1
         a["ms"] += u["ms"]
         a["flops"] += u["flops"]
