@@ -367,6 +367,9 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
             }
 
             float tmax = -INFINITY;
+            // a tile wholly inside S and (causal) at or below this wave's first row needs no
+            // per-score bounds or causal test (wave-uniform)
+            const bool inner = k0 + A16_KB <= S && (!CAUSAL || k0 + A16_KB - 1 <= q_wave0);
 #pragma unroll
             for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -374,7 +377,7 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
                     const int kv = k0 + 16 * b + 4 * lg + r;
                     float sv = sacc[b][r];
                     if (HAS_MASK && kv < S && q < S) sv += g.mask[(bh * S + q) * (long long)S + kv] * LOG2E;
-                    if (kv >= S || (CAUSAL && kv > q)) sv = -INFINITY;
+                    if (!inner && (kv >= S || (CAUSAL && kv > q))) sv = -INFINITY;
                     sacc[b][r] = sv;
                     tmax = fmaxf(tmax, sv);
                 }
@@ -394,9 +397,13 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
             psum += __shfl_xor(psum, 16, 64);
             psum += __shfl_xor(psum, 32, 64);
             l_run = l_run * corr + psum;
-            m_run = m_new;
+            // the rescale is a multiply by exactly 1 unless some row's max moved: skip it
+            // when no lane's did (wave vote)
+            if (__any(m_new != m_run)) {
 #pragma unroll
-            for (int db = 0; db < NCH; ++db) oacc[db] *= corr;
+                for (int db = 0; db < NCH; ++db) oacc[db] *= corr;
+            }
+            m_run = m_new;
 
             // Oᵀ[d][q] += Σ_kv V[kv][d]·P[q][kv]; MFMA (b, r) takes key 16b + 4g + r from group g
 #pragma unroll
