@@ -262,6 +262,28 @@ __global__ __launch_bounds__(AT_NT, DP >= 256 ? 1 : 2) void attn_fwd_mfma(AttnAr
 // LDS rows are padded to hd+4 floats: the K reads (16 rows × 4 groups of
 // 16 B) and the V reads (4 rows × 16 lanes × W consecutive floats) hit
 // distinct banks.
+// Cross-row all-reduce of lanes l, l^16 and l^32 through the gfx950 row
+// swaps (v_permlane16_swap / v_permlane32_swap: VALU, no LDS round trip).
+// swap(x, x) returns the pair {x[l], x[l^16]} (resp. l^32) in some order;
+// max and + are commutative, so the result equals the shuffle reduction.
+__device__ __forceinline__ float rows4_max(float x) {
+    const unsigned u = __float_as_uint(x);
+    auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const unsigned v = __float_as_uint(x);
+    auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float rows4_sum(float x) {
+    const unsigned u = __float_as_uint(x);
+    auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const unsigned v = __float_as_uint(x);
+    auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 constexpr int A16_NT = 512;      // 8 waves
 constexpr int A16_QB = 128;      // query rows per workgroup (16 per wave)
 constexpr int A16_KB = 32;       // keys per tile
@@ -381,8 +403,7 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
                     sacc[b][r] = sv;
                     tmax = fmaxf(tmax, sv);
                 }
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+            tmax = rows4_max(tmax);
             const float m_new = fmaxf(m_run, tmax);
             const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
             float psum = 0.f;
@@ -394,8 +415,7 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
                     sacc[b][r] = p;
                     psum += p;
                 }
-            psum += __shfl_xor(psum, 16, 64);
-            psum += __shfl_xor(psum, 32, 64);
+            psum = rows4_sum(psum);
             l_run = l_run * corr + psum;
             // the rescale is a multiply by exactly 1 unless some row's max moved: skip it
             // when no lane's did (wave vote)
