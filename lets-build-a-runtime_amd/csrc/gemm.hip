@@ -833,14 +833,16 @@ constexpr DmaTile kDmaTiles[] = {
     {128, 128, 2, 0.92, "128x128"},   // 4 wavefronts (2×2), 64 KB LDS
     {128, 64, 3, 0.90, "128x64"},     // 4 wavefronts (2×2), 48 KB LDS
     {64, 128, 3, 0.90, "64x128"},
+    {64, 64, 4, 0.85, "64x64"},       // 4 wavefronts (2×2) of 32×32, 32 KB LDS
 };
 constexpr int kNumDmaTiles = sizeof(kDmaTiles) / sizeof(kDmaTiles[0]);
 
 // Tile shape and number of K ranges for the DMA GEMM.  Time model: the
 // busiest CU runs ceil(items / CUs) workgroups of TM·TN·kchunk MACs each
-// at the tile's efficiency; a K split adds writing and re-reading the
-// partial sums at ~5 TB/s plus a reduction launch.  LBR_GEMM_TILE (a tile
-// name) and LBR_GEMM_KSPLIT override the choice.
+// at the tile's efficiency, in rounds of `occ` resident workgroups that
+// each pay ~3 µs of first-load latency and epilogue; a K split adds writing
+// and re-reading the partial sums at ~5 TB/s plus a reduction launch.
+// LBR_GEMM_TILE (a tile name) and LBR_GEMM_KSPLIT override the choice.
 void choose_dma(long long M, long long N, int K, long long batches, int cus, int* tile, int* ksplit, int* kchunk) {
     const double peak_cu = 157.3e12 / 256.0;
     const char* force_tile = getenv("LBR_GEMM_TILE");
@@ -864,6 +866,7 @@ void choose_dma(long long M, long long N, int K, long long batches, int cus, int
             }
             const long long per_cu = (tiles * s_eff + cus - 1) / cus;
             double t_s = (double)per_cu * 2.0 * d.tm * d.tn * chunk / (d.eff * peak_cu);
+            t_s += (double)((per_cu + d.occ - 1) / d.occ) * 3e-6;   // per round: first DMA, epilogue
             if (s_eff > 1) t_s += (2.0 * s_eff + 1.0) * M * N * batches * 4.0 / 5e12 + 4e-6;
             if (s_eff > 1 && !force_ks) t_s *= 1.05;   // split only for a clear gain
             if (t_s < best) {
@@ -882,7 +885,8 @@ step_fn dma_launcher(int tile) {
         case 0: return launch_gemm_dma<256, 256, 4, 2, 1, HAS_BIAS>;
         case 1: return launch_gemm_dma<128, 128, 2, 2, 2, HAS_BIAS>;
         case 2: return launch_gemm_dma<128, 64, 2, 2, 3, HAS_BIAS>;
-        default: return launch_gemm_dma<64, 128, 2, 2, 3, HAS_BIAS>;
+        case 3: return launch_gemm_dma<64, 128, 2, 2, 3, HAS_BIAS>;
+        default: return launch_gemm_dma<64, 64, 2, 2, 4, HAS_BIAS>;
     }
 }
 

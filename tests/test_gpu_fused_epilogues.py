@@ -91,7 +91,7 @@ def test_gemm_activation_epilogue(monkeypatch, op, bias, tile, ks, M, N, K):
     _check(g, {"a": a}, ACTS[op](c), "gemm_act")
 
 
-@pytest.mark.parametrize("tile", [None, "256x256", "128x128", "128x64", "64x128"])
+@pytest.mark.parametrize("tile", [None, "256x256", "128x128", "128x64", "64x128", "64x64"])
 @pytest.mark.parametrize("act,gbias,order,mm_bias", [("silu", False, 0, False), ("gelu", True, 1, True),
                                                       ("silu", True, 0, True), ("gelu", False, 1, False)])
 def test_gemm_gated_epilogue(monkeypatch, tile, act, gbias, order, mm_bias):
