@@ -168,6 +168,9 @@ int lbr_plan_node_kernel(const lbr_plan* plan, int index, char* name_out,
 #define LBR_FUSE_GEMM_GATED    6  /* MATMUL[_ADD] (N = 2F) → SLICE [0,F) → SLICE [F,2F) →
                                      GATED_ACT: the GEMM pairs gate and up columns in each tile
                                      and writes act(gate)·up as [M, F]                           */
+#define LBR_FUSE_TRANSPOSE_GEMM 7 /* TRANSPOSE(H,S) of [B,H,S,hd] → MATMUL[_ADD] → [ADD(C, R)]:
+                                     the GEMM reads its A operand in the untransposed layout
+                                     (and adds R in its epilogue)                               */
 
 typedef struct {
     int first;   /* index of the run's first node */

@@ -36,6 +36,11 @@
 //               holds both values of an output element, and writes
 //               act(gate)·up as [M, F] (the merged gate/up projection of a
 //               SiLU-gated FFN).
+//   TRANSPOSE_GEMM  TRANSPOSE(H,S) of the attention output [B,H,S,hd] →
+//               MATMUL[_ADD] → [ADD(C, R)]: the GEMM reads its A operand in
+//               the [B,H,S,hd] layout (a 32-wide K step stays inside one head
+//               when hd is a multiple of 32) and adds R in its epilogue —
+//               the O projection and its residual without the transpose.
 #include "lbr_device.h"
 
 #include <math.h>
@@ -536,6 +541,59 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
             ++i;
             continue;
         }
+        // TRANSPOSE_GEMM: T = TRANSPOSE(O [B, H, S, hd] → [B, S, H, hd]) is the A operand of the
+        // next GEMM (DMA kernel, one batch, hd a multiple of its 32-wide K step): the GEMM reads
+        // O directly; a residual ADD right after it is taken into the epilogue as well
+        if (nd->op == OP_TRANSPOSE && i + 1 < n && is_f32(nd) && nd->n_dims == 4 && nd->n_inputs >= 1 &&
+            nd->extra[2] == 1) {
+            const int B = nd->extra[0], H = nd->extra[1], S = nd->extra[3], hd = nd->extra[4];
+            const OpNode* mm = &nodes[i + 1];
+            Step ms;
+            if (nd->out_shape[0] == B && nd->out_shape[1] == S && nd->out_shape[2] == H && nd->out_shape[3] == hd &&
+                hd % 32 == 0 && mm->n_inputs >= 2 && mm->inputs[0] == nd->output && is_f32(mm) &&
+                gemm_step(mm, &ms) && ms.i[14] && ms.i[3] == 1 && ms.i[0] == (long long)B * S &&
+                ms.i[2] == (long long)H * hd && lbr_aligned(nd->inputs[0], 16)) {
+                std::vector<Rng> reads;
+                gemm_input_rngs(mm, ms, &reads);
+                reads[0] = rng(nd->inputs[0], (long long)B * H * S * hd * 4);   // A is read as O
+                const Rng t_r = out_rng(nd), c_r = out_rng(mm);
+                FusedRun f;
+                f.first = i;
+                f.kind = LBR_FUSE_TRANSPOSE_GEMM;
+                f.src = nd->inputs[0];
+                f.B = B;
+                f.S = S;
+                f.hd = hd;
+                f.Hs[0] = H;
+                bool done = false;
+                // with the residual ADD: y = C + R
+                if (i + 2 < n) {
+                    const OpNode* ad = &nodes[i + 2];
+                    if (ad->op == OP_ADD && ad->n_inputs >= 2 && ad->extra[0] == 1 && is_f32(ad) &&
+                        node_total(ad) == node_total(mm) && (ad->inputs[0] == mm->output) != (ad->inputs[1] == mm->output)) {
+                        const void* R = ad->inputs[0] == mm->output ? ad->inputs[1] : ad->inputs[0];
+                        const Rng y = out_rng(ad), r_r = rng(R, node_total(mm) * 4);
+                        if (!any_overlap(y, reads) && (y.lo == r_r.lo || !overlap(y, r_r)) &&
+                            dead_after(nodes, n, i + 3, {t_r, c_r}, {y}, live)) {
+                            f.count = 3;
+                            f.resid = R;
+                            f.out = ad->output;
+                            done = true;
+                        }
+                    }
+                }
+                if (!done && !any_overlap(c_r, reads) && dead_after(nodes, n, i + 2, {t_r}, {c_r}, live)) {
+                    f.count = 2;
+                    f.out = mm->output;
+                    done = true;
+                }
+                if (done) {
+                    out->push_back(f);
+                    i += f.count;
+                    continue;
+                }
+            }
+        }
         // ATTN_TRANSPOSE: attention output [B, H, S, hd] transposed to [B, S, H, hd]
         if (nd->op == OP_ATTENTION && i + 1 < n && is_f32(nd) && nd->n_dims == 4) {
             const OpNode* tr = &nodes[i + 1];
@@ -636,6 +694,26 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
         s->out = (void*)f.out;
         s->i[9] = f.Hs[0];
         s->name = "attn_fwd_mfma16_f32+transpose";
+    } else if (f.kind == LBR_FUSE_TRANSPOSE_GEMM) {
+        int rc = decode_matmul(&nodes[f.first + 1], s);
+        if (rc) return rc;
+        if (!s->i[14] || s->i[3] != 1) {
+            lbr_set_error("fusion: GEMM node %d is not on the single-batch DMA path", f.first + 1);
+            return LBR_ERR_INVALID;
+        }
+        s->in[0] = f.src;
+        s->run = gemm_dma_heads_launcher((int)s->i[14] - 1, s->i[6] != 0);
+        s->i[35] = f.Hs[0];
+        s->i[36] = f.S;
+        s->i[37] = f.hd;
+        s->out = (void*)f.out;
+        if (f.resid) {
+            s->in[3] = f.resid;
+            s->i[12] = s->i[12] && lbr_aligned(f.out, 16);
+            s->name = "gemm_dma_f32_nt+tin+resid";
+        } else {
+            s->name = "gemm_dma_f32_nt+tin";
+        }
     } else if (f.kind == LBR_FUSE_GEMM_ACT || f.kind == LBR_FUSE_GEMM_GATED) {
         int rc = decode_matmul(&nodes[f.first], s);
         if (rc) return rc;

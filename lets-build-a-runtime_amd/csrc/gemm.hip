@@ -66,6 +66,9 @@ struct GemmArgs {
     int gbase;                // first column of the gate half (0 or gF; up is the other half)
     int gact;                 // 0: SiLU, 1: GELU (GATED_ACT extras[1])
     const float* gbias;       // GATED_ACT bias (applied to gate) or null
+    // A in head layout (DMA kernel): A is stored [B, aH, aS, ahd] and read as the
+    // [B·aS, aH·ahd] matrix its TRANSPOSE(1, 2) would give (aH = 0: A is row-major)
+    int aH, aS, ahd;
 };
 
 // Final store of one C element (row m, column n of batch bz) with the fused
@@ -418,7 +421,7 @@ __device__ __forceinline__ void chunk_schedule() {
     __builtin_amdgcn_sched_group_barrier(0x008, NM - NV - ND, 0);
 }
 
-template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS>
+template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS, bool AHEADS>
 __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) {
     constexpr int NW = WGM * WGN;
     constexpr int CH = DBK / 4;                 // 16-byte chunks per tile row
@@ -446,7 +449,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
 #pragma unroll
     for (int t = 0; t < IA; ++t) {
         const int row = wave * (TM / NW) + t * RPI + dr;
-        offA[t] = (unsigned)(min(m0 + row, M - 1) * K + ((dp ^ dr) * 4)) * 4u;
+        const int m = min(m0 + row, M - 1);
+        if (AHEADS) {
+            // head layout: row m = (b, s) starts at ((b·aH)·aS + s)·ahd; the K step's head and
+            // offset inside it are the same for every row (soffA below)
+            const int b = m / g.aS, s = m - b * g.aS;
+            offA[t] = (unsigned)(((b * g.aH) * g.aS + s) * g.ahd + ((dp ^ dr) * 4)) * 4u;
+        } else {
+            offA[t] = (unsigned)(m * K + ((dp ^ dr) * 4)) * 4u;
+        }
     }
 #pragma unroll
     for (int t = 0; t < IB; ++t) {
@@ -468,8 +479,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
     auto issue = [&](int k0, float* st) {
         float* la = st + wave * (TM / NW) * DBK;
         float* lb = st + TM * DBK + wave * (TN / NW) * DBK;
+        // K step k0 of A: column k0 (row-major), or head k0 / ahd at offset k0 % ahd (head
+        // layout; ahd is a multiple of the step, so a step never straddles two heads)
+        const unsigned soffA =
+            AHEADS ? (unsigned)((k0 / g.ahd) * g.aS * g.ahd + k0 % g.ahd) * 4u : (unsigned)k0 * 4u;
 #pragma unroll
-        for (int t = 0; t < IA; ++t) dma16(ra, la + t * RPI * DBK, offA[t], (unsigned)k0 * 4u);
+        for (int t = 0; t < IA; ++t) dma16(ra, la + t * RPI * DBK, offA[t], soffA);
 #pragma unroll
         for (int t = 0; t < IB; ++t) dma16(rb, lb + t * RPI * DBK, offB[t], (unsigned)k0 * 4u);
     };
@@ -703,7 +718,8 @@ __global__ __launch_bounds__(256) void gemv_n(GemmArgs g) {
 // Step::i: [0]=M [1]=N [2]=K [3]=batches [4]=trans_b [5]=vec [6]=has_bias
 //          [7]=sA [8]=sB [9]=sC [10]=ksplit [11]=kchunk [12]=float4 reduce
 //          [13]=1 (takes fused epilogues) [14]=DMA tile + 1 (0: gemm_mfma_f32)
-//          [19..30] head scatter, [31] activation, [32..34] gated pair (see below) ; f[0] = alpha
+//          [19..30] head scatter, [31] activation, [32..34] gated pair, [35..37] A in
+//          head layout (see below) ; f[0] = alpha
 GemmArgs make_args(const Step& s) {
     GemmArgs g;
     g.A = (const float*)s.in[0];
@@ -741,6 +757,10 @@ GemmArgs make_args(const Step& s) {
     g.hd = (int)s.i[29];
     g.S = (int)s.i[30];
     g.act = (int)s.i[31];
+    // i[35..37] = A in head layout [B, H, S, hd]: H, S, hd (0: row-major A)
+    g.aH = (int)s.i[35];
+    g.aS = (int)s.i[36];
+    g.ahd = (int)s.i[37];
     return g;
 }
 
@@ -809,7 +829,7 @@ void launch_gemm_t(const Step& s, hipStream_t st) {
     if (g.ksplit > 1) launch_splitk_reduce<HAS_BIAS>(s, g, st);
 }
 
-template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS>
+template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS, bool AHEADS>
 void launch_gemm_dma(const Step& s, hipStream_t st) {
     GemmArgs g = make_args(s);
     if (g.M <= 0 || g.N <= 0) return;
@@ -817,7 +837,7 @@ void launch_gemm_dma(const Step& s, hipStream_t st) {
     // a gated pair's tile covers TN/2 output columns (TN/2 gate + TN/2 up columns of C)
     g.tiles_n = g.gF ? (g.gF + TN / 2 - 1) / (TN / 2) : (g.N + TN - 1) / TN;
     dim3 grid(g.tiles_m * g.tiles_n, g.ksplit, (unsigned)s.i[3]);
-    hipLaunchKernelGGL((gemm_dma_f32<TM, TN, WGM, WGN, OCC, HAS_BIAS>), grid, dim3(64 * WGM * WGN), 0, st, g);
+    hipLaunchKernelGGL((gemm_dma_f32<TM, TN, WGM, WGN, OCC, HAS_BIAS, AHEADS>), grid, dim3(64 * WGM * WGN), 0, st, g);
     if (g.ksplit > 1) launch_splitk_reduce<HAS_BIAS>(s, g, st);
 }
 
@@ -879,14 +899,14 @@ void choose_dma(long long M, long long N, int K, long long batches, int cus, int
     }
 }
 
-template <bool HAS_BIAS>
+template <bool HAS_BIAS, bool AHEADS = false>
 step_fn dma_launcher(int tile) {
     switch (tile) {
-        case 0: return launch_gemm_dma<256, 256, 4, 2, 1, HAS_BIAS>;
-        case 1: return launch_gemm_dma<128, 128, 2, 2, 2, HAS_BIAS>;
-        case 2: return launch_gemm_dma<128, 64, 2, 2, 3, HAS_BIAS>;
-        case 3: return launch_gemm_dma<64, 128, 2, 2, 3, HAS_BIAS>;
-        default: return launch_gemm_dma<64, 64, 2, 2, 4, HAS_BIAS>;
+        case 0: return launch_gemm_dma<256, 256, 4, 2, 1, HAS_BIAS, AHEADS>;
+        case 1: return launch_gemm_dma<128, 128, 2, 2, 2, HAS_BIAS, AHEADS>;
+        case 2: return launch_gemm_dma<128, 64, 2, 2, 3, HAS_BIAS, AHEADS>;
+        case 3: return launch_gemm_dma<64, 128, 2, 2, 3, HAS_BIAS, AHEADS>;
+        default: return launch_gemm_dma<64, 64, 2, 2, 4, HAS_BIAS, AHEADS>;
     }
 }
 
@@ -958,6 +978,12 @@ void zero_k_fill(const Step& s, hipStream_t st) {
 }
 
 }  // namespace
+
+// Launcher of the DMA GEMM with its A operand in head layout (TRANSPOSE_GEMM
+// fusion): `tile` = Step::i[14] − 1 of the decoded GEMM.
+step_fn gemm_dma_heads_launcher(int tile, bool has_bias) {
+    return has_bias ? dma_launcher<true, true>(tile) : dma_launcher<false, true>(tile);
+}
 
 // MATMUL extras [K, trans_b, b_is_2d, alpha_bits] (alpha_bits 0 ⇒ 1.0);
 // MATMUL_ADD inputs [A, B, bias] with the same extras (executor.c:197-224,

@@ -148,6 +148,8 @@ int decode_slice(const OpNode* n, Step* s);
 int decode_cat(const OpNode* n, Step* s);
 int decode_embedding(const OpNode* n, Step* s);
 int decode_matmul(const OpNode* n, Step* s);
+// DMA GEMM launcher reading A in head layout (fused TRANSPOSE → GEMM); tile = Step::i[14] − 1
+step_fn gemm_dma_heads_launcher(int tile, bool has_bias);
 int decode_attention(const OpNode* n, Step* s);
 
 // Helpers over the node record (same meaning as csrc/executor.c:30-48).

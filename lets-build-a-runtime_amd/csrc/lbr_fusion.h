@@ -34,6 +34,8 @@ struct FusedRun {
     // GATED_ACT's act code and bias (`out` is the GATED_ACT output)
     int gF = 0, gate_base = 0, gact = 0;
     const void* gbias = nullptr;
+    // TRANSPOSE_GEMM: the GEMM's A in head layout [B, H, S, hd] at `src`; `resid` /
+    // `out` set when the residual ADD is fused as well (B, S, hd and Hs[0] = H)
 };
 
 // Fusable runs of nodes[0..n) in stream order; live-out ranges are the

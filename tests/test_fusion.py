@@ -56,11 +56,14 @@ def _workload_nodes(key: str, seq: int):
 EXPECTED = {
     # merged QKV → three (slice, bias add, transpose) chains in the GEMM epilogue; the O-proj residual
     # add writes over the GEMM's own A input (refused), the FFN2 one fuses
-    # FFN1 → GELU runs in the GEMM epilogue
+    # FFN1 → GELU runs in the GEMM epilogue; the attention output transpose → O-proj → residual
+    # ADD is one GEMM reading the [B,H,S,hd] layout (hd = 16 in the toy block: not a multiple of
+    # the GEMM's K step, so the toy keeps its transpose)
     "toy": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1}),
-    "gpt2w": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1}),
-    "7b4k": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1}),
-    # c_attn is MATMUL_ADD (bias already in the GEMM): three (slice, transpose) chains per layer
+    "gpt2w": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1, ("transpose_gemm", 3): 1}),
+    "7b4k": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1, ("transpose_gemm", 3): 1}),
+    # c_attn is MATMUL_ADD (bias already in the GEMM): three (slice, transpose) chains per layer;
+    # c_proj's output lands over the attention output it would read (transpose kept)
     "gpt2": Counter({("gemm_heads", 7): 2, ("gemm_resid", 2): 4, ("gemm_act", 2): 2}),
     # q/k: slice → per-head RMSNorm → transpose → 7-node RoPE as one kernel; v's transpose lands
     # over the QKV rows it reads at this size (refused); the attention output transpose is fused
@@ -344,3 +347,41 @@ def test_gemm_gated_refusals():
     nodes = _gated(16 * MB, bias=True)
     nodes[3].inputs[1] = ARENA + 16 * MB + 64
     assert _windows(nodes) == []
+
+
+# ------------------------------------------------------------ transpose → GEMM
+
+TB, TH, TS, THD = 1, 4, 64, 32      # attention output [B, H, S, hd] → [B, S, H·hd] for the GEMM
+TK = TH * THD
+
+
+def _tgemm(o_off, t_off, c_off, y_off=None, hd=THD, later=()):
+    """O [B,H,S,hd] → TRANSPOSE(H,S) → T; MATMUL T·Wᵀ → C [B·S, N]; [ADD(C, R) → Y]."""
+    heads = TK // hd
+    tr = _node(OpType.TRANSPOSE, [ARENA + o_off], ARENA + t_off, (TB, TS, heads, hd), (TB, heads, 1, TS, hd))
+    mm = _node(OpType.MATMUL, [ARENA + t_off, W_], ARENA + c_off, (TB, TS, N), (TK, 1, 1, 0))
+    nodes = [tr, mm]
+    if y_off is not None:
+        nodes.append(_node(OpType.ADD, [ARENA + c_off, R_], ARENA + y_off, (TB, TS, N), (1,)))
+    return [*nodes, *later]
+
+
+def test_transpose_gemm_fuses():
+    assert _windows(_tgemm(0, 1 * MB, 2 * MB, 3 * MB)) == [(0, 3, "transpose_gemm")]
+    assert _windows(_tgemm(0, 1 * MB, 2 * MB)) == [(0, 2, "transpose_gemm")]
+    # C or Y over the dead transposed copy T is fine: T is never written
+    assert _windows(_tgemm(0, 1 * MB, 1 * MB, 1 * MB)) == [(0, 3, "transpose_gemm")]
+
+
+def test_transpose_gemm_refusals():
+    # the GEMM's output over the attention output it now reads (GPT-2's c_proj): with no
+    # residual ADD, C is that output; with one, Y is (C itself is never written)
+    assert _windows(_tgemm(0, 1 * MB, 0)) == []
+    assert _windows(_tgemm(0, 1 * MB, 0, 3 * MB)) == [(0, 3, "transpose_gemm")]
+    # Y over O: the residual ADD stays a node of its own, the transpose is still absorbed
+    assert _windows(_tgemm(0, 1 * MB, 2 * MB, 0)) == [(0, 2, "transpose_gemm")]
+    # head dim not a multiple of the 32-wide K step (a step would straddle two heads)
+    assert _windows(_tgemm(0, 1 * MB, 2 * MB, hd=16)) == []
+    # T read by a later node
+    reader = _node(OpType.RELU, [ARENA + 1 * MB], ARENA + 8 * MB, (16,))
+    assert all(k != "transpose_gemm" for _, _, k in _windows(_tgemm(0, 1 * MB, 2 * MB, 3 * MB, later=[reader])))

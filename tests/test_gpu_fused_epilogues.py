@@ -121,3 +121,50 @@ def test_gemm_gated_epilogue(monkeypatch, tile, act, gbias, order, mm_bias):
     g.outputs.append("y")
     ref = (cf_silu(x) if act == "silu" else cf_gelu_tanh(x)) * up
     _check(g, {"a": a}, ref, "gemm_gated")
+
+
+@pytest.mark.parametrize("tile", [None, "256x256", "128x64", "64x64"])
+@pytest.mark.parametrize("H,S,hd,N,bias,resid", [(4, 300, 64, 200, True, True), (2, 130, 128, 96, False, True),
+                                                  (8, 64, 32, 520, True, False)])
+def test_transpose_gemm(monkeypatch, tile, H, S, hd, N, bias, resid):
+    """O [1, H, S, hd] → TRANSPOSE(1, 2) → [1, S, H·hd] → MATMUL[_ADD] → [ADD(C, R)]: the GEMM reads
+    O in its head layout (the transposed copy is never made)."""
+    if tile:
+        monkeypatch.setenv("LBR_GEMM_TILE", tile)
+        monkeypatch.setenv("LBR_GEMM_KSPLIT", "1")
+    r = rng(H * S + hd + N)
+    K = H * hd
+    o = randn(r, 1, H, S, hd)
+    w = randn(r, N, K)
+    g = Graph()
+    g.add_tensor("o", (1, H, S, hd))
+    g.inputs.append("o")
+    g.add_tensor("t", (1, S, H, hd))
+    g.add_node(OpType.TRANSPOSE, ["o"], "t", {"dim0": 1, "dim1": 2})
+    g.add_tensor("a", (1, S, K))
+    g.add_node(OpType.RESHAPE, ["t"], "a", {"shape": (1, S, K)})
+    g.add_tensor("w", (N, K)).buffer = w
+    g.constants.append("w")
+    ins = ["a", "w"]
+    c = np.swapaxes(o, 1, 2).reshape(1, S, K).astype(np.float64) @ w.T.astype(np.float64)
+    if bias:
+        b = randn(r, N)
+        g.add_tensor("b", (N,)).buffer = b
+        g.constants.append("b")
+        ins.append("b")
+        c = c + b
+    g.add_tensor("c", (1, S, N))
+    g.add_node(OpType.MATMUL_ADD if bias else OpType.MATMUL, ins, "c", {"transpose_b": True})
+    inputs = {"o": o}
+    out = "c"
+    if resid:
+        res = randn(r, 1, S, N)
+        g.add_tensor("r", (1, S, N))
+        g.inputs.append("r")
+        inputs["r"] = res
+        g.add_tensor("y", (1, S, N))
+        g.add_node(OpType.ADD, ["c", "r"], "y", {})
+        c = c + res
+        out = "y"
+    g.outputs.append(out)
+    _check(g, inputs, c, "transpose_gemm")
