@@ -275,6 +275,16 @@ def main() -> int:
     ms_per_step = wall_ms
     tokens = x.shape[0] * x.shape[1]
     log(f"[bench] {args.steps} steps: {wall_ms:.3f} ms/step wall, {event_ms:.3f} ms/step hipEvent")
+    # median of single replays (hipEvent pair around each graph launch), and the end-to-end
+    # Session.run wall time with the input H2D and output D2H copies included
+    replay_ms = float(np.median([ex.time_launches(1) for _ in range(max(20, args.steps))]))
+    run_wall = []
+    for _ in range(5):
+        t1 = time.perf_counter()
+        sess.run({graph.inputs[0]: x})
+        run_wall.append((time.perf_counter() - t1) * 1e3)
+    session_run_ms = float(np.median(run_wall))
+    log(f"[bench] replay median {replay_ms:.3f} ms; Session.run (H2D + replay + D2H) median {session_run_ms:.3f} ms")
 
     # per-kernel device time (eager launches, hipEvent pairs on the library stream)
     names = ex.kernel_names()
@@ -328,6 +338,9 @@ def main() -> int:
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
         "event_ms_per_step": round(event_ms, 4),
+        "latency": {"replay_median_ms": round(replay_ms, 4), "replays": max(20, args.steps),
+                    "session_run_median_ms": round(session_run_ms, 4), "session_runs": 5,
+                    "session_run_includes": "input H2D copy, graph replay, output D2H copy"},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
