@@ -209,7 +209,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="7b4k", help="workload key (toy, gpt2w, gpt2, 7b4k, qwen3_4b)")
+    ap.add_argument("--config", default="7b4k", help="workload key (toy, gpt2w, gpt2, 7b4k, qwen3_4b, gpt2_lm, qwen3_4b_lm)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-parity", action="store_true", help="skip the GPU-vs-oracle output check")
     ap.add_argument("--eager", action="store_true", help="launch node by node instead of replaying a hipGraph")

@@ -123,15 +123,17 @@ def test_gemm_gated_epilogue(monkeypatch, tile, act, gbias, order, mm_bias):
     _check(g, {"a": a}, ref, "gemm_gated")
 
 
-@pytest.mark.parametrize("tile", [None, "256x256", "128x64", "64x64"])
+@pytest.mark.parametrize("tile,ks", [(None, None), ("256x256", "1"), ("128x64", "1"), ("64x64", "1"),
+                                     ("128x128", "3")])
 @pytest.mark.parametrize("H,S,hd,N,bias,resid", [(4, 300, 64, 200, True, True), (2, 130, 128, 96, False, True),
                                                   (8, 64, 32, 520, True, False)])
-def test_transpose_gemm(monkeypatch, tile, H, S, hd, N, bias, resid):
+def test_transpose_gemm(monkeypatch, tile, ks, H, S, hd, N, bias, resid):
     """O [1, H, S, hd] → TRANSPOSE(1, 2) → [1, S, H·hd] → MATMUL[_ADD] → [ADD(C, R)]: the GEMM reads
-    O in its head layout (the transposed copy is never made)."""
+    O in its head layout (the transposed copy is never made).  ks=3 splits K into ranges that
+    start inside a head (e.g. k0 = 96 with hd = 64)."""
     if tile:
         monkeypatch.setenv("LBR_GEMM_TILE", tile)
-        monkeypatch.setenv("LBR_GEMM_KSPLIT", "1")
+        monkeypatch.setenv("LBR_GEMM_KSPLIT", ks)
     r = rng(H * S + hd + N)
     K = H * hd
     o = randn(r, 1, H, S, hd)
