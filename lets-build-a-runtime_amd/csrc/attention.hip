@@ -287,6 +287,14 @@ __device__ __forceinline__ float rows4_sum(float x) {
 constexpr int A16_NT = 512;      // 8 waves
 constexpr int A16_QB = 128;      // query rows per workgroup (16 per wave)
 constexpr int A16_KB = 32;       // keys per tile
+// The softmax reference max moves only when a score exceeds it by more than
+// this (log2 units), so every exponentiated score stays ≤ 2^8.
+constexpr float ATTN_LAZY = 8.0f;
+
+template <bool B>
+struct BoolTag {
+    static constexpr bool value = B;
+};
 
 // Key tiles query block `qblk` needs: all of them, or (causal) up to the one
 // holding its last row's diagonal.
@@ -339,18 +347,38 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
     floatx4 oacc[NCH];
 #pragma unroll
     for (int b = 0; b < NCH; ++b) oacc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -FLT_MAX, l_run = 0.f;
+    // m_run: the reference max of this lane's row (the same in the row's 4 lanes);
+    // l_part: Σ 2^(s − m_run) over the keys this lane holds (4g + r, 16 + 4g + r of
+    // each tile) — the row sum is the total over the 4 lanes, taken once at the end
+    float m_run = -FLT_MAX, l_part = 0.f;
+
+    // Tiles [t0, t_fast) lie wholly inside S and, causal, at or below the block's
+    // first row, and the head dim fills DP: no bounds, causal or padding test.
+    int t_fast = t0;
+    if (!HAS_MASK && D == DP) {
+        int e = S / A16_KB;
+        if (CAUSAL) e = min(e, (qblk * A16_QB + 1) / A16_KB);
+        t_fast = max(t0, min(t1, e));
+    }
 
     float4 kr[PER], vr[PER];
-    auto load = [&](int k0) {
+    auto load = [&](int k0, auto checked_tag) {
+        constexpr bool CHECKED = decltype(checked_tag)::value;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int idx = tid + i * A16_NT;
-            const int r = idx / (DP / 4), d = (idx % (DP / 4)) * 4;
-            const bool ok = idx < TILE4 && k0 + r < S && d < D;
-            const long long off = (long long)(k0 + r) * D + d;
-            kr[i] = ok ? *reinterpret_cast<const float4*>(Kb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
-            vr[i] = ok ? *reinterpret_cast<const float4*>(Vb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (CHECKED) {
+                const int r = idx / (DP / 4), d = (idx % (DP / 4)) * 4;
+                const bool ok = idx < TILE4 && k0 + r < S && d < D;
+                const long long off = (long long)(k0 + r) * D + d;
+                kr[i] = ok ? *reinterpret_cast<const float4*>(Kb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+                vr[i] = ok ? *reinterpret_cast<const float4*>(Vb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+            } else if (TILE4 % A16_NT == 0 || idx < TILE4) {
+                // D == DP: granule idx of the tile is float offset 4·idx from row k0
+                const long long off = (long long)k0 * DP + 4 * idx;
+                kr[i] = *reinterpret_cast<const float4*>(Kb + off);
+                vr[i] = *reinterpret_cast<const float4*>(Vb + off);
+            }
         }
     };
     auto store = [&]() {
@@ -365,15 +393,24 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
         }
     };
 
-    load(t0 * A16_KB);
+    if (t0 < t_fast) load(t0 * A16_KB, BoolTag<false>());
+    else load(t0 * A16_KB, BoolTag<true>());
     store();
     __syncthreads();
 
-    for (int kt = t0; kt < t1; ++kt) {
+    // One key tile.  The scores are exponentiated against m_run, which moves only
+    // when some lane's tile max exceeds it by more than ATTN_LAZY (log2 units):
+    // then the row max is taken across the row's 4 lanes, and O and l_part are
+    // rescaled.  Otherwise every p = 2^(s − m_run) ≤ 2^ATTN_LAZY and the
+    // softmax step is 8 exponentials and 8 adds, with no cross-lane work.
+    // MASKED tiles apply the bounds, causal and additive-mask terms per score.
+    // PCHECK: the prefetched next tile needs the bounds-checked load.
+    auto tile = [&](int kt, auto masked_tag, auto pcheck_tag) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
         const int k0 = kt * A16_KB;
-        if (kt + 1 < t1) load(k0 + A16_KB);
+        if (kt + 1 < t1) load(k0 + A16_KB, pcheck_tag);
 
-        if (!CAUSAL || k0 <= q_wave0 + 15) {
+        if (!MASKED || !CAUSAL || k0 <= q_wave0 + 15) {
             // Sᵀ for two 16-key blocks; register r of block b = key k0 + 16b + 4g + r
             floatx4 sacc[2];
 #pragma unroll
@@ -389,41 +426,43 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
             }
 
             float tmax = -INFINITY;
-            // a tile wholly inside S and (causal) at or below this wave's first row needs no
-            // per-score bounds or causal test (wave-uniform)
-            const bool inner = k0 + A16_KB <= S && (!CAUSAL || k0 + A16_KB - 1 <= q_wave0);
+            if (MASKED) {
+                // a tile wholly inside S and (causal) at or below this wave's first row
+                // needs no per-score bounds or causal test (wave-uniform)
+                const bool inner = k0 + A16_KB <= S && (!CAUSAL || k0 + A16_KB - 1 <= q_wave0);
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
+                for (int b = 0; b < 2; ++b)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int kv = k0 + 16 * b + 4 * lg + r;
-                    float sv = sacc[b][r];
-                    if (HAS_MASK && kv < S && q < S) sv += g.mask[(bh * S + q) * (long long)S + kv] * LOG2E;
-                    if (!inner && (kv >= S || (CAUSAL && kv > q))) sv = -INFINITY;
-                    sacc[b][r] = sv;
-                    tmax = fmaxf(tmax, sv);
-                }
-            tmax = rows4_max(tmax);
-            const float m_new = fmaxf(m_run, tmax);
-            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
-            float psum = 0.f;
+                    for (int r = 0; r < 4; ++r) {
+                        const int kv = k0 + 16 * b + 4 * lg + r;
+                        float sv = sacc[b][r];
+                        if (HAS_MASK && kv < S && q < S) sv += g.mask[(bh * S + q) * (long long)S + kv] * LOG2E;
+                        if (!inner && (kv >= S || (CAUSAL && kv > q))) sv = -INFINITY;
+                        sacc[b][r] = sv;
+                        tmax = fmaxf(tmax, sv);
+                    }
+            } else {
 #pragma unroll
-            for (int b = 0; b < 2; ++b)
+                for (int b = 0; b < 2; ++b)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float p = __builtin_amdgcn_exp2f(sacc[b][r] - m_new);
-                    sacc[b][r] = p;
-                    psum += p;
-                }
-            psum = rows4_sum(psum);
-            l_run = l_run * corr + psum;
-            // the rescale is a multiply by exactly 1 unless some row's max moved: skip it
-            // when no lane's did (wave vote)
-            if (__any(m_new != m_run)) {
+                    for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sacc[b][r]);
+            }
+            if (__any(tmax > m_run + ATTN_LAZY)) {
+                const float m_new = fmaxf(m_run, rows4_max(tmax));
+                const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
 #pragma unroll
                 for (int db = 0; db < NCH; ++db) oacc[db] *= corr;
+                l_part *= corr;
+                m_run = m_new;
             }
-            m_run = m_new;
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float p = __builtin_amdgcn_exp2f(sacc[b][r] - m_run);
+                    sacc[b][r] = p;
+                    l_part += p;
+                }
 
             // Oᵀ[d][q] += Σ_kv V[kv][d]·P[q][kv]; MFMA (b, r) takes key 16b + 4g + r from group g
 #pragma unroll
@@ -446,7 +485,12 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
             store();
             __syncthreads();
         }
-    }
+    };
+    int kt = t0;
+    for (; kt + 1 < t_fast; ++kt) tile(kt, BoolTag<false>(), BoolTag<false>());
+    if (kt < t_fast) tile(kt++, BoolTag<false>(), BoolTag<true>());
+    for (; kt < t1; ++kt) tile(kt, BoolTag<true>(), BoolTag<true>());
+    const float l_run = rows4_sum(l_part);
 
     // O[q][d] = Oᵀ[d][q] / l; register r of block W·h + w holds row i = 4g + r,
     // i.e. d = 16W·h + W·(4g + r) + w: W consecutive floats per (h, r)
