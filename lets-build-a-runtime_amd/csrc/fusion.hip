@@ -76,11 +76,20 @@ __global__ __launch_bounds__(256) void head_prologue(HeadArgs a) {
     const long long bs = row / a.H;
     const int s = (int)(bs % a.S), b = (int)(bs / a.S);
     const float* __restrict__ x = a.src + bs * a.ld + a.col0 + (long long)h * a.hd;
-    float v[VPL];
+    const long long cb = ROPE ? b * a.cst[0] + h * a.cst[1] + s * a.cst[2] : 0;
+    const long long sb = ROPE ? b * a.sst[0] + h * a.sst[1] + s * a.sst[2] : 0;
+    // every load (row, bias, norm weight, RoPE tables) issues before the
+    // reduction, so the row's memory latencies overlap
+    float v[VPL], wv[VPL], cv[VPL], sv[VPL];
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
         const int d = lane + 64 * j;
         v[j] = x[d];
+        if (NORM) wv[j] = a.w[d];
+        if (ROPE) {
+            cv[j] = a.cos[cb + d];
+            sv[j] = a.sin[sb + d];
+        }
         if (BIAS) v[j] = v[j] + a.bias[h * a.hd + d];
     }
     if (NORM) {   // norm.c:100-107 order: x · (1/sqrt(Σx²/n + eps)) · w
@@ -90,13 +99,11 @@ __global__ __launch_bounds__(256) void head_prologue(HeadArgs a) {
         ss = wave_sum(ss);
         const float scale = 1.0f / sqrtf(ss / a.hd + a.eps);
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) v[j] = v[j] * scale * a.w[lane + 64 * j];
+        for (int j = 0; j < VPL; ++j) v[j] = v[j] * scale * wv[j];
     }
     float* __restrict__ o = a.out + (((long long)b * a.H + h) * a.S + s) * a.hd;
     if (ROPE) {   // y = x·cos + rotate_half(x)·sin, rotate_half = cat(−x[half:], x[:half])
         const int half = a.hd / 2;
-        const long long cb = b * a.cst[0] + h * a.cst[1] + s * a.cst[2];
-        const long long sb = b * a.sst[0] + h * a.sst[1] + s * a.sst[2];
         float p[VPL];
 #pragma unroll
         for (int j = 0; j < VPL; ++j) {
@@ -107,7 +114,7 @@ __global__ __launch_bounds__(256) void head_prologue(HeadArgs a) {
         for (int j = 0; j < VPL; ++j) {
             const int d = lane + 64 * j;
             const float rot = d < half ? -p[j] : p[j];
-            o[d] = __fadd_rn(__fmul_rn(v[j], a.cos[cb + d]), __fmul_rn(rot, a.sin[sb + d]));
+            o[d] = __fadd_rn(__fmul_rn(v[j], cv[j]), __fmul_rn(rot, sv[j]));
         }
     } else {
 #pragma unroll

@@ -33,17 +33,25 @@ __global__ __launch_bounds__(NB) void norm_wave_rows(const float* __restrict__ x
     if (row >= rows) return;
     const int c4 = cols / 4;
     const float4* xr = reinterpret_cast<const float4*>(x + row * cols);
-    float4 v[VPL];
-    float s = 0.f;
+    const float4* g4 = reinterpret_cast<const float4*>(g);
+    const float4* b4 = reinterpret_cast<const float4*>(b);
+    // row, weight and (LayerNorm) bias loads all issue before the reduction
+    float4 v[VPL], wv[VPL], bv[RMS ? 1 : VPL];
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
         const int idx = lane + k * 64;
-        v[k] = idx < c4 ? xr[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const bool in = idx < c4;
+        v[k] = in ? xr[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+        wv[k] = in ? g4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (!RMS) bv[k] = in ? b4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
         if (!RMS) s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
         else s += (v[k].x * v[k].x + v[k].y * v[k].y) + (v[k].z * v[k].z + v[k].w * v[k].w);
     }
     s = wave_sum(s);
-    const float4* g4 = reinterpret_cast<const float4*>(g);
     float4* o4 = reinterpret_cast<float4*>(out + row * cols);
     if (RMS) {
         const float scale = 1.0f / sqrtf(s / cols + eps);
@@ -51,7 +59,7 @@ __global__ __launch_bounds__(NB) void norm_wave_rows(const float* __restrict__ x
         for (int k = 0; k < VPL; ++k) {
             const int idx = lane + k * 64;
             if (idx < c4) {
-                const float4 w = g4[idx];
+                const float4 w = wv[k];
                 float4 r;
                 r.x = v[k].x * scale * w.x;
                 r.y = v[k].y * scale * w.y;
@@ -73,12 +81,11 @@ __global__ __launch_bounds__(NB) void norm_wave_rows(const float* __restrict__ x
         }
         var = wave_sum(var);
         const float inv_std = 1.0f / sqrtf(var / cols + eps);
-        const float4* b4 = reinterpret_cast<const float4*>(b);
 #pragma unroll
         for (int k = 0; k < VPL; ++k) {
             const int idx = lane + k * 64;
             if (idx < c4) {
-                const float4 w = g4[idx], bb = b4[idx];
+                const float4 w = wv[k], bb = bv[k];
                 float4 r;
                 r.x = v[k].x * inv_std * w.x + bb.x;
                 r.y = v[k].y * inv_std * w.y + bb.y;
@@ -99,17 +106,26 @@ __global__ __launch_bounds__(NB) void norm_block_rows(const float* __restrict__ 
     const long long row = blockIdx.x;
     const int c4 = cols / 4;
     const float4* xr = reinterpret_cast<const float4*>(x + row * cols);
-    float4 v[VPL];
-    float s = 0.f;
+    const float4* g4 = reinterpret_cast<const float4*>(g);
+    const float4* b4 = reinterpret_cast<const float4*>(b);
+    // the row, the weight and (LayerNorm) the bias are all loaded before the
+    // first reduction, so their latencies overlap
+    float4 v[VPL], wv[VPL], bv[RMS ? 1 : VPL];
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
         const int idx = threadIdx.x + k * NB;
-        v[k] = idx < c4 ? xr[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const bool in = idx < c4;
+        v[k] = in ? xr[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+        wv[k] = in ? g4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (!RMS) bv[k] = in ? b4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
         if (!RMS) s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
         else s += (v[k].x * v[k].x + v[k].y * v[k].y) + (v[k].z * v[k].z + v[k].w * v[k].w);
     }
     s = block_sum(s, red);
-    const float4* g4 = reinterpret_cast<const float4*>(g);
     float4* o4 = reinterpret_cast<float4*>(out + row * cols);
     if (RMS) {
         const float scale = 1.0f / sqrtf(s / cols + eps);
@@ -117,7 +133,7 @@ __global__ __launch_bounds__(NB) void norm_block_rows(const float* __restrict__ 
         for (int k = 0; k < VPL; ++k) {
             const int idx = threadIdx.x + k * NB;
             if (idx < c4) {
-                const float4 w = g4[idx];
+                const float4 w = wv[k];
                 float4 r;
                 r.x = v[k].x * scale * w.x;
                 r.y = v[k].y * scale * w.y;
@@ -139,12 +155,11 @@ __global__ __launch_bounds__(NB) void norm_block_rows(const float* __restrict__ 
         }
         var = block_sum(var, red);
         const float inv_std = 1.0f / sqrtf(var / cols + eps);
-        const float4* b4 = reinterpret_cast<const float4*>(b);
 #pragma unroll
         for (int k = 0; k < VPL; ++k) {
             const int idx = threadIdx.x + k * NB;
             if (idx < c4) {
-                const float4 w = g4[idx], bb = b4[idx];
+                const float4 w = wv[k], bb = bv[k];
                 float4 r;
                 r.x = v[k].x * inv_std * w.x + bb.x;
                 r.y = v[k].y * inv_std * w.y + bb.y;
