@@ -171,6 +171,9 @@ int lbr_plan_node_kernel(const lbr_plan* plan, int index, char* name_out,
 #define LBR_FUSE_TRANSPOSE_GEMM 7 /* TRANSPOSE(H,S) of [B,H,S,hd] → MATMUL[_ADD] → [ADD(C, R)]:
                                      the GEMM reads its A operand in the untransposed layout
                                      (and adds R in its epilogue)                               */
+#define LBR_FUSE_ATTN_SLICED_V  8 /* SLICE(C, last dim) → TRANSPOSE(S,H) → ATTENTION with it as
+                                     V → [TRANSPOSE(H,S)]: the attention kernel reads V rows
+                                     straight from C's columns (and writes [B, S, H, hd])        */
 
 typedef struct {
     int first;   /* index of the run's first node */

@@ -59,6 +59,11 @@ struct AttnArgs {
     float* part;                 // split partials Σ p·V: [bh][query block][sk_maxseg][128 rows][D]
     float* ml;                   // split running max and Σ p, same slots: [..][128 rows][2]
     int o_heads;                 // 0: O is [bh, S, D]; H > 0: O is [B, S, H, D] (fused transpose)
+    // V read from the columns of a row-major [B·S, v_ld] tensor (16x16 kernel, fused
+    // SLICE → TRANSPOSE): row s of K/V head b·v_heads + h at V + (b·S + s)·v_ld + h·D.
+    // v_ld = 0: V is [kv heads, S, D] like K.
+    long long v_ld;
+    int v_heads;
 };
 
 // Row q of head bh in the output: [bh][S][D], or [B][S][H][D] when the
@@ -326,6 +331,12 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
     const float* __restrict__ Qb = g.Q + bh * (long long)S * D;
     const float* __restrict__ Kb = g.K + kvh * (long long)S * D;
     const float* __restrict__ Vb = g.V + kvh * (long long)S * D;
+    long long vst = D;                                           // V row stride
+    if (g.v_ld) {
+        const long long b = kvh / g.v_heads;
+        Vb = g.V + b * S * g.v_ld + (kvh - b * g.v_heads) * D;
+        vst = g.v_ld;
+    }
     const int q_wave0 = qblk * A16_QB + wave * 16;
     const int q = q_wave0 + lr;
 
@@ -367,17 +378,18 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int idx = tid + i * A16_NT;
+            const int r = idx / (DP / 4), d = (idx % (DP / 4)) * 4;
+            const long long voff = (long long)(k0 + r) * vst + d;
             if (CHECKED) {
-                const int r = idx / (DP / 4), d = (idx % (DP / 4)) * 4;
                 const bool ok = idx < TILE4 && k0 + r < S && d < D;
                 const long long off = (long long)(k0 + r) * D + d;
                 kr[i] = ok ? *reinterpret_cast<const float4*>(Kb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
-                vr[i] = ok ? *reinterpret_cast<const float4*>(Vb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
+                vr[i] = ok ? *reinterpret_cast<const float4*>(Vb + voff) : make_float4(0.f, 0.f, 0.f, 0.f);
             } else if (TILE4 % A16_NT == 0 || idx < TILE4) {
-                // D == DP: granule idx of the tile is float offset 4·idx from row k0
+                // D == DP: granule idx of the K tile is float offset 4·idx from row k0
                 const long long off = (long long)k0 * DP + 4 * idx;
                 kr[i] = *reinterpret_cast<const float4*>(Kb + off);
-                vr[i] = *reinterpret_cast<const float4*>(Vb + off);
+                vr[i] = *reinterpret_cast<const float4*>(Vb + voff);
             }
         }
     };
@@ -676,7 +688,8 @@ __global__ __launch_bounds__(256) void attn_fwd_rows(AttnArgs g, int causal) {
 // Step::i: [0]=bh [1]=S [2]=D [3]=causal [4]=group [5]=DP (0 = row fallback)
 //          [6]=fold [7]=split workgroups (0 = none) [8]=split partial slots per (head, block)
 //          [9]=heads of a fused output transpose (0 = none) [10]=16x16 kernel (transpose fusable)
-//          [11]=key tiles per head (split)
+//          [11]=key tiles per head (split) [12]=V row stride when V is read from the columns
+//          of a row-major tensor (0 = contiguous) [13]=K/V heads of that layout
 AttnArgs make_args(const Step& s) {
     AttnArgs g;
     g.Q = (const float*)s.in[0];
@@ -691,6 +704,8 @@ AttnArgs make_args(const Step& s) {
     g.scale_log2 = s.f[0] * LOG2E;
     g.fold = 0;
     g.o_heads = 0;
+    g.v_ld = 0;
+    g.v_heads = 1;
     return g;
 }
 
@@ -716,6 +731,10 @@ void launch_attn16(const Step& s, hipStream_t st) {
     g.n_qblocks = (g.S + A16_QB - 1) / A16_QB;
     g.fold = CAUSAL && s.i[6] != 0;
     g.o_heads = (int)s.i[9];
+    if (s.i[12]) {
+        g.v_ld = s.i[12];
+        g.v_heads = (int)s.i[13];
+    }
     g.sk_wg = (int)s.i[7];
     g.sk_maxseg = (int)s.i[8];
     g.sk_head_tiles = (int)s.i[11];

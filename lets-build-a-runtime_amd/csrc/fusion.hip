@@ -28,6 +28,10 @@
 //               MUL sin, ADD]: one wavefront per (token, head) row.
 //   ATTN_TRANSPOSE  ATTENTION → TRANSPOSE(H,S): the attention kernel stores
 //               its rows straight into [B, S, H, hd].
+//   ATTN_SLICED_V  SLICE(C, last dim) → TRANSPOSE(S,H) → ATTENTION taking it
+//               as V → [TRANSPOSE(H,S)]: the attention kernel reads the V
+//               rows from C's column range with C's row stride (the V of a
+//               merged QKV projection whose Q and K went through norm/RoPE).
 //   GEMM_ACT    MATMUL[_ADD] → RELU | GELU | SILU: the activation runs in the
 //               GEMM epilogue (the FFN's first projection).
 //   GEMM_GATED  MATMUL[_ADD] with 2F columns → SLICE [0,F) and SLICE [F,2F)
@@ -379,6 +383,60 @@ bool any_overlap(Rng a, const std::vector<Rng>& v) {
     return false;
 }
 
+// ATTN_SLICED_V: the ATTENTION at node at_i takes as its V the [B, H, S, hd]
+// head layout `v` of H column groups of hd starting at column col0 of the
+// row-major [B·S, ld] tensor `src`; nodes [first, at_i) made `v` (their
+// outputs `inter`) and are dropped, the kernel reading src instead.  The
+// attention's output TRANSPOSE(H,S) at at_i + 1 joins the run when it can.
+bool match_attn_sliced_v(const OpNode* nodes, int n, int first, int at_i, const void* src, int ld, int col0, int B,
+                         int S, int H, int hd, const void* v, std::vector<Rng> inter, const std::vector<Rng>& live,
+                         FusedRun* f) {
+    if (at_i >= n) return false;
+    const OpNode* at = &nodes[at_i];
+    if (at->op != OP_ATTENTION || at->n_inputs < 3 || at->inputs[2] != v || at->inputs[0] == v ||
+        at->inputs[1] == v || !is_f32(at) || at->n_dims != 4 || at->out_shape[0] != B || at->out_shape[2] != S ||
+        at->out_shape[3] != hd || at->extra[0] != S || at->extra[1] != hd || ld % 4 || col0 % 4 ||
+        !lbr_aligned(src, 16))
+        return false;
+    Step as = Step();
+    if (decode_attention(at, &as) != LBR_OK) {
+        lbr_set_error("");
+        return false;
+    }
+    const int Hq = at->out_shape[1], group = at->extra[4] > 0 ? at->extra[4] : 1;
+    if (as.i[10] != 1 || Hq != H * group) return false;   // the 16x16 kernel reads a strided V
+    const long long q_bytes = (long long)B * Hq * S * hd * 4;
+    std::vector<Rng> reads{rng(at->inputs[0], q_bytes), rng(at->inputs[1], q_bytes / group),
+                           rng(src, (long long)B * S * ld * 4)};
+    if (at->extra[3] != 0) reads.push_back(rng(at->inputs[3], (long long)B * Hq * S * S * 4));
+    const OpNode* tr = at_i + 1 < n ? &nodes[at_i + 1] : nullptr;
+    int end = at_i + 1;
+    Rng y = out_rng(at);
+    if (tr && tr->op == OP_TRANSPOSE && tr->n_inputs >= 1 && tr->inputs[0] == at->output && is_f32(tr) &&
+        tr->n_dims == 4 && tr->extra[0] == B && tr->extra[1] == Hq && tr->extra[2] == 1 && tr->extra[3] == S &&
+        tr->extra[4] == hd) {
+        std::vector<Rng> inter2 = inter;
+        inter2.push_back(out_rng(at));
+        if (!any_overlap(out_rng(tr), reads) && dead_after(nodes, n, at_i + 2, inter2, {out_rng(tr)}, live)) {
+            inter = inter2;
+            y = out_rng(tr);
+            end = at_i + 2;
+        }
+    }
+    if (any_overlap(y, reads) || !dead_after(nodes, n, end, inter, {y}, live)) return false;
+    f->first = first;
+    f->count = end - first;
+    f->kind = LBR_FUSE_ATTN_SLICED_V;
+    f->attn_at = at_i - first;
+    f->src = src;
+    f->ld = ld;
+    f->col_begin[0] = col0;
+    f->Hs[0] = Hq;
+    f->Hs[1] = H;
+    f->out = end == at_i + 2 ? tr->output : at->output;
+    return true;
+}
+
 bool gemm_step(const OpNode* g, Step* st) {
     if (g->op != OP_MATMUL && g->op != OP_MATMUL_ADD) return false;
     *st = Step();
@@ -631,6 +689,37 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
             }
             lbr_set_error("");
         }
+        // ATTN_SLICED_V: V of the attention two nodes on is SLICE(C, last dim) →
+        // TRANSPOSE(S,H), read from C's columns ...
+        if (nd->op == OP_SLICE && nd->n_inputs >= 1 && nd->extra[4] == 1 && is_f32(nd)) {
+            HeadChain hc;
+            const long long rows = nd->extra[0];
+            const int ld = nd->extra[1];
+            FusedRun f;
+            if (match_head_chain(nodes, n, i, nd->inputs[0], rows, ld, false, &hc) && !hc.bias && hc.count == 2) {
+                std::vector<Rng> inter = hc.inter;
+                inter.push_back(hc.out_r);
+                if (match_attn_sliced_v(nodes, n, i, i + 2, nd->inputs[0], ld, hc.col0, hc.B, hc.S, hc.H, hc.hd,
+                                        hc.out, inter, live, &f)) {
+                    out->push_back(f);
+                    i += f.count;
+                    continue;
+                }
+            }
+        }
+        // ... or V of the next attention is TRANSPOSE(S,H) of a [B, S, H, hd] tensor, read
+        // in place
+        if (nd->op == OP_TRANSPOSE && nd->n_inputs >= 1 && is_f32(nd) && nd->n_dims == 4 && nd->extra[2] == 1) {
+            const int B = nd->extra[0], S = nd->extra[1], H = nd->extra[3], hd = nd->extra[4];
+            FusedRun f;
+            if (nd->out_shape[0] == B && nd->out_shape[1] == H && nd->out_shape[2] == S && nd->out_shape[3] == hd &&
+                match_attn_sliced_v(nodes, n, i, i + 1, nd->inputs[0], H * hd, 0, B, S, H, hd, nd->output,
+                                    {out_rng(nd)}, live, &f)) {
+                out->push_back(f);
+                i += f.count;
+                continue;
+            }
+        }
         // HEAD_PROLOGUE: a SLICE of a row-major [rows, ld] tensor
         if (nd->op == OP_SLICE && nd->n_inputs >= 1 && nd->extra[4] == 1 && is_f32(nd)) {
             HeadChain hc;
@@ -701,6 +790,21 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
         s->out = (void*)f.out;
         s->i[9] = f.Hs[0];
         s->name = "attn_fwd_mfma16_f32+transpose";
+    } else if (f.kind == LBR_FUSE_ATTN_SLICED_V) {
+        const int at = f.first + f.attn_at;
+        int rc = decode_attention(&nodes[at], s);
+        if (rc) return rc;
+        if (s->i[10] != 1) {
+            lbr_set_error("fusion: attention node %d cannot read a strided V", at);
+            return LBR_ERR_INVALID;
+        }
+        s->in[2] = (const float*)f.src + f.col_begin[0];
+        s->i[12] = f.ld;
+        s->i[13] = f.Hs[1];
+        s->out = (void*)f.out;
+        const bool tout = f.count == f.attn_at + 2;   // the output TRANSPOSE(H,S) joined the run
+        if (tout) s->i[9] = f.Hs[0];
+        s->name = tout ? "attn_fwd_mfma16_f32+v+transpose" : "attn_fwd_mfma16_f32+v";
     } else if (f.kind == LBR_FUSE_TRANSPOSE_GEMM) {
         int rc = decode_matmul(&nodes[f.first + 1], s);
         if (rc) return rc;

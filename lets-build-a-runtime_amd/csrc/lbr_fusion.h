@@ -36,6 +36,11 @@ struct FusedRun {
     const void* gbias = nullptr;
     // TRANSPOSE_GEMM: the GEMM's A in head layout [B, H, S, hd] at `src`; `resid` /
     // `out` set when the residual ADD is fused as well (B, S, hd and Hs[0] = H)
+    // ATTN_SLICED_V: the ATTENTION is node first + attn_at; V rows come from `src`
+    // ([B·S, ld] row-major) at column col_begin[0], Hs[1] K/V heads; Hs[0] query
+    // heads; `out` is the attention output or, when the run ends with its
+    // TRANSPOSE(H,S), that transpose's output
+    int attn_at = 0;
 };
 
 // Fusable runs of nodes[0..n) in stream order; live-out ranges are the

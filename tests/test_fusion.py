@@ -65,13 +65,15 @@ EXPECTED = {
     # c_attn is MATMUL_ADD (bias already in the GEMM): three (slice, transpose) chains per layer;
     # c_proj's output lands over the attention output it would read (transpose kept)
     "gpt2": Counter({("gemm_heads", 7): 2, ("gemm_resid", 2): 4, ("gemm_act", 2): 2}),
-    # q/k: slice → per-head RMSNorm → transpose → 7-node RoPE as one kernel; v's transpose lands
-    # over the QKV rows it reads at this size (refused); the attention output transpose is fused
-    # here, while in the other workloads the planner places it over the dead V (refused); at
-    # S=64 the gated FFN output lands over the gate/up GEMM's input (refused)
-    "qwen3_4b": Counter({("head_prologue", 10): 4, ("gemm_resid", 2): 4, ("attn_transpose", 2): 2}),
+    # q/k: slice → per-head RMSNorm → transpose → 7-node RoPE as one kernel; v's slice copy
+    # stays (its transpose would land over the QKV rows it reads, and the attention output lands
+    # over QKV too), while v's transpose, the attention and its output transpose are one kernel
+    # reading V from the slice (in the other workloads the planner places the output transpose
+    # over the dead V: refused); at S=64 the gated FFN output lands over the gate/up GEMM's
+    # input (refused)
+    "qwen3_4b": Counter({("head_prologue", 10): 4, ("gemm_resid", 2): 4, ("attn_sliced_v", 3): 2}),
     # at the benchmark length the merged gate/up GEMM → two half slices → SiLU gate is one GEMM
-    "qwen3_4b@1024": Counter({("head_prologue", 10): 4, ("gemm_resid", 2): 4, ("attn_transpose", 2): 2,
+    "qwen3_4b@1024": Counter({("head_prologue", 10): 4, ("gemm_resid", 2): 4, ("attn_sliced_v", 3): 2,
                               ("gemm_gated", 4): 2}),
 }
 
@@ -279,6 +281,47 @@ def test_attention_transpose_refuses_output_over_v():
 def test_attention_transpose_needs_the_16x16_kernel():
     # head dim 256 runs the 32x32 kernel, which writes [bh, S, hd] only
     assert _windows(_attn_transpose(40 * MB, hd=256)) == []
+
+
+def _sliced_v(v_src_off, att_off, out_off, sliced=False, hd=64, later=()):
+    """[SLICE of the V columns of [S, 3·Hkv·hd] rows at v_src_off →] TRANSPOSE(S,H) → V of a GQA
+    ATTENTION (8 query heads, 2 K/V heads) → output TRANSPOSE(H,S) at out_off, then `later`."""
+    B, H, Hkv, S = 1, 8, 2, 128
+    nodes = []
+    t_in = ARENA + v_src_off
+    if sliced:
+        ld = 3 * Hkv * hd
+        nodes.append(_node(OpType.SLICE, [t_in], ARENA + 40 * MB, (B, S, Hkv * hd),
+                           (B * S, ld, 2 * Hkv * hd, Hkv * hd, 1)))
+        t_in = ARENA + 40 * MB
+    tv = _node(OpType.TRANSPOSE, [t_in], ARENA + 44 * MB, (B, Hkv, S, hd), (B, S, 1, Hkv, hd))
+    att = _node(OpType.ATTENTION, [ARENA + 16 * MB, ARENA + 18 * MB, ARENA + 44 * MB, ARENA + 30 * MB],
+                ARENA + att_off, (B, H, S, hd), (S, hd, 1, 0, H // Hkv))
+    tr = _node(OpType.TRANSPOSE, [ARENA + att_off], ARENA + out_off, (B, S, H, hd), (B, H, 1, S, hd))
+    return nodes + [tv, att, tr, *later]
+
+
+def test_attention_sliced_v_fuses():
+    # V's transpose, the attention and its output transpose: the kernel reads V from the
+    # transpose's [B, S, Hkv·hd] input
+    assert _windows(_sliced_v(0, 24 * MB, 26 * MB)) == [(0, 3, "attn_sliced_v")]
+    # from the slice's source rows (its columns 2·Hkv·hd ..), without the slice copy
+    assert _windows(_sliced_v(0, 24 * MB, 26 * MB, sliced=True)) == [(0, 4, "attn_sliced_v")]
+
+
+def test_attention_sliced_v_refusals():
+    # the attention output over the rows V is read from is fine while the output transpose
+    # joins the run (the fused kernel never writes it) ...
+    assert _windows(_sliced_v(24 * MB, 24 * MB, 26 * MB)) == [(0, 3, "attn_sliced_v")]
+    # ... but not when the final output lands there: the plain output transpose fusion only
+    assert _windows(_sliced_v(24 * MB, 24 * MB, 24 * MB)) == [(1, 2, "attn_transpose")]
+    # the output transpose over V's source: the attention joins, its output transpose does not
+    assert _windows(_sliced_v(26 * MB, 24 * MB, 26 * MB)) == [(0, 2, "attn_sliced_v")]
+    # the transposed V read again later: it must be written
+    reader = _node(OpType.RELU, [ARENA + 44 * MB], ARENA + 50 * MB, (1, 2, 128, 64))
+    assert _windows(_sliced_v(0, 24 * MB, 26 * MB, later=[reader])) == [(1, 2, "attn_transpose")]
+    # head dim 256 runs the 32x32 kernel, which reads V as [bh, S, hd] only
+    assert _windows(_sliced_v(0, 24 * MB, 26 * MB, hd=256)) == []
 
 
 # ------------------------------------------------------------ activation epilogues

@@ -5,6 +5,9 @@
 * the gated pair MATMUL[_ADD] with 2F columns → SLICE [0,F) and [F,2F) →
   GATED_ACT(gate, [bias], up), computed by one GEMM whose tiles pair gate
   and up columns,
+* TRANSPOSE → MATMUL[_ADD] → [ADD], the GEMM reading A in head layout, and
+  SLICE → TRANSPOSE → ATTENTION → TRANSPOSE, the attention reading V from
+  the sliced tensor's columns,
 
 each against the float64 closed form, the CPU oracle, and the same graph run
 node by node (fusion off): the bits must be identical, since the epilogue
@@ -170,3 +173,43 @@ def test_transpose_gemm(monkeypatch, tile, ks, H, S, hd, N, bias, resid):
         out = "y"
     g.outputs.append(out)
     _check(g, inputs, c, "transpose_gemm")
+
+
+@pytest.mark.parametrize("split", [None, "3"])
+@pytest.mark.parametrize("H,Hkv,S,hd,causal", [(8, 2, 300, 128, True), (4, 4, 200, 64, False),
+                                               (12, 4, 1024, 64, True)])
+def test_attention_sliced_v(monkeypatch, split, H, Hkv, S, hd, causal):
+    """kv [1, S, 2·Hkv·hd] → SLICE (V columns) → RESHAPE → TRANSPOSE(1, 2) → V of a GQA ATTENTION →
+    TRANSPOSE(1, 2): one attention kernel reading the V rows from kv's columns with kv's row
+    stride (the sliced and transposed copies are never made), under the plain and the split
+    (LBR_ATTN_SPLIT=3: shares of 3 key tiles) schedules."""
+    from helpers import cf_attention
+    if split:
+        monkeypatch.setenv("LBR_ATTN_SPLIT", split)
+        monkeypatch.setenv("LBR_ATTN_FOLD", "0")
+    r = rng(H * S + hd)
+    W = Hkv * hd
+    q = randn(r, 1, H, S, hd)
+    k = randn(r, 1, Hkv, S, hd)
+    kv = randn(r, 1, S, 2 * W)
+    g = Graph()
+    for name, arr in (("q", q), ("k", k), ("kv", kv)):
+        g.add_tensor(name, arr.shape)
+        g.inputs.append(name)
+    g.add_tensor("v2", (1, S, W))
+    g.add_node(OpType.SLICE, ["kv"], "v2", {"dim": 2, "start": W, "end": 2 * W})
+    g.add_tensor("v4", (1, S, Hkv, hd))
+    g.add_node(OpType.RESHAPE, ["v2"], "v4", {"shape": (1, S, Hkv, hd)})
+    g.add_tensor("vt", (1, Hkv, S, hd))
+    g.add_node(OpType.TRANSPOSE, ["v4"], "vt", {"dim0": 1, "dim1": 2})
+    attrs = {"group_size": H // Hkv}
+    if causal:
+        attrs["causal"] = True
+    g.add_tensor("att", (1, H, S, hd))
+    g.add_node(OpType.ATTENTION, ["q", "k", "vt"], "att", attrs)
+    g.add_tensor("out", (1, S, H, hd))
+    g.add_node(OpType.TRANSPOSE, ["att"], "out", {"dim0": 1, "dim1": 2})
+    g.outputs.append("out")
+    v = np.ascontiguousarray(kv[..., W:].reshape(1, S, Hkv, hd).transpose(0, 2, 1, 3))
+    ref = np.swapaxes(cf_attention(q, k, v, causal=causal, group=H // Hkv), 1, 2)
+    _check(g, {"q": q, "k": k, "kv": kv}, ref, "attn_sliced_v")
