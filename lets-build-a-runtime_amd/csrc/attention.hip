@@ -851,19 +851,25 @@ int decode_attention(const OpNode* n, Step* s) {
             const char* fold = getenv("LBR_ATTN_FOLD");
             if (fold) s->i[6] = causal && atoi(fold) != 0;
             // Grids that leave CUs idle (fewer than two 8-wavefront workgroups per
-            // CU, not folded) take the key-range split: two workgroups per CU with
-            // equal shares of all key tiles, shares of at least 8 tiles (4 for
-            // hd <= 64) since every segment pays a Q load, the first tile's
-            // latency and, when cut, a partial; no split when that gives no more
+            // CU, not folded) take the key-range split: equal shares of all key
+            // tiles, of at least 8 tiles (4 for hd <= 64) since every segment pays
+            // a Q load, the first tile's latency and, when cut, a partial.  The
+            // workgroup count is a whole number of rounds over the CUs (two
+            // workgroups per CU, or one) when the shares allow it — a partial
+            // round leaves some CUs with twice the work (measured: Qwen3 shares
+            // of 8 tiles, 576 workgroups, 134 µs against 110 µs for 9-tile shares
+            // on 512; GPT-2 256 workgroups 36 µs against 38 µs on 432) — else
+            // one workgroup per minimum share.  No split when that gives no more
             // workgroups than the plain grid.  LBR_ATTN_SPLIT=<n> forces shares
-            // of n tiles (0: no split).
+            // of n tiles (0: no split), LBR_ATTN_SPLIT_WG=<n> n workgroups.
             long long head_tiles = 0;
             for (int q = 0; q < nq; ++q) head_tiles += attn16_block_tiles(seq, causal != 0, q);
             const long long total = head_tiles * bh;
             long long wg = 0;
             if (!s->i[6] && nq * bh < 2LL * cus) {
                 const int min_share = hd <= 64 ? 4 : 8;
-                wg = std::min(2LL * cus, total / min_share);
+                const long long rounds = std::min(2LL, total / ((long long)min_share * cus));
+                wg = rounds > 0 ? rounds * cus : total / min_share;
                 if (wg <= nq * bh) wg = 0;
             }
             const char* split = getenv("LBR_ATTN_SPLIT");
@@ -871,6 +877,8 @@ int decode_attention(const OpNode* n, Step* s) {
                 const long long n = atoi(split);
                 wg = n > 0 ? (total + n - 1) / n : 0;
             }
+            const char* split_wg = getenv("LBR_ATTN_SPLIT_WG");   // forces the workgroup count
+            if (split_wg) wg = std::max(0, atoi(split_wg));
             wg = std::min(wg, total);   // every share holds at least one tile
             if (wg > 0 && !s->i[6]) {
                 const int maxseg = attn16_max_segments(seq, causal != 0, bh, wg);

@@ -185,13 +185,15 @@ def test_attention(B, H, S, hd, causal, group):
 # LBR_ATTN_SPLIT=c the key-range split: every workgroup an equal share of c
 # key tiles (32 keys) of the whole (head, query block, tile) sequence, plus
 # the merge kernel (c=1: every tile its own segment; c=3, 7: shares that cut
-# blocks at varying offsets and span several blocks and heads).
+# blocks at varying offsets and span several blocks and heads);
+# LBR_ATTN_SPLIT_WG=7 seven workgroups, shares of a non-integer tile count.
 @pytest.mark.parametrize("env", [{"LBR_ATTN_FOLD": "1"}, {"LBR_ATTN_TILE": "32"},
                                  {"LBR_ATTN_SPLIT": "1", "LBR_ATTN_FOLD": "0"},
                                  {"LBR_ATTN_SPLIT": "3", "LBR_ATTN_FOLD": "0"},
                                  {"LBR_ATTN_SPLIT": "7", "LBR_ATTN_FOLD": "0"},
-                                 {"LBR_ATTN_SPLIT": "8", "LBR_ATTN_FOLD": "0"}],
-                         ids=["fold", "tile32", "split1", "split3", "split7", "split8"])
+                                 {"LBR_ATTN_SPLIT": "8", "LBR_ATTN_FOLD": "0"},
+                                 {"LBR_ATTN_SPLIT_WG": "7", "LBR_ATTN_FOLD": "0"}],
+                         ids=["fold", "tile32", "split1", "split3", "split7", "split8", "wg7"])
 @pytest.mark.parametrize("B,H,S,hd,causal,group", [
     (1, 4, 257, 128, True, 1),      # 3 query blocks: pair (2, 0) and the middle block 1 alone
     (1, 8, 512, 64, True, 2),       # 4 query blocks: pairs (3, 0), (2, 1)
