@@ -9,16 +9,25 @@
 // inputs [Q, K, V, scratch] or [Q, K, V, mask, scratch].  The planner's
 // scratch slot is not needed: the online-softmax state lives in registers.
 //
-// One single-pass online-softmax kernel serves every sequence length (the
+// Single-pass online-softmax kernels serve every sequence length (the
 // reference's S ≤ 256 / mask path and its flash path compute the same
-// function).  Layout choice: the kernel computes Sᵀ = K·Qᵀ and Oᵀ = Vᵀ·Pᵀ with
-// v_mfma_f32_32x32x2_f32, so in both accumulators lane l owns query row
-// q0 + l%32.  The running max / sum and the rescale of O are then per-lane
-// scalars, the row max needs one cross-half exchange (lane l ↔ l^32), and
-// the exponentiated scores are fed straight back as the B operand of the
-// P·V product without leaving registers.
+// function).  Layout choice: they compute Sᵀ = K·Qᵀ and Oᵀ = Vᵀ·Pᵀ, so in both
+// accumulators a lane owns one query row: the running max / sum and the
+// rescale of O are per-lane scalars, and the exponentiated scores are fed
+// straight back as the B operand of the P·V product without leaving
+// registers.
 //
-// Workgroup = 4 wavefronts × 32 query rows = 128 rows of one (batch·head);
+// * attn_fwd_mfma16 (hd ≤ 128, the main path): v_mfma_f32_16x16x4_f32,
+//   8 wavefronts × 16 query rows = 128 rows per workgroup; a row's scores are
+//   spread over 4 lanes (exchanged with permlane swaps).  Interior key tiles
+//   run without mask code, the softmax reference max moves only in steps of
+//   more than 2^8, and the row sum is reduced once at the end.  Causal grids
+//   fold query blocks in pairs; small grids split the key range
+//   (attn_fwd_mfma16_split + attn_split_merge).
+// * attn_fwd_mfma (128 < hd ≤ 256): v_mfma_f32_32x32x2_f32, 4 wavefronts × 32
+//   query rows, a row's scores in 2 lanes (lane l ↔ l^32).
+// * attn_fwd_rows (hd % 8 != 0): one workgroup per query row, scores in LDS.
+//
 // K/V tiles of 32 keys are staged in LDS (zero-filled past S and past hd);
 // the next tile is fetched into registers while the current one is consumed
 // from LDS, so global-load latency hides behind the MFMAs.  Exponentials use
