@@ -853,7 +853,7 @@ constexpr DmaTile kDmaTiles[] = {
     {128, 128, 2, 0.92, "128x128"},   // 4 wavefronts (2×2), 64 KB LDS
     {128, 64, 3, 0.90, "128x64"},     // 4 wavefronts (2×2), 48 KB LDS
     {64, 128, 3, 0.90, "64x128"},
-    {64, 64, 4, 0.85, "64x64"},       // 4 wavefronts (2×2) of 32×32, 32 KB LDS
+    {64, 64, 4, 0.90, "64x64"},       // 4 wavefronts (2×2) of 32×32, 32 KB LDS
 };
 constexpr int kNumDmaTiles = sizeof(kDmaTiles) / sizeof(kDmaTiles[0]);
 
