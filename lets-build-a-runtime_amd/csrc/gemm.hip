@@ -844,16 +844,16 @@ void launch_gemm_dma(const Step& s, hipStream_t st) {
 // Tile shapes of the DMA GEMM: (TM, TN), workgroups resident per CU (LDS
 // and registers), and measured steady-state fraction of the fp32 MFMA peak.
 struct DmaTile {
-    int tm, tn, occ;
+    int tm, tn, occ, waves;
     double eff;
     const char* name;
 };
 constexpr DmaTile kDmaTiles[] = {
-    {256, 256, 1, 0.94, "256x256"},   // 8 wavefronts (4×2), 128 KB LDS
-    {128, 128, 2, 0.92, "128x128"},   // 4 wavefronts (2×2), 64 KB LDS
-    {128, 64, 3, 0.90, "128x64"},     // 4 wavefronts (2×2), 48 KB LDS
-    {64, 128, 3, 0.90, "64x128"},
-    {64, 64, 4, 0.90, "64x64"},       // 4 wavefronts (2×2) of 32×32, 32 KB LDS
+    {256, 256, 1, 8, 0.94, "256x256"},   // 8 wavefronts (4×2), 128 KB LDS
+    {128, 128, 2, 4, 0.92, "128x128"},   // 4 wavefronts (2×2), 64 KB LDS
+    {128, 64, 3, 4, 0.90, "128x64"},     // 4 wavefronts (2×2), 48 KB LDS
+    {64, 128, 3, 4, 0.90, "64x128"},
+    {64, 64, 4, 4, 0.90, "64x64"},       // 4 wavefronts (2×2) of 32×32, 32 KB LDS
 };
 constexpr int kNumDmaTiles = sizeof(kDmaTiles) / sizeof(kDmaTiles[0]);
 
@@ -861,7 +861,11 @@ constexpr int kNumDmaTiles = sizeof(kDmaTiles) / sizeof(kDmaTiles[0]);
 // busiest CU runs ceil(items / CUs) workgroups of TM·TN·kchunk MACs each
 // at the tile's efficiency, in rounds of `occ` resident workgroups that
 // each pay ~3 µs of first-load latency and epilogue; a K split adds writing
-// and re-reading the partial sums at ~5 TB/s plus a reduction launch.
+// and re-reading the partial sums at ~5 TB/s plus a reduction launch.  A CU
+// left with fewer than 8 resident wavefronts (one 4-wavefront workgroup)
+// runs its tile at 0.9 of the efficiency: measured on GPT-2's FFN2 (1024 ×
+// 768 × 3072, 192 tiles of 64×64), one workgroup per CU took 55.8 µs, and
+// four K ranges, three workgroups per CU, took 46.3 µs.
 // LBR_GEMM_TILE (a tile name) and LBR_GEMM_KSPLIT override the choice.
 void choose_dma(long long M, long long N, int K, long long batches, int cus, int* tile, int* ksplit, int* kchunk) {
     const double peak_cu = 157.3e12 / 256.0;
@@ -885,7 +889,8 @@ void choose_dma(long long M, long long N, int K, long long batches, int cus, int
                 continue;
             }
             const long long per_cu = (tiles * s_eff + cus - 1) / cus;
-            double t_s = (double)per_cu * 2.0 * d.tm * d.tn * chunk / (d.eff * peak_cu);
+            const double eff = std::min<long long>(per_cu, d.occ) * d.waves < 8 ? 0.9 * d.eff : d.eff;
+            double t_s = (double)per_cu * 2.0 * d.tm * d.tn * chunk / (eff * peak_cu);
             t_s += (double)((per_cu + d.occ - 1) / d.occ) * 3e-6;   // per round: first DMA, epilogue
             if (s_eff > 1) t_s += (2.0 * s_eff + 1.0) * M * N * batches * 4.0 / 5e12 + 4e-6;
             if (s_eff > 1 && !force_ks) t_s *= 1.05;   // split only for a clear gain
