@@ -67,6 +67,9 @@ struct AttnArgs {
     int sk_head_tiles;           // key tiles of one head
     float* part;                 // split partials Σ p·V: [bh][query block][sk_maxseg][128 rows][D]
     float* ml;                   // split running max and Σ p, same slots: [..][128 rows][2]
+    int sk_defer;                // 1: every block's rows go through the workspace and
+                                 // attn_split_merge writes all of O, after the split kernel
+                                 // has read Q, K and V (O may then lie over them)
     int o_heads;                 // 0: O is [bh, S, D]; H > 0: O is [B, S, H, D] (fused transpose)
     // V read from the columns of a row-major [B·S, v_ld] tensor (16x16 kernel, fused
     // SLICE → TRANSPOSE): row s of K/V head b·v_heads + h at V + (b·S + s)·v_ld + h·D.
@@ -606,9 +609,11 @@ __global__ __launch_bounds__(A16_NT, 4) void attn_fwd_mfma16_split(AttnArgs g) {
             nt = attn16_tiles(g, ++qb, CAUSAL);
         }
         const int t1 = (int)min((long long)nt, t0 + (end - G));
-        // a block cut by a share boundary: segment index = this workgroup − the owner of its first tile
-        const long long slot =
-            (t0 > 0 || t1 < nt) ? (bh * g.n_qblocks + qb) * g.sk_maxseg + (w - sk_owner(g, G - t0)) : -1;
+        // a block cut by a share boundary (or any block, deferred): segment index = this
+        // workgroup − the owner of its first tile
+        const long long slot = (g.sk_defer || t0 > 0 || t1 < nt)
+                                   ? (bh * g.n_qblocks + qb) * g.sk_maxseg + (w - sk_owner(g, G - t0))
+                                   : -1;
         attn16_qblock<DP, CAUSAL, HAS_MASK, true>(g, (int)bh, qb, t0, t1, slot, Ks, Vs);
         G += t1 - t0;
     }
@@ -616,7 +621,9 @@ __global__ __launch_bounds__(A16_NT, 4) void attn_fwd_mfma16_split(AttnArgs g) {
 
 // Combine the key-range partials of every query row whose block was split:
 // O = Σ_c 2^(m_c − M)·acc_c / Σ_c 2^(m_c − M)·l_c, M = max_c m_c, segments
-// summed in key order.  Rows of unsplit blocks return.  Thread t of a row
+// summed in key order.  Rows of unsplit blocks return, unless g.sk_defer:
+// then their single partial is normalised here (weight 2^0 = 1, so the
+// result is bit-identical to the direct store).  Thread t of a row
 // handles d = 4t .. 4t+3 (D % 4 == 0 on this path), so a row of hd = 128
 // takes 32 threads and every load and store is a float4.
 __global__ __launch_bounds__(256) void attn_split_merge(AttnArgs g, int causal) {
@@ -630,7 +637,7 @@ __global__ __launch_bounds__(256) void attn_split_merge(AttnArgs g, int causal) 
     const long long G0 = bh * g.sk_head_tiles + sk_block_start(g, qb, causal != 0);
     const long long G1 = G0 + attn16_tiles(g, qb, causal != 0);
     const int nc = (int)(sk_owner(g, G1 - 1) - sk_owner(g, G0)) + 1;
-    if (nc <= 1) return;
+    if (nc <= 1 && !g.sk_defer) return;
     const long long r0 = (bh * g.n_qblocks + qb) * g.sk_maxseg * A16_QB + (row - (long long)qb * A16_QB);
     float M = -FLT_MAX;
     for (int c = 0; c < nc; ++c) M = fmaxf(M, g.ml[2 * (r0 + (long long)c * A16_QB)]);
@@ -699,6 +706,7 @@ __global__ __launch_bounds__(256) void attn_fwd_rows(AttnArgs g, int causal) {
 //          [9]=heads of a fused output transpose (0 = none) [10]=16x16 kernel (transpose fusable)
 //          [11]=key tiles per head (split) [12]=V row stride when V is read from the columns
 //          of a row-major tensor (0 = contiguous) [13]=K/V heads of that layout
+//          [14]=deferred output (split only: the merge kernel writes every row of O)
 AttnArgs make_args(const Step& s) {
     AttnArgs g;
     g.Q = (const float*)s.in[0];
@@ -713,6 +721,7 @@ AttnArgs make_args(const Step& s) {
     g.scale_log2 = s.f[0] * LOG2E;
     g.fold = 0;
     g.o_heads = 0;
+    g.sk_defer = 0;
     g.v_ld = 0;
     g.v_heads = 1;
     return g;
@@ -753,6 +762,7 @@ void launch_attn16(const Step& s, hipStream_t st) {
         const long long rows = s.i[0] * g.n_qblocks * (long long)g.sk_maxseg * A16_QB;
         g.part = (float*)s.ws;
         g.ml = g.part + rows * g.D;
+        g.sk_defer = s.i[14] != 0;
         hipLaunchKernelGGL((attn_fwd_mfma16_split<DP, CAUSAL, HAS_MASK>), dim3((unsigned)g.sk_wg), dim3(A16_NT), 0, st,
                            g);
         hipLaunchKernelGGL(attn_split_merge, dim3((unsigned)(((long long)g.S * (g.D / 4) + 255) / 256), (unsigned)s.i[0]),

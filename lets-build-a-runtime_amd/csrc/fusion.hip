@@ -409,6 +409,8 @@ bool match_attn_sliced_v(const OpNode* nodes, int n, int first, int at_i, const 
     std::vector<Rng> reads{rng(at->inputs[0], q_bytes), rng(at->inputs[1], q_bytes / group),
                            rng(src, (long long)B * S * ld * 4)};
     if (at->extra[3] != 0) reads.push_back(rng(at->inputs[3], (long long)B * Hq * S * S * 4));
+    // under the key-range split the output may lie over what the kernel reads (deferred store)
+    const bool split = as.i[7] > 0;
     const OpNode* tr = at_i + 1 < n ? &nodes[at_i + 1] : nullptr;
     int end = at_i + 1;
     Rng y = out_rng(at);
@@ -417,13 +419,15 @@ bool match_attn_sliced_v(const OpNode* nodes, int n, int first, int at_i, const 
         tr->extra[4] == hd) {
         std::vector<Rng> inter2 = inter;
         inter2.push_back(out_rng(at));
-        if (!any_overlap(out_rng(tr), reads) && dead_after(nodes, n, at_i + 2, inter2, {out_rng(tr)}, live)) {
+        if ((split || !any_overlap(out_rng(tr), reads)) && dead_after(nodes, n, at_i + 2, inter2, {out_rng(tr)}, live)) {
             inter = inter2;
             y = out_rng(tr);
             end = at_i + 2;
         }
     }
-    if (any_overlap(y, reads) || !dead_after(nodes, n, end, inter, {y}, live)) return false;
+    const bool over = any_overlap(y, reads);
+    if ((over && !split) || !dead_after(nodes, n, end, inter, {y}, live)) return false;
+    f->defer = over;
     f->first = first;
     f->count = end - first;
     f->kind = LBR_FUSE_ATTN_SLICED_V;
@@ -445,6 +449,59 @@ bool gemm_step(const OpNode* g, Step* st) {
         return false;
     }
     return st->i[13] == 1;
+}
+
+// TRANSPOSE_GEMM at node i: T = TRANSPOSE(O [B, H, S, hd] → [B, S, H, hd]) is the A
+// operand of the next GEMM (DMA kernel, one batch, hd a multiple of its 32-wide K
+// step): the GEMM reads O directly; a residual ADD right after it is taken into the
+// epilogue as well.
+bool match_transpose_gemm(const OpNode* nodes, int n, int i, const std::vector<Rng>& live, FusedRun* f) {
+    const OpNode* nd = &nodes[i];
+    if (!(nd->op == OP_TRANSPOSE && i + 1 < n && is_f32(nd) && nd->n_dims == 4 && nd->n_inputs >= 1 &&
+          nd->extra[2] == 1))
+        return false;
+    const int B = nd->extra[0], H = nd->extra[1], S = nd->extra[3], hd = nd->extra[4];
+    const OpNode* mm = &nodes[i + 1];
+    Step ms;
+    if (!(nd->out_shape[0] == B && nd->out_shape[1] == S && nd->out_shape[2] == H && nd->out_shape[3] == hd &&
+          hd % 32 == 0 && mm->n_inputs >= 2 && mm->inputs[0] == nd->output && is_f32(mm) && gemm_step(mm, &ms) &&
+          ms.i[14] && ms.i[3] == 1 && ms.i[0] == (long long)B * S && ms.i[2] == (long long)H * hd &&
+          lbr_aligned(nd->inputs[0], 16)))
+        return false;
+    std::vector<Rng> reads;
+    gemm_input_rngs(mm, ms, &reads);
+    reads[0] = rng(nd->inputs[0], (long long)B * H * S * hd * 4);   // A is read as O
+    const Rng t_r = out_rng(nd), c_r = out_rng(mm);
+    *f = FusedRun();
+    f->first = i;
+    f->kind = LBR_FUSE_TRANSPOSE_GEMM;
+    f->src = nd->inputs[0];
+    f->B = B;
+    f->S = S;
+    f->hd = hd;
+    f->Hs[0] = H;
+    // with the residual ADD: y = C + R
+    if (i + 2 < n) {
+        const OpNode* ad = &nodes[i + 2];
+        if (ad->op == OP_ADD && ad->n_inputs >= 2 && ad->extra[0] == 1 && is_f32(ad) &&
+            node_total(ad) == node_total(mm) && (ad->inputs[0] == mm->output) != (ad->inputs[1] == mm->output)) {
+            const void* R = ad->inputs[0] == mm->output ? ad->inputs[1] : ad->inputs[0];
+            const Rng y = out_rng(ad), r_r = rng(R, node_total(mm) * 4);
+            if (!any_overlap(y, reads) && (y.lo == r_r.lo || !overlap(y, r_r)) &&
+                dead_after(nodes, n, i + 3, {t_r, c_r}, {y}, live)) {
+                f->count = 3;
+                f->resid = R;
+                f->out = ad->output;
+                return true;
+            }
+        }
+    }
+    if (!any_overlap(c_r, reads) && dead_after(nodes, n, i + 2, {t_r}, {c_r}, live)) {
+        f->count = 2;
+        f->out = mm->output;
+        return true;
+    }
+    return false;
 }
 
 }  // namespace
@@ -606,57 +663,13 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
             ++i;
             continue;
         }
-        // TRANSPOSE_GEMM: T = TRANSPOSE(O [B, H, S, hd] → [B, S, H, hd]) is the A operand of the
-        // next GEMM (DMA kernel, one batch, hd a multiple of its 32-wide K step): the GEMM reads
-        // O directly; a residual ADD right after it is taken into the epilogue as well
-        if (nd->op == OP_TRANSPOSE && i + 1 < n && is_f32(nd) && nd->n_dims == 4 && nd->n_inputs >= 1 &&
-            nd->extra[2] == 1) {
-            const int B = nd->extra[0], H = nd->extra[1], S = nd->extra[3], hd = nd->extra[4];
-            const OpNode* mm = &nodes[i + 1];
-            Step ms;
-            if (nd->out_shape[0] == B && nd->out_shape[1] == S && nd->out_shape[2] == H && nd->out_shape[3] == hd &&
-                hd % 32 == 0 && mm->n_inputs >= 2 && mm->inputs[0] == nd->output && is_f32(mm) &&
-                gemm_step(mm, &ms) && ms.i[14] && ms.i[3] == 1 && ms.i[0] == (long long)B * S &&
-                ms.i[2] == (long long)H * hd && lbr_aligned(nd->inputs[0], 16)) {
-                std::vector<Rng> reads;
-                gemm_input_rngs(mm, ms, &reads);
-                reads[0] = rng(nd->inputs[0], (long long)B * H * S * hd * 4);   // A is read as O
-                const Rng t_r = out_rng(nd), c_r = out_rng(mm);
-                FusedRun f;
-                f.first = i;
-                f.kind = LBR_FUSE_TRANSPOSE_GEMM;
-                f.src = nd->inputs[0];
-                f.B = B;
-                f.S = S;
-                f.hd = hd;
-                f.Hs[0] = H;
-                bool done = false;
-                // with the residual ADD: y = C + R
-                if (i + 2 < n) {
-                    const OpNode* ad = &nodes[i + 2];
-                    if (ad->op == OP_ADD && ad->n_inputs >= 2 && ad->extra[0] == 1 && is_f32(ad) &&
-                        node_total(ad) == node_total(mm) && (ad->inputs[0] == mm->output) != (ad->inputs[1] == mm->output)) {
-                        const void* R = ad->inputs[0] == mm->output ? ad->inputs[1] : ad->inputs[0];
-                        const Rng y = out_rng(ad), r_r = rng(R, node_total(mm) * 4);
-                        if (!any_overlap(y, reads) && (y.lo == r_r.lo || !overlap(y, r_r)) &&
-                            dead_after(nodes, n, i + 3, {t_r, c_r}, {y}, live)) {
-                            f.count = 3;
-                            f.resid = R;
-                            f.out = ad->output;
-                            done = true;
-                        }
-                    }
-                }
-                if (!done && !any_overlap(c_r, reads) && dead_after(nodes, n, i + 2, {t_r}, {c_r}, live)) {
-                    f.count = 2;
-                    f.out = mm->output;
-                    done = true;
-                }
-                if (done) {
-                    out->push_back(f);
-                    i += f.count;
-                    continue;
-                }
+        // TRANSPOSE_GEMM: the GEMM after a head-layout transpose reads O directly
+        {
+            FusedRun f;
+            if (match_transpose_gemm(nodes, n, i, live, &f)) {
+                out->push_back(f);
+                i += f.count;
+                continue;
             }
         }
         // ATTN_TRANSPOSE: attention output [B, H, S, hd] transposed to [B, S, H, hd]
@@ -674,14 +687,20 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
                 std::vector<Rng> reads{rng(nd->inputs[0], qkv), rng(nd->inputs[1], qkv / group),
                                        rng(nd->inputs[2], qkv / group)};
                 if (mask) reads.push_back(rng(nd->inputs[3], (long long)B * H * S * S * 4));
+                // under the key-range split the output may lie over them (deferred store),
+                // unless the transpose can go into the next GEMM instead, which costs nothing
                 const Rng y = out_rng(tr);
-                if (!any_overlap(y, reads) && dead_after(nodes, n, i + 2, {out_rng(nd)}, {y}, live)) {
+                const bool over = any_overlap(y, reads);
+                FusedRun tg;
+                const bool defer_ok = as.i[7] > 0 && !match_transpose_gemm(nodes, n, i + 1, live, &tg);
+                if ((!over || defer_ok) && dead_after(nodes, n, i + 2, {out_rng(nd)}, {y}, live)) {
                     FusedRun f;
                     f.first = i;
                     f.count = 2;
                     f.kind = LBR_FUSE_ATTN_TRANSPOSE;
                     f.out = tr->output;
                     f.Hs[0] = H;
+                    f.defer = over;
                     out->push_back(f);
                     i += 2;
                     continue;
@@ -790,6 +809,14 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
         s->out = (void*)f.out;
         s->i[9] = f.Hs[0];
         s->name = "attn_fwd_mfma16_f32+transpose";
+        if (f.defer) {
+            if (s->i[7] <= 0) {
+                lbr_set_error("fusion: attention node %d writes over its inputs without the split", f.first);
+                return LBR_ERR_INVALID;
+            }
+            s->i[14] = 1;
+            s->name = "attn_fwd_mfma16_f32+transpose+defer";
+        }
     } else if (f.kind == LBR_FUSE_ATTN_SLICED_V) {
         const int at = f.first + f.attn_at;
         int rc = decode_attention(&nodes[at], s);
@@ -805,6 +832,14 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
         const bool tout = f.count == f.attn_at + 2;   // the output TRANSPOSE(H,S) joined the run
         if (tout) s->i[9] = f.Hs[0];
         s->name = tout ? "attn_fwd_mfma16_f32+v+transpose" : "attn_fwd_mfma16_f32+v";
+        if (f.defer) {
+            if (s->i[7] <= 0) {
+                lbr_set_error("fusion: attention node %d writes over its inputs without the split", at);
+                return LBR_ERR_INVALID;
+            }
+            s->i[14] = 1;
+            s->name = tout ? "attn_fwd_mfma16_f32+v+transpose+defer" : "attn_fwd_mfma16_f32+v+defer";
+        }
     } else if (f.kind == LBR_FUSE_TRANSPOSE_GEMM) {
         int rc = decode_matmul(&nodes[f.first + 1], s);
         if (rc) return rc;

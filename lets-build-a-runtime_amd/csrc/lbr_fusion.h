@@ -41,6 +41,10 @@ struct FusedRun {
     // heads; `out` is the attention output or, when the run ends with its
     // TRANSPOSE(H,S), that transpose's output
     int attn_at = 0;
+    // ATTN_TRANSPOSE / ATTN_SLICED_V: the final output lies over memory the attention
+    // reads; taken only under the key-range split, whose merge kernel then writes every
+    // row (after the split kernel has finished reading)
+    bool defer = false;
 };
 
 // Fusable runs of nodes[0..n) in stream order; live-out ranges are the

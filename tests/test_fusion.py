@@ -72,9 +72,18 @@ EXPECTED = {
     # over the dead V: refused); at S=64 the gated FFN output lands over the gate/up GEMM's
     # input (refused)
     "qwen3_4b": Counter({("head_prologue", 10): 4, ("gemm_resid", 2): 4, ("attn_sliced_v", 3): 2}),
-    # at the benchmark length the merged gate/up GEMM → two half slices → SiLU gate is one GEMM
-    "qwen3_4b@1024": Counter({("head_prologue", 10): 4, ("gemm_resid", 2): 4, ("attn_sliced_v", 3): 2,
+    # at the benchmark length the merged gate/up GEMM → two half slices → SiLU gate is one GEMM,
+    # and the attention takes the key-range split, whose merge kernel writes every output row
+    # after all of Q, K and V have been read: v's slice joins the attention run although the
+    # output lands over the QKV rows
+    "qwen3_4b@1024": Counter({("head_prologue", 10): 4, ("gemm_resid", 2): 4, ("attn_sliced_v", 4): 2,
                               ("gemm_gated", 4): 2}),
+    # likewise the output transpose over the dead V, when the attention is split
+    "gpt2@1024": Counter({("gemm_heads", 7): 2, ("gemm_resid", 2): 4, ("gemm_act", 2): 2,
+                          ("attn_transpose", 2): 2}),
+    # ... but where the transpose can go into the O projection instead, that is taken
+    "gpt2w@512": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1,
+                          ("transpose_gemm", 3): 1}),
 }
 
 
@@ -276,6 +285,26 @@ def test_attention_transpose_fuses():
 def test_attention_transpose_refuses_output_over_v():
     # the planner may reuse V's memory once attention is done; one fused kernel still reads V
     assert _windows(_attn_transpose(20 * MB)) == []
+
+
+def _split_attn_transpose(out_off, H=12, S=1024, hd=64, later=()):
+    """A causal attention small enough to take the key-range split (12 heads × 8 query blocks
+    of 128 rows on 256 CUs) → output TRANSPOSE(H,S) at out_off; Q, K, V at 16, 24, 32 MB."""
+    q, k, v = ARENA + 16 * MB, ARENA + 24 * MB, ARENA + 32 * MB
+    att = _node(OpType.ATTENTION, [q, k, v, ARENA + 60 * MB], ARENA + 40 * MB, (1, H, S, hd), (S, hd, 1, 0, 1))
+    att.n_inputs = 4
+    tr = _node(OpType.TRANSPOSE, [ARENA + 40 * MB], ARENA + out_off, (1, S, H, hd), (1, H, 1, S, hd))
+    return [att, tr, *later]
+
+
+def test_split_attention_transpose_may_write_over_its_inputs():
+    # the split's merge kernel writes every row once the split kernel has read Q, K and V
+    for off in (16, 24, 32):
+        assert _windows(_split_attn_transpose(off * MB)) == [(0, 2, "attn_transpose")]
+    # ... unless a GEMM right after takes the transpose (reading the head layout): that
+    # costs no extra pass over the rows
+    w = _node(OpType.MATMUL, [ARENA + 32 * MB, W_], ARENA + 48 * MB, (1, 1024, 256), (768, 1, 1, 0))
+    assert _windows(_split_attn_transpose(32 * MB, later=[w])) == [(1, 2, "transpose_gemm")]
 
 
 def test_attention_transpose_needs_the_16x16_kernel():

@@ -8,6 +8,8 @@
 * TRANSPOSE → MATMUL[_ADD] → [ADD], the GEMM reading A in head layout, and
   SLICE → TRANSPOSE → ATTENTION → TRANSPOSE, the attention reading V from
   the sliced tensor's columns,
+* ATTENTION → TRANSPOSE with the output over V (split attention, the merge
+  kernel writing every row),
 
 each against the float64 closed form, the CPU oracle, and the same graph run
 node by node (fusion off): the bits must be identical, since the epilogue
@@ -213,3 +215,37 @@ def test_attention_sliced_v(monkeypatch, split, H, Hkv, S, hd, causal):
     v = np.ascontiguousarray(kv[..., W:].reshape(1, S, Hkv, hd).transpose(0, 2, 1, 3))
     ref = np.swapaxes(cf_attention(q, k, v, causal=causal, group=H // Hkv), 1, 2)
     _check(g, {"q": q, "k": k, "kv": kv}, ref, "attn_sliced_v")
+
+
+@pytest.mark.parametrize("H,S,hd,causal", [(12, 1024, 64, True), (8, 640, 128, True), (4, 700, 64, False)])
+def test_attention_transpose_over_v(H, S, hd, causal):
+    """V = RELU(x) lives in the arena and is dead after an ATTENTION small enough for the
+    key-range split; the planner puts the output TRANSPOSE(1, 2) over V's memory.  The fused
+    kernel sends every row through the split's workspace and the merge kernel, which runs
+    after V has been read, writes the [B, S, H, hd] output (bit-identical to the direct store)."""
+    from helpers import cf_attention
+    from runtime.executor.compiled import CompiledExecutor
+    from runtime.planner import plan
+    r = rng(H * S + hd)
+    q, k, x = randn(r, 1, H, S, hd), randn(r, 1, H, S, hd), randn(r, 1, H, S, hd)
+    g = Graph()
+    for name in ("q", "k", "x"):
+        g.add_tensor(name, (1, H, S, hd))
+        g.inputs.append(name)
+    g.add_tensor("v", (1, H, S, hd))
+    g.add_node(OpType.RELU, ["x"], "v", {})
+    g.add_tensor("att", (1, H, S, hd))
+    g.add_node(OpType.ATTENTION, ["q", "k", "v"], "att", {"causal": True} if causal else {})
+    g.add_tensor("out", (1, S, H, hd))
+    g.add_node(OpType.TRANSPOSE, ["att"], "out", {"dim0": 1, "dim1": 2})
+    g.outputs.append("out")
+    mem = plan(g)
+    assert mem.offsets["out"] == mem.offsets["v"]
+    ex = CompiledExecutor(fuse=True)
+    ex.compile(mem)
+    try:
+        assert any(n.endswith("+transpose+defer") for n in ex.kernel_names())
+    finally:
+        ex.close()
+    ref = np.swapaxes(cf_attention(q, k, np.maximum(x, 0.0), causal=causal), 1, 2)
+    _check(g, {"q": q, "k": k, "x": x}, ref, "attn_transpose")
