@@ -851,8 +851,8 @@ struct DmaTile {
 constexpr DmaTile kDmaTiles[] = {
     {256, 256, 1, 8, 0.94, "256x256"},   // 8 wavefronts (4×2), 128 KB LDS
     {128, 128, 2, 4, 0.92, "128x128"},   // 4 wavefronts (2×2), 64 KB LDS
-    {128, 64, 3, 4, 0.90, "128x64"},     // 4 wavefronts (2×2), 48 KB LDS
-    {64, 128, 3, 4, 0.90, "64x128"},
+    {128, 64, 3, 4, 0.9225, "128x64"},   // 4 wavefronts (2×2), 48 KB LDS
+    {64, 128, 3, 4, 0.9225, "64x128"},
     {64, 64, 4, 4, 0.90, "64x64"},       // 4 wavefronts (2×2) of 32×32, 32 KB LDS
 };
 constexpr int kNumDmaTiles = sizeof(kDmaTiles) / sizeof(kDmaTiles[0]);
