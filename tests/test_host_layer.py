@@ -128,7 +128,9 @@ def test_dim0_slice_alias_arena_known_answer():
     np.testing.assert_array_equal(OracleRun(p).run({"x": x})["out"], np.maximum(x, 0)[4:8])
 
 
-# ---------------------------------------------------------------- node streams (derived in SURVEY §8(a))
+# ---------------------------------------------------------------- node streams
+# The dispatched node sequence of a custom block after the reference's default
+# passes (runtime/passes/passes.py pipeline; merged QKV, three head chains).
 
 BLOCK_STREAM = ["LAYERNORM", "MATMUL", "SLICE", "SLICE", "SLICE", "ADD", "ADD", "ADD", "TRANSPOSE", "TRANSPOSE",
                 "TRANSPOSE", "ATTENTION", "TRANSPOSE", "MATMUL_ADD", "ADD", "LAYERNORM", "MATMUL_ADD", "GELU",
