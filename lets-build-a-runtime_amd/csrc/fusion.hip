@@ -692,8 +692,8 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
                 const Rng y = out_rng(tr);
                 const bool over = any_overlap(y, reads);
                 FusedRun tg;
-                const bool defer_ok = as.i[7] > 0 && !match_transpose_gemm(nodes, n, i + 1, live, &tg);
-                if ((!over || defer_ok) && dead_after(nodes, n, i + 2, {out_rng(nd)}, {y}, live)) {
+                const bool ok = !over || (as.i[7] > 0 && !match_transpose_gemm(nodes, n, i + 1, live, &tg));
+                if (ok && dead_after(nodes, n, i + 2, {out_rng(nd)}, {y}, live)) {
                     FusedRun f;
                     f.first = i;
                     f.count = 2;
