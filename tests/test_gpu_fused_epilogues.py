@@ -217,6 +217,51 @@ def test_attention_sliced_v(monkeypatch, split, H, Hkv, S, hd, causal):
     _check(g, {"q": q, "k": k, "kv": kv}, ref, "attn_sliced_v")
 
 
+@pytest.mark.parametrize("H,S,hd", [(12, 1024, 64), (8, 640, 128)])
+def test_attention_sliced_v_over_its_source(H, S, hd):
+    """kv = RELU(kv_in) in the arena → SLICE (V columns) → RESHAPE → TRANSPOSE → V of a causal
+    ATTENTION small enough for the key-range split → TRANSPOSE: the planner puts the output over
+    kv's rows, which the fused kernel reads V from.  The run is still one kernel: every row
+    goes through the split's workspace and the merge kernel writes the output after kv has
+    been read (bit-identical to the plan without fusion)."""
+    from helpers import cf_attention
+    from runtime.executor.compiled import CompiledExecutor
+    from runtime.planner import plan
+    r = rng(H * S + hd + 1)
+    W = H * hd
+    q, k, kv_in = randn(r, 1, H, S, hd), randn(r, 1, H, S, hd), randn(r, 1, S, 2 * W)
+    g = Graph()
+    for name, arr in (("q", q), ("k", k), ("kv_in", kv_in)):
+        g.add_tensor(name, arr.shape)
+        g.inputs.append(name)
+    g.add_tensor("kv", (1, S, 2 * W))
+    g.add_node(OpType.RELU, ["kv_in"], "kv", {})
+    g.add_tensor("v2", (1, S, W))
+    g.add_node(OpType.SLICE, ["kv"], "v2", {"dim": 2, "start": W, "end": 2 * W})
+    g.add_tensor("v4", (1, S, H, hd))
+    g.add_node(OpType.RESHAPE, ["v2"], "v4", {"shape": (1, S, H, hd)})
+    g.add_tensor("vt", (1, H, S, hd))
+    g.add_node(OpType.TRANSPOSE, ["v4"], "vt", {"dim0": 1, "dim1": 2})
+    g.add_tensor("att", (1, H, S, hd))
+    g.add_node(OpType.ATTENTION, ["q", "k", "vt"], "att", {"causal": True})
+    g.add_tensor("out", (1, S, H, hd))
+    g.add_node(OpType.TRANSPOSE, ["att"], "out", {"dim0": 1, "dim1": 2})
+    g.outputs.append("out")
+    mem = plan(g)
+    kv0, out0 = mem.offsets["kv"], mem.offsets["out"]
+    assert out0 < kv0 + S * 2 * W * 4 and kv0 < out0 + S * W * 4   # the output lies over kv
+    ex = CompiledExecutor(fuse=True)
+    ex.compile(mem)
+    try:
+        assert any(n.endswith("+v+transpose+defer") for n in ex.kernel_names())
+    finally:
+        ex.close()
+    kv = np.maximum(kv_in, 0.0)
+    v = np.ascontiguousarray(kv[..., W:].reshape(1, S, H, hd).transpose(0, 2, 1, 3))
+    ref = np.swapaxes(cf_attention(q, k, v, causal=True), 1, 2)
+    _check(g, {"q": q, "k": k, "kv_in": kv_in}, ref, "attn_sliced_v")
+
+
 @pytest.mark.parametrize("H,S,hd,causal", [(12, 1024, 64, True), (8, 640, 128, True), (4, 700, 64, False)])
 def test_attention_transpose_over_v(H, S, hd, causal):
     """V = RELU(x) lives in the arena and is dead after an ATTENTION small enough for the
