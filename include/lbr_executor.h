@@ -111,8 +111,22 @@ int lbr_memset(void* dst_device, int value, size_t bytes);
 /* Drop-in for execute(OpNode*, int) (csrc/executor.c:458-467): launch every
  * node in order on the library stream and wait for completion.  Returns
  * LBR_ERR_UNSUPPORTED for an op without a kernel (where the reference
- * aborts), LBR_ERR_INVALID for a node whose fields do not fit its op. */
+ * aborts), LBR_ERR_INVALID for a node whose fields do not fit its op.
+ * Every node is decoded and checked before the first launch.  Kernels that
+ * need a workspace (GEMM split-K partial sums, attention key-range
+ * partials) share one library-owned device block that grows to the largest
+ * need seen and is kept for later calls; calls are serialised. */
 int lbr_execute(const OpNode* nodes, int n_nodes);
+
+/* The reference's symbol itself, `void execute(OpNode* nodes, int n_nodes)`
+ * (csrc/executor.c:458), bound by name in runtime/executor/common.py:157-159
+ * with restype None.  Same behaviour as lbr_execute; the returned status is
+ * ignored by that binding and can be read by callers that declare c_int. */
+int execute(const OpNode* nodes, int n_nodes);
+
+/* Bytes of the one-shot workspace currently held (0 before any call that
+ * needed one). */
+int lbr_execute_workspace_bytes(size_t* out_bytes);
 
 /* Plans: validate and decode the node array once; launches reuse the
  * decoded kernel arguments.  With use_graph != 0 the launch sequence is
@@ -198,6 +212,15 @@ int lbr_plan_create_fused(const OpNode* nodes, int n_nodes, int use_graph,
 int lbr_plan_num_steps(const lbr_plan* plan);
 int lbr_plan_step_info(const lbr_plan* plan, int step, int* first_node,
                        int* n_nodes, int* kind);
+
+/* The decoded integer launch arguments of step `step` (up to `cap` of them,
+ * 40 at most), for tests and reports.  Their meaning is the kernel's: for
+ * the attention kernel [6] = causal blocks folded in pairs, [7] = key-range
+ * split workgroups (0: no split), [14] = deferred output; for the GEMM
+ * kernels [10] = K ranges, [14] = DMA tile index + 1 (0: register-staged
+ * kernel). */
+int lbr_plan_step_args(const lbr_plan* plan, int step, long long* ints_out,
+                       int cap);
 
 #ifdef __cplusplus
 }

@@ -73,6 +73,40 @@ static int ensure_init() {
     return lbr_init(0);
 }
 
+// Workspace of the one-shot entry points (lbr_execute / execute): owned by
+// the library, grown when a call needs more and never shrunk, so repeated
+// calls allocate nothing.  Every one-shot call ends with a stream
+// synchronisation, so when the next call grows it no kernel still uses the
+// old block.  Guarded by g_exec_mu (the one-shot calls are serialised, as
+// the reference's execute is single-caller).
+static std::mutex g_exec_mu;
+static void* g_exec_ws = nullptr;
+static size_t g_exec_ws_bytes = 0;
+static int g_exec_ws_device = -1;
+
+static int exec_workspace(size_t need, void** out) {
+    if (g_exec_ws && g_exec_ws_device != g_device) {
+        // the library moved to another device: the old block belongs to that one
+        int cur = g_device;
+        HIP_TRY(hipSetDevice(g_exec_ws_device));
+        (void)hipFree(g_exec_ws);
+        HIP_TRY(hipSetDevice(cur));
+        g_exec_ws = nullptr;
+        g_exec_ws_bytes = 0;
+    }
+    if (need > g_exec_ws_bytes) {
+        if (g_exec_ws) HIP_TRY(hipFree(g_exec_ws));
+        g_exec_ws = nullptr;
+        g_exec_ws_bytes = 0;
+        const size_t grown = (need + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);   // whole MiB
+        HIP_TRY(hipMalloc(&g_exec_ws, grown));
+        g_exec_ws_bytes = grown;
+        g_exec_ws_device = g_device;
+    }
+    *out = need ? g_exec_ws : nullptr;
+    return LBR_OK;
+}
+
 // ------------------------------------------------------------------ dispatch table
 typedef int (*decode_fn)(const OpNode*, Step*);
 
@@ -323,21 +357,40 @@ int lbr_execute(const OpNode* nodes, int n_nodes) {
     int rc = ensure_init();
     if (rc) return rc;
     std::vector<Step> steps((size_t)n_nodes);
+    size_t need = 0;
     for (int i = 0; i < n_nodes; ++i) {
         rc = decode_node(&nodes[i], i, &steps[i]);
         if (rc) return rc;
+        need = steps[i].ws_bytes > need ? steps[i].ws_bytes : need;
     }
+    std::lock_guard<std::mutex> lock(g_exec_mu);
     void* ws = nullptr;
-    rc = assign_workspace(steps, &ws);
+    rc = exec_workspace(need, &ws);
     if (rc) return rc;
+    for (Step& s : steps) s.ws = ws;
     run_steps(steps, g_stream);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
-    if (ws) (void)hipFree(ws);
     if (e != hipSuccess) {
         lbr_set_error("lbr_execute: %s", hipGetErrorString(e));
         return LBR_ERR_HIP;
     }
+    return LBR_OK;
+}
+
+// The reference's entry point by its own name (csrc/executor.c:458), so its
+// ctypes binding (runtime/executor/common.py:157-159: argtypes
+// [POINTER(COpNode), c_int], restype None) resolves unchanged.  Same work as
+// lbr_execute; the int status is there for callers that read it.
+int execute(const OpNode* nodes, int n_nodes) { return lbr_execute(nodes, n_nodes); }
+
+int lbr_execute_workspace_bytes(size_t* out_bytes) {
+    if (!out_bytes) {
+        lbr_set_error("lbr_execute_workspace_bytes: null out_bytes");
+        return LBR_ERR_INVALID;
+    }
+    std::lock_guard<std::mutex> lock(g_exec_mu);
+    *out_bytes = g_exec_ws_bytes;
     return LBR_OK;
 }
 
@@ -393,6 +446,16 @@ int lbr_plan_step_info(const lbr_plan* p, int step, int* first_node, int* n_node
     if (first_node) *first_node = p->steps[step].node_index;
     if (n_nodes) *n_nodes = p->steps[step].n_nodes;
     if (kind) *kind = p->steps[step].fuse_kind;
+    return LBR_OK;
+}
+
+int lbr_plan_step_args(const lbr_plan* p, int step, long long* ints_out, int cap) {
+    const int n = (int)(sizeof(Step::i) / sizeof(Step::i[0]));
+    if (!p || step < 0 || step >= (int)p->steps.size() || cap < 0 || (cap > 0 && !ints_out)) {
+        lbr_set_error("lbr_plan_step_args: bad arguments");
+        return LBR_ERR_INVALID;
+    }
+    for (int k = 0; k < cap && k < n; ++k) ints_out[k] = p->steps[step].i[k];
     return LBR_OK;
 }
 

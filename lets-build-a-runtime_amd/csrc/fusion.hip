@@ -178,6 +178,91 @@ Rng out_rng(const OpNode* n) {
     return {p, p + (uintptr_t)(node_total(n) * (n->elem_size > 0 ? n->elem_size : 4))};
 }
 
+long long prod_dims(const OpNode* n, int lo, int hi) {
+    long long r = 1;
+    for (int d = lo; d < hi && d < n->n_dims; ++d) r *= n->out_shape[d];
+    return r;
+}
+
+// Bytes input k of node nd reads: the per-op rule the host layer checks
+// before launch (elements from the output shape and the extras, times the
+// element size; token ids are int64).  An extent the node does not fix (an
+// EMBEDDING table with no row count, an op outside the table) reaches to the
+// top of the address space, which can only make the liveness walk refuse
+// more.
+Rng input_rng(const OpNode* nd, int k) {
+    const uintptr_t p = (uintptr_t)nd->inputs[k];
+    const long long es = nd->elem_size > 0 ? nd->elem_size : 4;
+    const long long total = node_total(nd), last = node_last_dim(nd);
+    const long long lead = last ? total / last : 0;
+    const int* x = nd->extra;
+    long long e = -1;   // elements read; −1: not fixed by the node
+    auto bcast = [&](int base) {   // [ndim, a strides, b strides, out shape] at extra[base]
+        const int nd_ = x[base];
+        if (nd_ < 0 || base + 1 + 3 * nd_ > MAX_DIMS || k > 1) return -1LL;
+        long long span = 1;
+        for (int d = 0; d < nd_; ++d) {
+            const long long s = x[base + 1 + 2 * nd_ + d];
+            if (s == 0) return 0LL;
+            span += (s - 1) * x[base + 1 + k * nd_ + d];
+        }
+        return span;
+    };
+    switch (nd->op) {
+        case OP_RELU: case OP_EXP: case OP_TANH: case OP_POW: case OP_GELU: case OP_RSQRT: case OP_SILU:
+        case OP_NEG: case OP_COS: case OP_SIN: case OP_SOFTMAX: case OP_RESHAPE:
+            e = k == 0 ? total : -1;
+            break;
+        case OP_ADD:   // modes: 0 bias row, 1 same shape, 2 scalar, 3 broadcast
+            e = x[0] == 3 ? bcast(1) : (k == 0 || x[0] == 1) ? total : x[0] == 0 ? last : -1;
+            break;
+        case OP_SUB: case OP_MUL: case OP_DIV:   // modes: 0 same shape, 1 scalar, 2 broadcast
+            e = x[0] == 2 ? bcast(1) : (k == 0 || x[0] == 0) ? total : -1;
+            break;
+        case OP_MAX: case OP_SUM:
+            e = x[0] >= 0 ? prod_dims(nd, 0, x[0]) * x[1] * prod_dims(nd, x[0], nd->n_dims) : (long long)x[1] * total;
+            break;
+        case OP_MATMUL: case OP_MATMUL_ADD: {
+            const long long K = x[0], N = last;
+            const bool b2d = x[2] != 0;
+            const long long M = b2d ? lead : (nd->n_dims >= 2 ? nd->out_shape[nd->n_dims - 2] : 1);
+            const long long batches = b2d ? 1 : prod_dims(nd, 0, nd->n_dims - 2);
+            e = k == 0 ? batches * M * K : k == 1 ? batches * N * K : k == 2 ? N : -1;
+            break;
+        }
+        case OP_TRANSPOSE:
+            e = nd->n_dims == 2 ? (long long)x[0] * x[1] : (long long)x[0] * x[1] * x[2] * x[3] * x[4];
+            break;
+        case OP_SLICE:
+            e = (long long)x[0] * x[1] * x[4];
+            break;
+        case OP_CAT:
+            e = (x[0] >= 0 && k < MAX_DIMS - 1)
+                    ? prod_dims(nd, 0, x[0]) * x[1 + k] * prod_dims(nd, x[0] + 1, nd->n_dims) : -1;
+            break;
+        case OP_EMBEDDING:
+            if (k == 0) return {p, p + (uintptr_t)(lead * 8)};
+            e = x[1] > 0 ? (long long)x[1] * last : -1;
+            break;
+        case OP_LAYERNORM: case OP_RMSNORM: case OP_FUSED_BIAS_RELU:
+            e = k == 0 ? total : last;
+            break;
+        case OP_GATED_ACT:
+            e = (x[0] != 0 && k == 1) ? last : total;
+            break;
+        case OP_ATTENTION: {
+            const long long S = x[0], hd = x[1], group = x[4] > 0 ? x[4] : 1;
+            const long long bh = prod_dims(nd, 0, nd->n_dims - 2), kvh = bh ? (bh - 1) / group + 1 : 0;
+            e = k == 0 ? bh * S * hd : k <= 2 ? kvh * S * hd : (k == 3 && x[3]) ? bh * S * S : -1;
+            break;
+        }
+        default:
+            break;
+    }
+    if (e < 0) return {p, UINTPTR_MAX};
+    return {p, p + (uintptr_t)(e * es)};
+}
+
 Rng rng(const void* p, long long bytes) { return {(uintptr_t)p, (uintptr_t)p + (uintptr_t)bytes}; }
 
 bool contains(Rng r, const void* p) { return (uintptr_t)p >= r.lo && (uintptr_t)p < r.hi; }
@@ -200,8 +285,9 @@ void subtract(std::vector<Rng>* inter, Rng w) {
 
 // Values the run [first, end) writes to `inter` are dead once the run is
 // over: the parts its own final outputs `outs` overwrite do not count;
-// walking the later nodes in order, no input pointer lands in a part not
-// yet overwritten, and what is left at the end overlaps no live-out range.
+// walking the later nodes in order, no input's read extent (input_rng)
+// overlaps a part not yet overwritten, and what is left at the end overlaps
+// no live-out range.
 bool dead_after(const OpNode* nodes, int n, int end, std::vector<Rng> inter, const std::vector<Rng>& outs,
                 const std::vector<Rng>& live) {
     for (const Rng& o : outs) subtract(&inter, o);
@@ -210,9 +296,11 @@ bool dead_after(const OpNode* nodes, int n, int end, std::vector<Rng> inter, con
         // ATTENTION's trailing input is the planner's scratch slot (ops.py:437-459):
         // written before it is read, so it is not a read of older values
         const int reads = nd->op == OP_ATTENTION ? 3 + (nd->extra[3] != 0) : nd->n_inputs;
-        for (int k = 0; k < reads && k < nd->n_inputs && k < MAX_INPUTS; ++k)
+        for (int k = 0; k < reads && k < nd->n_inputs && k < MAX_INPUTS; ++k) {
+            const Rng in = input_rng(nd, k);
             for (const Rng& r : inter)
-                if (contains(r, nd->inputs[k])) return false;
+                if (overlap(r, in)) return false;
+        }
         subtract(&inter, out_rng(nd));
     }
     for (const Rng& r : inter)
@@ -414,9 +502,10 @@ bool match_attn_sliced_v(const OpNode* nodes, int n, int first, int at_i, const 
     const OpNode* tr = at_i + 1 < n ? &nodes[at_i + 1] : nullptr;
     int end = at_i + 1;
     Rng y = out_rng(at);
+    // the kernel stores the transposed rows as float4s: the transpose output must be 16-byte aligned
     if (tr && tr->op == OP_TRANSPOSE && tr->n_inputs >= 1 && tr->inputs[0] == at->output && is_f32(tr) &&
         tr->n_dims == 4 && tr->extra[0] == B && tr->extra[1] == Hq && tr->extra[2] == 1 && tr->extra[3] == S &&
-        tr->extra[4] == hd) {
+        tr->extra[4] == hd && lbr_aligned(tr->output, 16)) {
         std::vector<Rng> inter2 = inter;
         inter2.push_back(out_rng(at));
         if ((split || !any_overlap(out_rng(tr), reads)) && dead_after(nodes, n, at_i + 2, inter2, {out_rng(tr)}, live)) {
@@ -677,9 +766,11 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
             const OpNode* tr = &nodes[i + 1];
             Step as = Step();
             const int B = nd->out_shape[0], H = nd->out_shape[1], S = nd->out_shape[2], hd = nd->out_shape[3];
+            // (the kernel stores the transposed rows as float4s: 16-byte aligned output only)
             if (tr->op == OP_TRANSPOSE && tr->n_inputs >= 1 && tr->inputs[0] == nd->output && is_f32(tr) &&
                 tr->n_dims == 4 && tr->extra[0] == B && tr->extra[1] == H && tr->extra[2] == 1 &&
-                tr->extra[3] == S && tr->extra[4] == hd && decode_attention(nd, &as) == LBR_OK && as.i[10] == 1) {
+                tr->extra[3] == S && tr->extra[4] == hd && lbr_aligned(tr->output, 16) &&
+                decode_attention(nd, &as) == LBR_OK && as.i[10] == 1) {
                 // the kernel reads Q, K, V (and the mask) while it writes the transposed output
                 const bool mask = nd->extra[3] != 0;
                 const long long qkv = (long long)B * H * S * hd * 4;

@@ -196,6 +196,28 @@ class CompiledExecutor(Executor):
                 runs.append((first.value, count.value, FUSE_KINDS.get(kind.value, "?")))
         return runs
 
+    def step_params(self) -> list[dict]:
+        """Every kernel step of the compiled plan: its kernel, the nodes it covers, and the
+        schedule its launch arguments encode (attention: causal fold, key-range split
+        workgroups, deferred output; GEMM: DMA tile index, K ranges)."""
+        lib, h = self._lib, self._plan_handle
+        first, count, kind = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        ints = (ctypes.c_longlong * 40)()
+        names = self.kernel_names()
+        out = []
+        for st in range(lib.lbr_plan_num_steps(h)):
+            lib.check(lib.lbr_plan_step_info(h, st, ctypes.byref(first), ctypes.byref(count), ctypes.byref(kind)),
+                      "lbr_plan_step_info")
+            lib.check(lib.lbr_plan_step_args(h, st, ints, 40), "lbr_plan_step_args")
+            d = {"kernel": names[first.value].split("+")[0], "first": first.value, "count": count.value,
+                 "kind": FUSE_KINDS.get(kind.value, "?")}
+            if d["kernel"].startswith("attn_fwd_mfma16"):
+                d.update(fold=bool(ints[6]), split_wg=int(ints[7]), defer=bool(ints[14]))
+            elif d["kernel"].startswith("gemm_"):
+                d.update(ksplit=max(1, int(ints[10])), dma_tile=int(ints[14]) - 1)
+            out.append(d)
+        return out
+
     # ------------------------------------------------------------------ run
     def _upload_inputs(self, inputs: dict[str, np.ndarray]) -> None:
         graph = self._graph

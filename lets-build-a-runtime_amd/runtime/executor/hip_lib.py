@@ -60,6 +60,7 @@ class HipLibrary:
             "lbr_memcpy_d2d": ([c_vp, c_vp, c_size], c_int),
             "lbr_memset": ([c_vp, c_int, c_size], c_int),
             "lbr_execute": ([P(COpNode), c_int], c_int),
+            "lbr_execute_workspace_bytes": ([P(c_size)], c_int),
             "lbr_plan_create": ([P(COpNode), c_int, c_int, P(c_vp)], c_int),
             "lbr_plan_destroy": ([c_vp], c_int),
             "lbr_plan_num_nodes": ([c_vp], c_int),
@@ -73,6 +74,7 @@ class HipLibrary:
             "lbr_plan_create_fused": ([P(COpNode), c_int, c_int, P(c_vp), P(c_size), c_int, P(c_vp)], c_int),
             "lbr_plan_num_steps": ([c_vp], c_int),
             "lbr_plan_step_info": ([c_vp, c_int, P(c_int), P(c_int), P(c_int)], c_int),
+            "lbr_plan_step_args": ([c_vp, c_int, P(ctypes.c_longlong), c_int], c_int),
         }
         for name, (args, res) in sig.items():
             fn = getattr(lib, name)

@@ -167,6 +167,25 @@ def test_gemm_resid_refuses_live_intermediate():
     assert _windows(_gemm_resid(c_off, 4 * MB, later=[writer, reader])) == [(0, 2, "gemm_resid")]
 
 
+def test_gemm_resid_refuses_intermediate_read_from_below():
+    # a later input that starts below C and extends over it still reads C's values: the
+    # liveness walk compares each input's read extent, not just its first byte
+    c_off = 64 * MB
+    reader = _node(OpType.RELU, [ARENA + c_off - 4096], ARENA + 16 * MB, (MB // 4,))
+    assert _windows(_gemm_resid(c_off, 4 * MB, later=[reader])) == []
+    # ... the same read ending where C begins does not
+    short = _node(OpType.RELU, [ARENA + c_off - 4096], ARENA + 16 * MB, (1024,))
+    assert _windows(_gemm_resid(c_off, 4 * MB, later=[short])) == [(0, 2, "gemm_resid")]
+    # a broadcast operand's extent follows its strides: a [M, N] read of a row-broadcast
+    # tensor spans N elements only, so one starting 4 KiB below C ends before it ...
+    bc = [2, 2, N, 1, 0, 1, M, N]   # mode 2 (broadcast), ndim 2, a strides, b strides, shape
+    brd = _node(OpType.MUL, [R_, ARENA + c_off - 4096], ARENA + 16 * MB, (M, N), bc)
+    assert _windows(_gemm_resid(c_off, 4 * MB, later=[brd])) == [(0, 2, "gemm_resid")]
+    # ... while a full-stride one reaches into it
+    full = _node(OpType.MUL, [R_, ARENA + c_off - 4096], ARENA + 16 * MB, (M, N), [2, 2, N, 1, N, 1, M, N])
+    assert _windows(_gemm_resid(c_off, 4 * MB, later=[full])) == []
+
+
 def test_gemm_resid_refuses_intermediate_in_live_out():
     nodes = _gemm_resid(0, 4 * MB)
     assert _windows(nodes, live=[(ARENA + 8, 4)]) == []
@@ -280,6 +299,15 @@ def test_attention_transpose_fuses():
     assert _windows(_attn_transpose(26 * MB)) == [(0, 2, "attn_transpose")]
     # the dead attention output's own memory is fine
     assert _windows(_attn_transpose(24 * MB)) == [(0, 2, "attn_transpose")]
+
+
+def test_attention_transpose_refuses_misaligned_output():
+    # the fused kernel stores the transposed rows as float4s: a planner offset that is not
+    # 16-byte aligned keeps the two nodes apart
+    assert _windows(_attn_transpose(26 * MB + 4)) == []
+    assert _windows(_attn_transpose(26 * MB + 16)) == [(0, 2, "attn_transpose")]
+    # with V read from the source rows, the attention still joins but its output transpose does not
+    assert _windows(_sliced_v(0, 24 * MB, 26 * MB + 8)) == [(0, 2, "attn_sliced_v")]
 
 
 def test_attention_transpose_refuses_output_over_v():

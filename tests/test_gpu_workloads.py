@@ -46,6 +46,41 @@ def test_workload_parity(key, seq):
     assert e_go <= TOL
 
 
+# Full BASELINE sizes where the float64 PyTorch leg would take minutes on the host:
+# the GPU output against the oracle on the same plan and input (the oracle itself is
+# pinned against float64 PyTorch by the reduced-size cases above and by
+# tests/test_oracle.py).  7b4k at S=4096 is the north star's headline case: it runs
+# the folded causal attention schedule (32 blocks x 32 heads fill the chip), the
+# 256x256 DMA GEMM tile and the transposed-A O projection, none of which the S=256
+# case reaches.
+@pytest.mark.parametrize("key,seq,kernels", [
+    ("7b4k", None, {"attn_fwd_mfma16_f32", "gemm_dma_f32_nt"}),
+    ("gpt2_lm", None, {"attn_fwd_mfma16_f32", "gemm_dma_f32_nt"}),
+    ("qwen3_4b_lm", None, {"attn_fwd_mfma16_f32", "gemm_dma_f32_nt"}),
+])
+def test_workload_parity_full_size(key, seq, kernels):
+    import time
+    from workloads import export_workload
+    from oracle.host_exec import OracleRun
+    t0 = time.time()
+    _, x, graph = export_workload(key, seq_len=seq)
+    y, sess = _session_run(graph, x)
+    names = set(sess.executor.kernel_names())
+    if key == "7b4k":
+        # the folded schedule, not the key-range split, at 32 blocks x 32 heads
+        att = [s for s in sess.executor.step_params() if s["kernel"] == "attn_fwd_mfma16_f32"]
+        assert att and all(s["fold"] and not s["split_wg"] for s in att), att
+    t1 = time.time()
+    o = OracleRun(sess.memory_plan).run({graph.inputs[0]: x})[graph.outputs[0]]
+    sess.close()
+    e_go = normwise_rel(y, o)
+    print(f"{key} S={x.shape[1]}: gpu-vs-oracle rel {e_go:.2e} abs {np.abs(y - o).max():.2e} "
+          f"(gpu side {t1 - t0:.1f}s, oracle {time.time() - t1:.1f}s)")
+    assert kernels <= names, names
+    assert np.isfinite(y).all()
+    assert e_go <= TOL
+
+
 @pytest.mark.parametrize("key,seq,kinds", [
     ("toy", None, {"gemm_heads", "gemm_resid", "gemm_act"}),
     ("gpt2", None, {"gemm_heads", "gemm_resid", "gemm_act", "attn_transpose"}),

@@ -44,7 +44,7 @@ def test_header_op_codes_match_ir():
 
 
 def _declared_symbols():
-    return re.findall(r"^\s*(?:const char\*|int)\s+(lbr_[a-z_0-9]+)\s*\(", HEADER.read_text(), re.M)
+    return re.findall(r"^\s*(?:const char\*|int)\s+(lbr_[a-z_0-9]+|execute)\s*\(", HEADER.read_text(), re.M)
 
 
 def test_library_exports_every_declared_symbol():
@@ -53,8 +53,12 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(LIB))
     syms = _declared_symbols()
     assert len(syms) >= 20
+    assert "execute" in syms   # the reference's own symbol, csrc/executor.c:458
     for s in syms:
         assert hasattr(lib, s), s
+    # the reference's binding (runtime/executor/common.py:157-159) resolves unchanged
+    lib.execute.argtypes = [ctypes.POINTER(COpNode), ctypes.c_int]
+    lib.execute.restype = None
     lib.lbr_opnode_size.restype = ctypes.c_int
     assert lib.lbr_opnode_size() == 312
     lib.lbr_version.restype = ctypes.c_char_p
