@@ -43,7 +43,9 @@ def _via_execute(key, seq, execute_fn):
     from runtime.executor.compiled import CompiledExecutor
     from runtime.planner import plan
     from workloads import export_workload
+    from runtime.passes import run_pipeline
     _, x, graph = export_workload(key, seq_len=seq)
+    run_pipeline(graph, None)   # the Session's optimisation passes (pre-transposed weights, merges)
     mp = plan(graph)
     ex = CompiledExecutor(fuse=False)
     ex.compile(mp)
