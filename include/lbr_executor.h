@@ -128,6 +128,21 @@ int execute(const OpNode* nodes, int n_nodes);
  * needed one). */
 int lbr_execute_workspace_bytes(size_t* out_bytes);
 
+/* lbr_execute without any allocation.  No counterpart in the reference
+ * (its execute never allocates, because its kernels need no device
+ * workspace); it is for callers that cannot allocate device memory: code
+ * that must not call hipMalloc/hipFree (serving loops, harnesses that forbid
+ * it).  The workspace is a fixed 128 MiB device array inside the library,
+ * one copy per GPU, held until the process ends; its address is resolved by
+ * lbr_init, which must have run on the current device first (this call does
+ * no set-up).  Node arrays whose kernels need more workspace than that (GEMM
+ * split-K partial sums, attention key-range partials) are rejected with
+ * LBR_ERR_INVALID before anything is launched.  All calls on one GPU share
+ * that array and keep the last call's contents (nothing relies on them);
+ * calls overlapping on one GPU would race on it, so the library serialises
+ * them, and each call waits for its work like lbr_execute. */
+int lbr_execute_noalloc(const OpNode* nodes, int n_nodes);
+
 /* Plans: validate and decode the node array once; launches reuse the
  * decoded kernel arguments.  With use_graph != 0 the launch sequence is
  * captured into a hipGraph at creation and every lbr_plan_launch replays it

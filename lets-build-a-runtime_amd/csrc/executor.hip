@@ -107,6 +107,18 @@ static int exec_workspace(size_t need, void** out) {
     return LBR_OK;
 }
 
+// Workspace of lbr_execute_noalloc: a file-scope device array of a fixed
+// size, one copy per GPU, held until the process ends.  Its host-side name
+// is only a stand-in for the symbol, never a device address: lbr_init
+// resolves the address once per device (hipGetSymbolAddress, that device
+// current) into g_scratch_dev[device], and only that pointer is passed to
+// kernels.  Nothing in it needs to start at zero: the GEMM split-K ranges
+// and the attention key-range segments write every partial they later read.
+#define LBR_SCRATCH_BYTES ((size_t)128 << 20)
+#define LBR_MAX_DEVICES 64
+static __device__ __align__(256) unsigned char scratch[LBR_SCRATCH_BYTES];
+static void* g_scratch_dev[LBR_MAX_DEVICES] = {};
+
 // ------------------------------------------------------------------ dispatch table
 typedef int (*decode_fn)(const OpNode*, Step*);
 
@@ -283,6 +295,16 @@ int lbr_init(int device) {
         lbr_set_error("lbr_init: device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
         return LBR_ERR_NO_DEVICE;
     }
+    // this device's copy of the no-allocation scratch array (see lbr_execute_noalloc)
+    if (device < LBR_MAX_DEVICES && !g_scratch_dev[device]) {
+        void* ptr = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (!ptr) {
+            lbr_set_error("lbr_init: no device address for the scratch array on device %d", device);
+            return LBR_ERR_HIP;
+        }
+        g_scratch_dev[device] = ptr;
+    }
     if (g_stream) {
         (void)hipStreamDestroy(g_stream);
         g_stream = nullptr;
@@ -373,6 +395,55 @@ int lbr_execute(const OpNode* nodes, int n_nodes) {
     if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
     if (e != hipSuccess) {
         lbr_set_error("lbr_execute: %s", hipGetErrorString(e));
+        return LBR_ERR_HIP;
+    }
+    return LBR_OK;
+}
+
+// lbr_execute without any allocation: the workspace is this device's copy
+// of `scratch` (address resolved by lbr_init), the node array is decoded
+// twice into one Step on the stack (every node checked, and the workspace
+// need summed up, before the first launch), and the call needs lbr_init to
+// have run on this device.  Every call on the device shares the array; the
+// library serialises the calls (g_exec_mu) and each ends with a stream
+// synchronisation.
+int lbr_execute_noalloc(const OpNode* nodes, int n_nodes) {
+    if (n_nodes < 0 || (n_nodes > 0 && !nodes)) {
+        lbr_set_error("lbr_execute_noalloc: bad node array");
+        return LBR_ERR_INVALID;
+    }
+    if (!g_stream || g_device < 0 || g_device >= LBR_MAX_DEVICES || !g_scratch_dev[g_device]) {
+        lbr_set_error("lbr_execute_noalloc: call lbr_init(device) first (this entry point does no set-up)");
+        return LBR_ERR_INVALID;
+    }
+    Step s;
+    size_t need = 0;
+    for (int i = 0; i < n_nodes; ++i) {
+        const int rc = decode_node(&nodes[i], i, &s);
+        if (rc) return rc;
+        need = s.ws_bytes > need ? s.ws_bytes : need;
+    }
+    if (need > LBR_SCRATCH_BYTES) {
+        lbr_set_error("lbr_execute_noalloc: the nodes need %zu bytes of workspace; the no-allocation scratch "
+                      "holds %zu (use lbr_execute or a plan)", need, (size_t)LBR_SCRATCH_BYTES);
+        return LBR_ERR_INVALID;
+    }
+    std::lock_guard<std::mutex> lock(g_exec_mu);
+    void* ws = g_scratch_dev[g_device];
+    for (int i = 0; i < n_nodes; ++i) {
+        const int rc = decode_node(&nodes[i], i, &s);
+        if (rc) return rc;
+        if (s.ws_bytes > LBR_SCRATCH_BYTES) {   // the same nodes: cannot differ from the first pass
+            lbr_set_error("lbr_execute_noalloc: node %d needs %zu bytes of workspace", i, s.ws_bytes);
+            return LBR_ERR_INVALID;
+        }
+        s.ws = s.ws_bytes ? ws : nullptr;
+        s.run(s, g_stream);
+    }
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+    if (e != hipSuccess) {
+        lbr_set_error("lbr_execute_noalloc: %s", hipGetErrorString(e));
         return LBR_ERR_HIP;
     }
     return LBR_OK;

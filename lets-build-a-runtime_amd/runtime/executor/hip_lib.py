@@ -61,6 +61,7 @@ class HipLibrary:
             "lbr_memset": ([c_vp, c_int, c_size], c_int),
             "lbr_execute": ([P(COpNode), c_int], c_int),
             "lbr_execute_workspace_bytes": ([P(c_size)], c_int),
+            "lbr_execute_noalloc": ([P(COpNode), c_int], c_int),
             "lbr_plan_create": ([P(COpNode), c_int, c_int, P(c_vp)], c_int),
             "lbr_plan_destroy": ([c_vp], c_int),
             "lbr_plan_num_nodes": ([c_vp], c_int),
