@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark: fp32 forward of a BASELINE workload through Session on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 7b4k]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config KEY]
 
 A step is one forward pass (Session's compiled plan, replayed as a hipGraph)
 over one batch of synthetic input that is already resident in HBM.  W
@@ -9,6 +9,12 @@ untimed warm-up steps, then exactly K steps between two device
 synchronisations; ms_per_step is host wall time / K (hipEvent time on the
 library stream is reported beside it).  value = tokens/s = batch·seq /
 (ms_per_step/1000).
+
+With no --config the headline is the 7B-shaped block at S=4096 (BASELINE
+configs[3]) and `configs` carries the same measurement for every BASELINE
+shape in order (toy, gpt2w, gpt2, 7b4k, qwen3_4b), each with its own
+latency, roofline, kernel table, parity and CPU baseline; --config KEY
+measures one workload only.
 
 Also reported, on the same JSON line:
   roofline      dominant kernel (largest share of device time): algorithmic
@@ -20,7 +26,11 @@ Also reported, on the same JSON line:
   kernels       the same per-kernel figures for every kernel in the step;
   parity        GPU output vs the CPU oracle on the same plan and input;
   cpu_baseline  the oracle (C restatement of the reference CPU executor),
-                one forward of the same workload on the host's cores.
+                the median of three whole forwards of the same workload after
+                a warm-up, on the host's cores; `host` states nproc, the CPU
+                model, OMP_NUM_THREADS and which sgemm ran;
+  latency       single-replay median and the end-to-end Session.run time
+                (input and output copies included).
 
 Only one GPU is used; --gpus above 1 exits with a message.
 """
@@ -44,6 +54,7 @@ import numpy as np  # noqa: E402
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 METRIC = "fp32 forward latency (ms) + tokens/s per shape; MFMA % and HBM GB/s of roofline"
+HEADLINE = "7b4k"   # BASELINE configs[3], the north star's named target
 
 
 def log(*a):
@@ -202,88 +213,78 @@ def calibrate_copy(mib: int) -> int:
     return 0 if ok else 1
 
 
-# ---------------------------------------------------------------- main
+# ---------------------------------------------------------------- host facts
 
-def main() -> int:
-    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="7b4k", help="workload key (toy, gpt2w, gpt2, 7b4k, qwen3_4b, gpt2_lm, qwen3_4b_lm)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-parity", action="store_true", help="skip the GPU-vs-oracle output check")
-    ap.add_argument("--eager", action="store_true", help="launch node by node instead of replaying a hipGraph")
-    ap.add_argument("--nodes", action="store_true", help="log every node's device time and roofline fraction")
-    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
-                    help="only run the library's copy kernel over MIB MiB, 5 times (reference for HBM counters)")
-    ap.add_argument("--save-graph", metavar="STEM",
-                    help="only export the --config workload and write STEM.json + STEM.weights")
-    ap.add_argument("--graph", metavar="STEM",
-                    help="run a saved graph (STEM.json + STEM.weights) instead of exporting --config")
-    args = ap.parse_args()
-    if args.calibrate_copy:
-        return calibrate_copy(args.calibrate_copy)
-    if args.save_graph:
-        from workloads import export_workload
-        _, _, graph = export_workload(args.config)
-        graph.save(args.save_graph)
-        log(f"[bench] wrote {args.save_graph}.json/.weights ({len(graph.nodes)} nodes, {len(graph.constants)} "
-            f"constants) for workload {args.config}")
-        return 0
+def host_facts() -> dict:
+    """What the CPU baseline ran on: core counts, CPU model, thread settings, sgemm."""
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    return {"nproc": affinity, "cpu_count": os.cpu_count(), "cpu_model": model,
+            "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS"),
+            "sgemm": "the oracle's own cache-blocked OpenMP fp32 sgemm (no CBLAS library is linked; the reference "
+                     "links OpenBLAS cblas_sgemm, csrc/Makefile:10-13, which this image does not have)"}
 
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
-              "(the multi-GPU sharding is a design note only; nothing here launches collectives)",
-              file=sys.stderr)
-        return 2
 
+# ---------------------------------------------------------------- one workload
+
+def measure(key: str, args, graph_stem: str | None = None) -> dict:
+    """Export (or load) one workload, compile it through Session, and measure it."""
     from runtime.session import Session
     from workloads import WORKLOADS, export_workload
 
     t0 = time.time()
-    if args.graph:
+    if graph_stem:
         # a saved graph: seeded N(0,1) input of the graph's input shape
         from runtime.ir import Graph
-        graph = Graph.load(args.graph)
+        graph = Graph.load(graph_stem)
         shape = tuple(graph.tensors[graph.inputs[0]].shape)
         x = np.random.default_rng(0).standard_normal(shape).astype(np.float32)
-        wl = type("SavedGraph", (), {"title": f"saved graph {Path(args.graph).name}"})()
-        args.config = Path(args.graph).name
+        title, d_model = f"saved graph {Path(graph_stem).name}", int(shape[-1])
     else:
-        wl = WORKLOADS[args.config]
-        model, x, graph = export_workload(args.config)
+        wl = WORKLOADS[key]
+        model, x, graph = export_workload(key)
         del model
+        title, d_model = wl.title, int(x.shape[2]) if x.ndim == 3 else int(getattr(wl, "d_model", 0))
     sess = Session(graph)
     sess.create(use_graph=not args.eager)
     ex = sess.executor
-    log(f"[bench] {wl.title}: export+optimise+plan+compile {time.time() - t0:.1f}s, "
+    log(f"[bench] {title}: export+optimise+plan+compile {time.time() - t0:.1f}s, "
         f"{len(ex.dispatch_order)} nodes/step, {len(ex.fused_runs())} fused runs, "
         f"arena {sess.plan_stats.arena_bytes / 2**20:.1f} MiB")
 
     ex.upload_inputs({graph.inputs[0]: x})
-    ex.synchronize()
     for _ in range(args.warmup):
         ex.launch()
     ex.synchronize()
-
     t_start = time.perf_counter()
     for _ in range(args.steps):
         ex.launch()
     ex.synchronize()
     wall_ms = (time.perf_counter() - t_start) * 1e3 / args.steps
     event_ms = ex.time_launches(args.steps) / args.steps
-    ms_per_step = wall_ms
     tokens = x.shape[0] * x.shape[1]
     log(f"[bench] {args.steps} steps: {wall_ms:.3f} ms/step wall, {event_ms:.3f} ms/step hipEvent")
     # median of single replays (hipEvent pair around each graph launch), and the end-to-end
     # Session.run wall time with the input H2D and output D2H copies included
-    replay_ms = float(np.median([ex.time_launches(1) for _ in range(max(20, args.steps))]))
+    replays = max(20, args.steps)
+    replay_ms = float(np.median([ex.time_launches(1) for _ in range(replays)]))
     run_wall = []
-    for _ in range(5):
+    for _ in range(6):
         t1 = time.perf_counter()
         sess.run({graph.inputs[0]: x})
         run_wall.append((time.perf_counter() - t1) * 1e3)
-    session_run_ms = float(np.median(run_wall))
+    session_run_ms = float(np.median(run_wall[1:]))      # the first run also allocates pinned output memory
+    io_bytes = x.nbytes + sum(int(np.prod(sess.resolved_graph.tensors[o].shape)) * 4 for o in graph.outputs)
     log(f"[bench] replay median {replay_ms:.3f} ms; Session.run (H2D + replay + D2H) median {session_run_ms:.3f} ms")
 
     # per-kernel device time (eager launches, hipEvent pairs on the library stream)
@@ -308,63 +309,143 @@ def main() -> int:
             f"({100 * r['share']:5.1f}%)  {r['achieved']:9.2f} {r['unit']:<8} {100 * r['frac']:5.1f}% of peak")
 
     y = ex.download_outputs()[graph.outputs[0]]
-    parity = None
-    cpu = None
+    parity = cpu = None
     if not (args.no_parity and args.no_cpu):
         from oracle.host_exec import OracleRun, num_threads
         orc = OracleRun(sess.memory_plan)
-        t1 = time.perf_counter()
-        o = orc.run({graph.inputs[0]: x})[graph.outputs[0]]
-        cpu_s = time.perf_counter() - t1
+        times = []
+        runs_cpu = 1 if args.no_cpu else 4          # one warm-up (also the parity run), then three timed
+        for _ in range(runs_cpu):
+            t1 = time.perf_counter()
+            o = orc.run({graph.inputs[0]: x})[graph.outputs[0]]
+            times.append(time.perf_counter() - t1)
         err = float(np.abs(y.astype(np.float64) - o).max())
         rel = err / float(np.abs(o).max())
         parity = {"vs": "cpu oracle, same plan and input", "max_abs_err": err, "normwise_rel_err": rel,
                   "tolerance": 1e-3, "ok": bool(np.isfinite(y).all() and rel <= 1e-3)}
         log(f"[bench] parity vs oracle: normwise rel {rel:.3e}, max abs {err:.3e}")
         if not args.no_cpu:
+            cpu_s = float(np.median(times[1:]))
             cpu = {"value": round(tokens / cpu_s, 2), "unit": "tokens/s", "cores": num_threads(),
-                   "kind": "port", "ms_per_step": round(cpu_s * 1e3, 1),
-                   "sample": f"one full forward of the same workload ({wl.title}) on the CPU oracle "
-                             f"(C restatement of the reference compiled executor, OpenMP)"}
-            log(f"[bench] cpu oracle: {cpu_s:.2f} s/forward on {num_threads()} threads")
+                   "kind": "port", "ms_per_step": round(cpu_s * 1e3, 2), "runs": len(times) - 1,
+                   "statistic": "median of 3 forwards after 1 warm-up",
+                   "sample": f"whole forward of the same workload ({title}) on the CPU oracle (C restatement of "
+                             f"the reference compiled executor, OpenMP), same plan and input"}
+            log(f"[bench] cpu oracle: {cpu_s * 1e3:.2f} ms/forward (median of {len(times) - 1}) on "
+                f"{num_threads()} threads")
 
-    traffic = committed_traffic(dom["kernel"], args.config)
+    traffic = committed_traffic(dom["kernel"], key)
+    ms_per_step = wall_ms
     result = {
-        "metric": METRIC,
-        "value": round(tokens / (ms_per_step / 1e3), 2),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "event_ms_per_step": round(event_ms, 4),
-        "latency": {"replay_median_ms": round(replay_ms, 4), "replays": max(20, args.steps),
-                    "session_run_median_ms": round(session_run_ms, 4), "session_runs": 5,
-                    "session_run_includes": "input H2D copy, graph replay, output D2H copy"},
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": ("synthetic (seeded uniform token ids" if x.dtype.kind == "i" else
-                 "synthetic (seeded N(0,1) input") + ", random-init N(0,0.02) weights)",
-        "config": {"workload": args.config, "title": wl.title, "batch": int(x.shape[0]),
-                   "seq_len": int(x.shape[1]),
-                   "d_model": int(x.shape[2]) if x.ndim == 3 else int(getattr(wl, "d_model", 0)),
-                   "graph": "hipGraph replay" if not args.eager else "eager launches",
-                   "nodes_per_step": len(ex.dispatch_order), "kernels_per_step": len(units),
-                   "fused_runs": len(runs)},
+        "workload": key, "title": title, "batch": int(x.shape[0]), "seq_len": int(x.shape[1]),
+        "d_model": d_model, "tokens_per_s": round(tokens / (ms_per_step / 1e3), 2),
+        "ms_per_step": round(ms_per_step, 4), "event_ms_per_step": round(event_ms, 4),
+        "latency": {"replay_median_ms": round(replay_ms, 4), "replays": replays,
+                    "session_run_median_ms": round(session_run_ms, 4), "session_runs": len(run_wall) - 1,
+                    "session_run_io_bytes": int(io_bytes),
+                    "session_run_includes": "input H2D copy (pinned ring), graph replay, output D2H copy "
+                                            "(into pinned memory); median after one run that allocates"},
+        "graph": "hipGraph replay" if not args.eager else "eager launches",
+        "nodes_per_step": len(ex.dispatch_order), "kernels_per_step": len(units), "fused_runs": len(runs),
         "roofline": {"kernel": dom["kernel"], "bound": dom["bound"], "achieved": dom["achieved"],
                      "peak": PEAK_FP32_MFMA_TFLOPS if dom["bound"] == "mfma" else PEAK_HBM_GBS,
                      "unit": dom["unit"], "frac": dom["frac"], "traffic": traffic,
                      "mean_launch_us": dom["mean_launch_us"], "launches_per_step": dom["launches"],
                      "work_per_launch": dom["flops_per_launch"] if dom["bound"] == "mfma"
                      else dom["bytes_per_launch"]},
-        "kernels": [{k: r[k] for k in ("kernel", "launches", "ms_per_step", "share", "achieved", "unit", "frac")}
-                    for r in rows],
+        "kernels": [{k: r[k] for k in ("kernel", "launches", "ms_per_step", "share", "achieved", "unit", "frac",
+                                       "mean_launch_us")} for r in rows],
         "parity": parity,
         "cpu_baseline": cpu,
     }
     sess.close()
+    return result
+
+
+# ---------------------------------------------------------------- main
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default=None,
+                    help="measure only this workload (toy, gpt2w, gpt2, 7b4k, qwen3_4b, gpt2_lm, qwen3_4b_lm); "
+                         "default: the 7b4k headline plus every BASELINE config in `configs`")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-parity", action="store_true", help="skip the GPU-vs-oracle output check")
+    ap.add_argument("--eager", action="store_true", help="launch node by node instead of replaying a hipGraph")
+    ap.add_argument("--nodes", action="store_true", help="log every node's device time and roofline fraction")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run the library's copy kernel over MIB MiB, 5 times (reference for HBM counters)")
+    ap.add_argument("--save-graph", metavar="STEM",
+                    help="only export the --config workload and write STEM.json + STEM.weights")
+    ap.add_argument("--graph", metavar="STEM",
+                    help="run a saved graph (STEM.json + STEM.weights) instead of exporting --config")
+    args = ap.parse_args()
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
+    if args.save_graph:
+        from workloads import export_workload
+        _, _, graph = export_workload(args.config or HEADLINE)
+        graph.save(args.save_graph)
+        log(f"[bench] wrote {args.save_graph}.json/.weights ({len(graph.nodes)} nodes, {len(graph.constants)} "
+            f"constants) for workload {args.config or HEADLINE}")
+        return 0
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(the multi-GPU sharding is a design note only; nothing here launches collectives)",
+              file=sys.stderr)
+        return 2
+
+    from workloads import CONFIG_ORDER
+    if args.graph:
+        head = measure(Path(args.graph).name, args, graph_stem=args.graph)
+        others = []
+    else:
+        head_key = args.config or HEADLINE
+        head = measure(head_key, args)
+        others = [] if args.config else [k for k in CONFIG_ORDER if k != head_key]
+    per_shape = []
+    for k in others:
+        per_shape.append(measure(k, args))
+    if per_shape:
+        by_key = {r["workload"]: r for r in per_shape}
+        by_key[head["workload"]] = dict(head, headline=True)
+        per_shape = [by_key[k] for k in CONFIG_ORDER if k in by_key]
+
+    cpu = head["cpu_baseline"]
+    if cpu is not None:
+        cpu = dict(cpu, host=host_facts())
+    result = {
+        "metric": METRIC,
+        "value": head["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "event_ms_per_step": head["event_ms_per_step"],
+        "latency": head["latency"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) input, random-init N(0,0.02) weights)"
+                if not head["workload"].endswith("_lm") else
+                "synthetic (seeded uniform token ids, random-init N(0,0.02) weights)",
+        "config": {"workload": head["workload"], "title": head["title"], "batch": head["batch"],
+                   "seq_len": head["seq_len"], "d_model": head["d_model"], "graph": head["graph"],
+                   "nodes_per_step": head["nodes_per_step"], "kernels_per_step": head["kernels_per_step"],
+                   "fused_runs": head["fused_runs"]},
+        "roofline": head["roofline"],
+        "kernels": head["kernels"],
+        "parity": head["parity"],
+        "cpu_baseline": cpu,
+    }
+    if per_shape:
+        result["configs"] = per_shape
     print(json.dumps(result), flush=True)
     return 0
 

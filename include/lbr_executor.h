@@ -108,6 +108,22 @@ int lbr_memcpy_d2h(void* dst_host, const void* src_device, size_t bytes);
 int lbr_memcpy_d2d(void* dst_device, const void* src_device, size_t bytes);
 int lbr_memset(void* dst_device, int value, size_t bytes);
 
+/* Pinned (page-locked) host memory, which the DMA engines read and write
+ * directly: the destination of choice for lbr_download_async. */
+int lbr_host_alloc(size_t bytes, void** out_ptr);
+int lbr_host_free(void* ptr);
+
+/* Enqueue a host→device copy on the library stream from ordinary host
+ * memory.  The bytes go through a library-owned pinned ring of two 8 MiB
+ * chunks: the host copies one chunk (split over a few threads) while the
+ * previous one is in flight.  When the call returns `src` may be reused;
+ * the device copy completes in stream order (before a later plan launch). */
+int lbr_upload_async(void* dst_device, const void* src_host, size_t bytes);
+
+/* Enqueue a device→host copy on the library stream (asynchronous when
+ * dst_host is pinned memory from lbr_host_alloc); lbr_synchronize waits. */
+int lbr_download_async(void* dst_host, const void* src_device, size_t bytes);
+
 /* Drop-in for execute(OpNode*, int) (csrc/executor.c:458-467): launch every
  * node in order on the library stream and wait for completion.  Returns
  * LBR_ERR_UNSUPPORTED for an op without a kernel (where the reference

@@ -15,7 +15,10 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+#include <condition_variable>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 #define LBR_VERSION "lbr-executor 0.1 gfx950"
@@ -118,6 +121,74 @@ static int exec_workspace(size_t need, void** out) {
 #define LBR_MAX_DEVICES 64
 static __device__ __align__(256) unsigned char scratch[LBR_SCRATCH_BYTES];
 static void* g_scratch_dev[LBR_MAX_DEVICES] = {};
+
+// ------------------------------------------------------------------ host staging
+// Uploads from ordinary (pageable) host memory go through a library-owned
+// pinned ring of two chunks: the host copies chunk k into one half while
+// the DMA engine moves chunk k−1 out of the other, so the input crosses
+// PCIe at pinned-memory speed with the host copy hidden behind it.  The
+// host copy itself is split over a small pool of persistent threads (one
+// thread copies at a fraction of the socket's memory bandwidth).
+#define LBR_RING_CHUNK ((size_t)8 << 20)
+
+class CopyPool {
+   public:
+    explicit CopyPool(unsigned workers) {
+        for (unsigned i = 0; i < workers; ++i) std::thread([this, i] { work(i + 1); }).detach();
+        n_threads_ = workers + 1;
+    }
+    // dst[0, n) = src[0, n), split into n_threads_ slices; returns when all are done
+    void copy(char* dst, const char* src, size_t n) {
+        const size_t per = ((n + n_threads_ - 1) / n_threads_ + 63) & ~(size_t)63;
+        if (n_threads_ == 1 || n < ((size_t)1 << 20)) {
+            memcpy(dst, src, n);
+            return;
+        }
+        {
+            std::lock_guard<std::mutex> lk(m_);
+            dst_ = dst;
+            src_ = src;
+            n_ = n;
+            per_ = per;
+            pending_ = n_threads_ - 1;
+            ++gen_;
+        }
+        cv_.notify_all();
+        memcpy(dst, src, std::min(per, n));
+        std::unique_lock<std::mutex> lk(m_);
+        done_.wait(lk, [this] { return pending_ == 0; });
+    }
+
+   private:
+    void work(unsigned id) {
+        unsigned seen = 0;
+        for (;;) {
+            std::unique_lock<std::mutex> lk(m_);
+            cv_.wait(lk, [&] { return gen_ != seen; });
+            seen = gen_;
+            char* d = dst_;
+            const char* s = src_;
+            const size_t n = n_, per = per_, lo = id * per;
+            lk.unlock();
+            if (lo < n) memcpy(d + lo, s + lo, std::min(per, n - lo));
+            lk.lock();
+            if (--pending_ == 0) done_.notify_one();
+        }
+    }
+    std::mutex m_;
+    std::condition_variable cv_, done_;
+    char* dst_ = nullptr;
+    const char* src_ = nullptr;
+    size_t n_ = 0, per_ = 0;
+    unsigned gen_ = 0, n_threads_ = 1;
+    int pending_ = 0;
+};
+
+static std::mutex g_up_mu;
+static CopyPool* g_copy_pool = nullptr;   // never destroyed: its threads are detached and idle at exit
+static char* g_ring = nullptr;
+static hipEvent_t g_ring_ev[2] = {nullptr, nullptr};
+static bool g_ring_busy[2] = {false, false};
 
 // ------------------------------------------------------------------ dispatch table
 typedef int (*decode_fn)(const OpNode*, Step*);
@@ -350,6 +421,68 @@ int lbr_memcpy_d2h(void* dst, const void* src, size_t bytes) {
     if (!bytes) return LBR_OK;
     HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
     HIP_TRY(hipStreamSynchronize(g_stream));
+    return LBR_OK;
+}
+
+int lbr_host_alloc(size_t bytes, void** out_ptr) {
+    if (!out_ptr) {
+        lbr_set_error("lbr_host_alloc: null out_ptr");
+        return LBR_ERR_INVALID;
+    }
+    int rc = ensure_init();
+    if (rc) return rc;
+    *out_ptr = nullptr;
+    HIP_TRY(hipHostMalloc(out_ptr, bytes ? bytes : 256, hipHostMallocDefault));
+    return LBR_OK;
+}
+
+int lbr_host_free(void* ptr) {
+    if (!ptr) return LBR_OK;
+    HIP_TRY(hipHostFree(ptr));
+    return LBR_OK;
+}
+
+int lbr_upload_async(void* dst, const void* src, size_t bytes) {
+    if (bytes && (!dst || !src)) {
+        lbr_set_error("lbr_upload_async: null pointer");
+        return LBR_ERR_INVALID;
+    }
+    int rc = ensure_init();
+    if (rc) return rc;
+    if (!bytes) return LBR_OK;
+    std::lock_guard<std::mutex> lock(g_up_mu);
+    if (!g_ring) {
+        void* ring = nullptr;
+        HIP_TRY(hipHostMalloc(&ring, 2 * LBR_RING_CHUNK, hipHostMallocDefault));
+        for (hipEvent_t& e : g_ring_ev) HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        const unsigned hw = std::thread::hardware_concurrency();
+        g_copy_pool = new CopyPool(std::min(7u, hw > 1 ? hw - 1 : 0u));
+        g_ring = (char*)ring;
+    }
+    size_t off = 0;
+    for (int k = 0; off < bytes; ++k) {
+        const int slot = k & 1;
+        const size_t n = std::min(LBR_RING_CHUNK, bytes - off);
+        if (g_ring_busy[slot]) HIP_TRY(hipEventSynchronize(g_ring_ev[slot]));   // its last DMA is done
+        char* stage = g_ring + slot * LBR_RING_CHUNK;
+        g_copy_pool->copy(stage, (const char*)src + off, n);
+        HIP_TRY(hipMemcpyAsync((char*)dst + off, stage, n, hipMemcpyHostToDevice, g_stream));
+        HIP_TRY(hipEventRecord(g_ring_ev[slot], g_stream));
+        g_ring_busy[slot] = true;
+        off += n;
+    }
+    return LBR_OK;
+}
+
+int lbr_download_async(void* dst, const void* src, size_t bytes) {
+    if (bytes && (!dst || !src)) {
+        lbr_set_error("lbr_download_async: null pointer");
+        return LBR_ERR_INVALID;
+    }
+    int rc = ensure_init();
+    if (rc) return rc;
+    if (!bytes) return LBR_OK;
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
     return LBR_OK;
 }
 

@@ -79,6 +79,70 @@ class DeviceWeights:
             self.base = 0
 
 
+class _PinnedBlock:
+    """Pinned host memory lent to one returned output array.  numpy keeps this object as the
+    array's base, so the block goes back to its pool when the last view of it is dropped."""
+
+    __slots__ = ("ptr", "nbytes", "pool")
+
+    def __init__(self, pool: "PinnedPool", ptr: int, nbytes: int) -> None:
+        self.ptr, self.nbytes, self.pool = ptr, nbytes, pool
+
+    @property
+    def __array_interface__(self):
+        return {"shape": (self.nbytes,), "typestr": "|u1", "data": (self.ptr, False), "version": 3}
+
+    def __del__(self):
+        try:
+            self.pool.give_back(self.ptr, self.nbytes)
+        except Exception:
+            pass
+
+
+class PinnedPool:
+    """Output buffers in pinned host memory, so device→host copies run at DMA speed straight
+    into the arrays run() returns.  Each array is the caller's own (as the reference's
+    compiled executor returns copies, runtime/executor/compiled.py:94-98); its block is
+    reused only after the caller drops it.  Beyond ``cap_bytes`` of blocks out at once,
+    arrays fall back to ordinary memory."""
+
+    def __init__(self, lib: HipLibrary, cap_bytes: int = 1 << 30) -> None:
+        self._lib = lib
+        self._free: dict[int, list[int]] = {}
+        self._out = 0
+        self._cap = cap_bytes
+        self._closed = False
+
+    def array(self, shape, dtype) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        nbytes = int(np.prod(shape)) * dtype.itemsize
+        free = self._free.get(nbytes)
+        if not nbytes or self._closed or (not free and self._out + nbytes > self._cap):
+            return np.empty(shape, dtype=dtype)
+        ptr = free.pop() if free else self._host_alloc(nbytes)
+        self._out += nbytes
+        return np.asarray(_PinnedBlock(self, ptr, nbytes)).view(dtype).reshape(shape)
+
+    def _host_alloc(self, nbytes: int) -> int:
+        p = ctypes.c_void_p()
+        self._lib.check(self._lib.lbr_host_alloc(nbytes, ctypes.byref(p)), f"pinned host alloc {nbytes} B")
+        return int(p.value)
+
+    def give_back(self, ptr: int, nbytes: int) -> None:
+        self._out -= nbytes
+        if self._closed:
+            self._lib.lbr_host_free(ctypes.c_void_p(ptr))
+        else:
+            self._free.setdefault(nbytes, []).append(ptr)
+
+    def close(self) -> None:
+        for ptrs in self._free.values():
+            for ptr in ptrs:
+                self._lib.lbr_host_free(ctypes.c_void_p(ptr))
+        self._free = {}
+        self._closed = True
+
+
 class CompiledExecutor(Executor):
     """Plan → device OpNode array → hipGraph, replayed per run()."""
 
@@ -101,6 +165,7 @@ class CompiledExecutor(Executor):
         self._owns_weights = weights is None
         self._inputs: dict[str, tuple[int, int]] = {}   # name -> (device ptr, nbytes)
         self._addr: dict[str, int] = {}
+        self._pinned: PinnedPool | None = None
 
     # ------------------------------------------------------------------ compile
     def compile(self, plan: MemoryPlan) -> None:
@@ -165,6 +230,7 @@ class CompiledExecutor(Executor):
                 arr[i].extra[1] = graph.tensors[node.inputs[1]].shape[0]
         self._nodes = arr
         self._order = order
+        self._pinned = PinnedPool(lib)
         handle = ctypes.c_void_p()
         if self._fuse:
             live = self.live_outs()
@@ -220,6 +286,8 @@ class CompiledExecutor(Executor):
 
     # ------------------------------------------------------------------ run
     def _upload_inputs(self, inputs: dict[str, np.ndarray]) -> None:
+        """Enqueue the input copies on the library stream (through its pinned ring); the
+        caller's arrays may change once this returns."""
         graph = self._graph
         for name, (ptr, nb) in self._inputs.items():
             if name not in inputs:
@@ -230,17 +298,27 @@ class CompiledExecutor(Executor):
                 raise ValueError(f"input '{name}' is {arr.dtype}, graph expects {t.dtype}")
             if arr.nbytes != nb:
                 raise ValueError(f"input '{name}' has shape {arr.shape}, graph expects {t.shape}")
-            self._lib.h2d(ptr, arr.ctypes.data, nb)
+            self._lib.check(self._lib.lbr_upload_async(ctypes.c_void_p(ptr), ctypes.c_void_p(arr.ctypes.data), nb),
+                            "upload")
 
-    def _download_outputs(self) -> dict[str, np.ndarray]:
+    def _enqueue_downloads(self) -> dict[str, np.ndarray]:
+        """Arrays for the graph outputs (pinned where possible) with their device→host copies
+        enqueued on the library stream; valid after synchronize()."""
         graph = self._graph
         out = {}
         for name in graph.outputs:
             t = graph.tensors[name]
-            host = np.empty(t.shape, dtype=np.dtype(t.dtype))
+            host = self._pinned.array(t.shape, t.dtype)
             if host.nbytes:
-                self._lib.d2h(host.ctypes.data, self._addr[name], host.nbytes)
+                self._lib.check(self._lib.lbr_download_async(ctypes.c_void_p(host.ctypes.data),
+                                                             ctypes.c_void_p(self._addr[name]), host.nbytes),
+                                "download")
             out[name] = host
+        return out
+
+    def _download_outputs(self) -> dict[str, np.ndarray]:
+        out = self._enqueue_downloads()
+        self.synchronize()
         return out
 
     def run(self, inputs: dict[str, np.ndarray]) -> dict[str, np.ndarray]:
@@ -255,15 +333,19 @@ class CompiledExecutor(Executor):
                             for node, ms in zip(self._order, times)],
                 total_ns=int(sum(times) * 1e6))
         else:
+            # inputs in, one graph replay, outputs out: all in stream order, one wait
             t0 = time.perf_counter_ns()
             self.launch()
+            out = self._enqueue_downloads()
             self.synchronize()
             self._last_profile = RunProfile(total_ns=time.perf_counter_ns() - t0)
+            return out
         return self._download_outputs()
 
     # ------------------------------------------------------------------ device-resident API
     def upload_inputs(self, inputs: dict[str, np.ndarray]) -> None:
         self._upload_inputs(inputs)
+        self.synchronize()
 
     def download_outputs(self) -> dict[str, np.ndarray]:
         return self._download_outputs()
@@ -318,6 +400,9 @@ class CompiledExecutor(Executor):
         for ptr, _ in self._inputs.values():
             lib.free(ptr)
         self._inputs = {}
+        if self._pinned is not None:
+            self._pinned.close()    # blocks still held by returned arrays are freed when those go
+            self._pinned = None
         if self._arena:
             lib.free(self._arena)
             self._arena = 0

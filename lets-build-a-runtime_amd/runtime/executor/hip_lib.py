@@ -59,6 +59,10 @@ class HipLibrary:
             "lbr_memcpy_d2h": ([c_vp, c_vp, c_size], c_int),
             "lbr_memcpy_d2d": ([c_vp, c_vp, c_size], c_int),
             "lbr_memset": ([c_vp, c_int, c_size], c_int),
+            "lbr_host_alloc": ([c_size, P(c_vp)], c_int),
+            "lbr_host_free": ([c_vp], c_int),
+            "lbr_upload_async": ([c_vp, c_vp, c_size], c_int),
+            "lbr_download_async": ([c_vp, c_vp, c_size], c_int),
             "lbr_execute": ([P(COpNode), c_int], c_int),
             "lbr_execute_workspace_bytes": ([P(c_size)], c_int),
             "lbr_execute_noalloc": ([P(COpNode), c_int], c_int),

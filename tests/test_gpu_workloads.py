@@ -195,6 +195,35 @@ def test_graph_replay_matches_eager_and_reruns():
     s_eager.close()
 
 
+def test_session_run_outputs_are_caller_owned():
+    """Session.run returns arrays the caller owns (the reference returns copies,
+    compiled.py:94-98), even though the device writes them straight into pinned host memory:
+    outputs of earlier runs keep their values while later runs execute, and a block is reused
+    once its array is dropped."""
+    import gc
+    from workloads import export_workload, WORKLOADS
+    from runtime.session import Session
+    from oracle.host_exec import OracleRun
+    _, _, graph = export_workload("gpt2w", seq_len=128)
+    s = Session(graph)
+    s.create()
+    orc = OracleRun(s.memory_plan)
+    xs = [WORKLOADS["gpt2w"].input(seed=k, seq_len=128) for k in range(3)]
+    ys = [s.run({graph.inputs[0]: x})[graph.outputs[0]] for x in xs]
+    for x, y in zip(xs, ys):
+        o = orc.run({graph.inputs[0]: x})[graph.outputs[0]]
+        assert normwise_rel(y, o) <= TOL
+    assert len({y.ctypes.data for y in ys}) == 3
+    addr = ys[1].ctypes.data
+    del ys[1]
+    gc.collect()
+    y3 = s.run({graph.inputs[0]: xs[1]})[graph.outputs[0]]
+    assert y3.ctypes.data == addr                  # the dropped block came back
+    np.testing.assert_array_equal(y3, s.run({graph.inputs[0]: xs[1]})[graph.outputs[0]])
+    s.close()
+    assert np.isfinite(y3).all() and np.isfinite(ys[0]).all()   # still readable after close
+
+
 def test_profile_run_reports_every_node():
     from workloads import export_workload
     from runtime.session import Session
