@@ -25,7 +25,9 @@
 //               projections, passes.py merge_parallel_matmuls).
 //   HEAD_PROLOGUE  SLICE last dim → [ADD bias row] → [RMSNORM over hd] →
 //               TRANSPOSE(S,H) → [RoPE: MUL cos, SLICE, SLICE, NEG, CAT,
-//               MUL sin, ADD]: one wavefront per (token, head) row.
+//               MUL sin, ADD]: hd/4 lanes per (token, head) row, one float4
+//               each (a whole wavefront per row when rows are not 16-byte
+//               aligned).
 //   ATTN_TRANSPOSE  ATTENTION → TRANSPOSE(H,S): the attention kernel stores
 //               its rows straight into [B, S, H, hd].
 //   ATTN_SLICED_V  SLICE(C, last dim) → TRANSPOSE(S,H) → ATTENTION taking it
@@ -48,6 +50,8 @@
 #include "lbr_device.h"
 
 #include <math.h>
+#include <stdlib.h>
+#include <string.h>
 #include <vector>
 
 #include "lbr_fusion.h"
@@ -126,10 +130,70 @@ __global__ __launch_bounds__(256) void head_prologue(HeadArgs a) {
     }
 }
 
+// float4 form for 16-byte aligned rows: a row of HD floats is LPR = HD/4
+// lanes holding one float4 each, so a 64-lane wavefront carries 64/LPR rows
+// (2 at HD = 128) and a 256-thread block 256/LPR rows; every load is a
+// 16-byte vector.  The rotate-half partner of a lane's four values sits
+// LPR/2 lanes away in the same row group (d ± HD/2), and the RMSNorm sum
+// reduces over the row's LPR lanes.
+//
+// Grid: x = token (b·S + s), y = group of RPB heads of that token, so the
+// (token, head) coordinates come from the block indices without divisions.
+template <int HD, bool BIAS, bool NORM, bool ROPE>
+__global__ __launch_bounds__(256) void head_prologue4(HeadArgs a) {
+    constexpr int LPR = HD / 4;
+    constexpr int RPB = 256 / LPR;
+    const int l = threadIdx.x % LPR;
+    const int h = blockIdx.y * RPB + threadIdx.x / LPR;
+    if (h >= a.H) return;        // whole row groups leave together: shuffles stay inside live groups
+    const unsigned bs = blockIdx.x;
+    const int s = (int)(bs % (unsigned)a.S), b = (int)(bs / (unsigned)a.S);
+    const int d = 4 * l;
+    const float4 xv = *reinterpret_cast<const float4*>(a.src + (long long)bs * a.ld + a.col0 + (long long)h * HD + d);
+    float4 wv, cv, sv;
+    if (NORM) wv = *reinterpret_cast<const float4*>(a.w + d);
+    if (ROPE) {
+        cv = *reinterpret_cast<const float4*>(a.cos + b * a.cst[0] + h * a.cst[1] + s * a.cst[2] + d);
+        sv = *reinterpret_cast<const float4*>(a.sin + b * a.sst[0] + h * a.sst[1] + s * a.sst[2] + d);
+    }
+    float v[4] = {xv.x, xv.y, xv.z, xv.w};
+    if (BIAS) {
+        const float4 bv = *reinterpret_cast<const float4*>(a.bias + h * HD + d);
+        v[0] = v[0] + bv.x;
+        v[1] = v[1] + bv.y;
+        v[2] = v[2] + bv.z;
+        v[3] = v[3] + bv.w;
+    }
+    if (NORM) {   // norm.c:100-107 order: x · (1/sqrt(Σx²/n + eps)) · w
+        float ss = (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+#pragma unroll
+        for (int off = LPR / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        const float scale = 1.0f / sqrtf(ss / HD + a.eps);
+        v[0] = v[0] * scale * wv.x;
+        v[1] = v[1] * scale * wv.y;
+        v[2] = v[2] * scale * wv.z;
+        v[3] = v[3] * scale * wv.w;
+    }
+    float4* o = reinterpret_cast<float4*>(a.out + (((long long)b * a.H + h) * a.S + s) * HD + d);
+    if (ROPE) {   // y = x·cos + rotate_half(x)·sin, rotate_half = cat(−x[half:], x[:half])
+        const float sign = l < LPR / 2 ? -1.0f : 1.0f;
+        const float c[4] = {cv.x, cv.y, cv.z, cv.w}, sn[4] = {sv.x, sv.y, sv.z, sv.w};
+        float r[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float rot = sign * __shfl_xor(v[k], LPR / 2, 64);
+            r[k] = __fadd_rn(__fmul_rn(v[k], c[k]), __fmul_rn(rot, sn[k]));
+        }
+        *o = make_float4(r[0], r[1], r[2], r[3]);
+    } else {
+        *o = make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
 // Step::in[0]=src [1]=bias [2]=w [3]=cos [4]=sin; i[0]=ld [1]=col0 [2]=B
-// [3]=S [4]=H [5]=hd [6..8]=cos strides [9..11]=sin strides [12]=rows; f[0]=eps
-template <int VPL, bool BIAS, bool NORM, bool ROPE>
-void launch_head_prologue(const Step& s, hipStream_t st) {
+// [3]=S [4]=H [5]=hd [6..8]=cos strides [9..11]=sin strides [12]=rows
+// [13]=float4 kernel; f[0]=eps
+HeadArgs head_args(const Step& s) {
     HeadArgs a;
     a.src = (const float*)s.in[0];
     a.bias = (const float*)s.in[1];
@@ -149,20 +213,41 @@ void launch_head_prologue(const Step& s, hipStream_t st) {
     }
     a.rows = s.i[12];
     a.eps = s.f[0];
+    return a;
+}
+
+template <int VPL, bool BIAS, bool NORM, bool ROPE>
+void launch_head_prologue(const Step& s, hipStream_t st) {
+    const HeadArgs a = head_args(s);
     if (a.rows <= 0) return;
     hipLaunchKernelGGL((head_prologue<VPL, BIAS, NORM, ROPE>), dim3((unsigned)((a.rows + 3) / 4)), dim3(256), 0, st,
                        a);
 }
 
-template <int VPL, bool BIAS>
-step_fn pick_hp2(bool norm, bool rope) {
-    if (norm) return rope ? launch_head_prologue<VPL, BIAS, true, true> : launch_head_prologue<VPL, BIAS, true, false>;
-    return rope ? launch_head_prologue<VPL, BIAS, false, true> : launch_head_prologue<VPL, BIAS, false, false>;
+template <int HD, bool BIAS, bool NORM, bool ROPE>
+void launch_head_prologue4(const Step& s, hipStream_t st) {
+    const HeadArgs a = head_args(s);
+    constexpr int RPB = 256 / (HD / 4);
+    if (a.rows <= 0) return;
+    hipLaunchKernelGGL((head_prologue4<HD, BIAS, NORM, ROPE>), dim3((unsigned)((long long)a.B * a.S),
+                       (unsigned)((a.H + RPB - 1) / RPB)), dim3(256), 0, st, a);
 }
 
-template <int VPL>
+// W = VPL (scalar kernel, 64·VPL = hd) or HD (float4 kernel)
+template <int W, bool BIAS, bool VEC>
+step_fn pick_hp2(bool norm, bool rope) {
+    if constexpr (VEC) {
+        if (norm) return rope ? launch_head_prologue4<W, BIAS, true, true> : launch_head_prologue4<W, BIAS, true, false>;
+        return rope ? launch_head_prologue4<W, BIAS, false, true> : launch_head_prologue4<W, BIAS, false, false>;
+    } else {
+        if (norm) return rope ? launch_head_prologue<W, BIAS, true, true> : launch_head_prologue<W, BIAS, true, false>;
+        return rope ? launch_head_prologue<W, BIAS, false, true> : launch_head_prologue<W, BIAS, false, false>;
+    }
+}
+
+template <int W, bool VEC>
 step_fn pick_hp(bool bias, bool norm, bool rope) {
-    return bias ? pick_hp2<VPL, true>(norm, rope) : pick_hp2<VPL, false>(norm, rope);
+    return bias ? pick_hp2<W, true, VEC>(norm, rope) : pick_hp2<W, false, VEC>(norm, rope);
 }
 
 // ------------------------------------------------------------ matching
@@ -1019,10 +1104,21 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
         s->i[12] = (long long)f.B * f.S * f.Hs[0];
         s->f[0] = f.eps;
         const bool bias = f.sbias[0] != nullptr, norm = f.norm_w != nullptr;
+        // 16-byte rows everywhere (source, output, bias, weight, RoPE rows) → float4 kernel
+        bool vec = (long long)f.B * f.S < (1LL << 31) &&   // one x-block per token
+                   lbr_aligned(f.src, 16) && f.ld % 4 == 0 && f.col_begin[0] % 4 == 0 && lbr_aligned(f.out, 16) &&
+                   (!bias || lbr_aligned(f.sbias[0], 16)) && (!norm || lbr_aligned(f.norm_w, 16));
+        if (f.rope) {
+            vec = vec && lbr_aligned(f.cos, 16) && lbr_aligned(f.sin, 16);
+            for (int k = 0; k < 3; ++k) vec = vec && f.cst[k] % 4 == 0 && f.sst[k] % 4 == 0;
+        }
+        const char* force = getenv("LBR_HEAD_PROLOGUE");   // "scalar" keeps the one-row-per-wave kernel
+        if (force && strcmp(force, "scalar") == 0) vec = false;
+        s->i[13] = vec;
         switch (f.hd / 64) {
-            case 1: s->run = pick_hp<1>(bias, norm, f.rope); break;
-            case 2: s->run = pick_hp<2>(bias, norm, f.rope); break;
-            default: s->run = pick_hp<4>(bias, norm, f.rope); break;
+            case 1: s->run = vec ? pick_hp<64, true>(bias, norm, f.rope) : pick_hp<1, false>(bias, norm, f.rope); break;
+            case 2: s->run = vec ? pick_hp<128, true>(bias, norm, f.rope) : pick_hp<2, false>(bias, norm, f.rope); break;
+            default: s->run = vec ? pick_hp<256, true>(bias, norm, f.rope) : pick_hp<4, false>(bias, norm, f.rope); break;
         }
         s->name = f.rope ? (norm ? "head_norm_rope" : "head_rope") : (norm ? "head_norm" : "head_transpose");
     }

@@ -265,7 +265,8 @@ class CompiledExecutor(Executor):
     def step_params(self) -> list[dict]:
         """Every kernel step of the compiled plan: its kernel, the nodes it covers, and the
         schedule its launch arguments encode (attention: causal fold, key-range split
-        workgroups, deferred output; GEMM: DMA tile index, K ranges)."""
+        workgroups, deferred output; GEMM: DMA tile index, K ranges; head prologue: float4
+        kernel or one wavefront per row)."""
         lib, h = self._lib, self._plan_handle
         first, count, kind = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
         ints = (ctypes.c_longlong * 40)()
@@ -281,6 +282,8 @@ class CompiledExecutor(Executor):
                 d.update(fold=bool(ints[6]), split_wg=int(ints[7]), defer=bool(ints[14]))
             elif d["kernel"].startswith("gemm_"):
                 d.update(ksplit=max(1, int(ints[10])), dma_tile=int(ints[14]) - 1)
+            elif d["kind"] == "head_prologue":
+                d.update(vec=bool(ints[13]))
             out.append(d)
         return out
 
