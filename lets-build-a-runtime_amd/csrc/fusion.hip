@@ -45,7 +45,8 @@
 //   TRANSPOSE_GEMM  TRANSPOSE(H,S) of the attention output [B,H,S,hd] →
 //               MATMUL[_ADD] → [ADD(C, R)]: the GEMM reads its A operand in
 //               the [B,H,S,hd] layout (a 32-wide K step stays inside one head
-//               when hd is a multiple of 32) and adds R in its epilogue —
+//               when hd is a multiple of 32, or covers 32/hd whole heads when hd
+//               divides 32) and adds R in its epilogue —
 //               the O projection and its residual without the transpose.
 #include "lbr_device.h"
 
@@ -627,8 +628,8 @@ bool gemm_step(const OpNode* g, Step* st) {
 
 // TRANSPOSE_GEMM at node i: T = TRANSPOSE(O [B, H, S, hd] → [B, S, H, hd]) is the A
 // operand of the next GEMM (DMA kernel, one batch, hd a multiple of its 32-wide K
-// step): the GEMM reads O directly; a residual ADD right after it is taken into the
-// epilogue as well.
+// step or a divisor of it, so every step starts a head): the GEMM reads O directly; a
+// residual ADD right after it is taken into the epilogue as well.
 bool match_transpose_gemm(const OpNode* nodes, int n, int i, const std::vector<Rng>& live, FusedRun* f) {
     const OpNode* nd = &nodes[i];
     if (!(nd->op == OP_TRANSPOSE && i + 1 < n && is_f32(nd) && nd->n_dims == 4 && nd->n_inputs >= 1 &&
@@ -638,7 +639,7 @@ bool match_transpose_gemm(const OpNode* nodes, int n, int i, const std::vector<R
     const OpNode* mm = &nodes[i + 1];
     Step ms;
     if (!(nd->out_shape[0] == B && nd->out_shape[1] == S && nd->out_shape[2] == H && nd->out_shape[3] == hd &&
-          hd % 32 == 0 && mm->n_inputs >= 2 && mm->inputs[0] == nd->output && is_f32(mm) && gemm_step(mm, &ms) &&
+          (hd % 32 == 0 || (32 % hd == 0 && hd % 4 == 0)) && mm->n_inputs >= 2 && mm->inputs[0] == nd->output && is_f32(mm) && gemm_step(mm, &ms) &&
           ms.i[14] && ms.i[3] == 1 && ms.i[0] == (long long)B * S && ms.i[2] == (long long)H * hd &&
           lbr_aligned(nd->inputs[0], 16)))
         return false;
@@ -679,6 +680,12 @@ bool match_transpose_gemm(const OpNode* nodes, int n, int i, const std::vector<R
 }
 
 }  // namespace
+
+void lbr_input_extent(const OpNode* nd, int k, unsigned long long* lo, unsigned long long* hi) {
+    const Rng r = input_rng(nd, k);
+    *lo = r.lo;
+    *hi = r.hi;
+}
 
 // Find the fusable runs of `nodes` (in order, non-overlapping).
 int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, const size_t* live_bytes, int n_live,

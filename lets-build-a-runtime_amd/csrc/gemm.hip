@@ -451,10 +451,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
         const int row = wave * (TM / NW) + t * RPI + dr;
         const int m = min(m0 + row, M - 1);
         if (AHEADS) {
-            // head layout: row m = (b, s) starts at ((b·aH)·aS + s)·ahd; the K step's head and
-            // offset inside it are the same for every row (soffA below)
+            // head layout: row m = (b, s) starts at ((b·aH)·aS + s)·ahd.  The lane's 4 columns
+            // c = 4·(dp ^ dr) of the 32-wide K step lie in head c / ahd of the step (0 when ahd
+            // is a multiple of 32; 0 or 1 for ahd = 16) at offset c % ahd; the step's first head
+            // goes in the scalar offset (soffA below)
             const int b = m / g.aS, s = m - b * g.aS;
-            offA[t] = (unsigned)(((b * g.aH) * g.aS + s) * g.ahd + ((dp ^ dr) * 4)) * 4u;
+            const int c = (dp ^ dr) * 4;
+            offA[t] = (unsigned)(((b * g.aH) * g.aS + s) * g.ahd + (c / g.ahd) * g.aS * g.ahd + c % g.ahd) * 4u;
         } else {
             offA[t] = (unsigned)(m * K + ((dp ^ dr) * 4)) * 4u;
         }
@@ -480,7 +483,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
         float* la = st + wave * (TM / NW) * DBK;
         float* lb = st + TM * DBK + wave * (TN / NW) * DBK;
         // K step k0 of A: column k0 (row-major), or head k0 / ahd at offset k0 % ahd (head
-        // layout; ahd is a multiple of the step, so a step never straddles two heads)
+        // layout; ahd is a multiple of the step, or divides it so the step starts a head)
         const unsigned soffA =
             AHEADS ? (unsigned)((k0 / g.ahd) * g.aS * g.ahd + k0 % g.ahd) * 4u : (unsigned)k0 * 4u;
 #pragma unroll

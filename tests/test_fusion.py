@@ -59,7 +59,9 @@ EXPECTED = {
     # FFN1 → GELU runs in the GEMM epilogue; the attention output transpose → O-proj → residual
     # ADD is one GEMM reading the [B,H,S,hd] layout (hd = 16 in the toy block: not a multiple of
     # the GEMM's K step, so the toy keeps its transpose)
-    "toy": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1}),
+    # hd = 16: a 32-wide K step of the O projection covers two whole heads
+    "toy": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1,
+                    ("transpose_gemm", 3): 1}),
     "gpt2w": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1, ("transpose_gemm", 3): 1}),
     "7b4k": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1, ("transpose_gemm", 3): 1}),
     # c_attn is MATMUL_ADD (bias already in the GEMM): three (slice, transpose) chains per layer;
@@ -480,8 +482,10 @@ def test_transpose_gemm_refusals():
     assert _windows(_tgemm(0, 1 * MB, 0, 3 * MB)) == [(0, 3, "transpose_gemm")]
     # Y over O: the residual ADD stays a node of its own, the transpose is still absorbed
     assert _windows(_tgemm(0, 1 * MB, 2 * MB, 0)) == [(0, 2, "transpose_gemm")]
-    # head dim not a multiple of the 32-wide K step (a step would straddle two heads)
-    assert _windows(_tgemm(0, 1 * MB, 2 * MB, hd=16)) == []
+    # head dim 2: a lane's 4-float chunk of the K step would straddle two heads; 16
+    # divides the 32-wide step (two whole heads per step)
+    assert _windows(_tgemm(0, 1 * MB, 2 * MB, hd=2)) == []
+    assert _windows(_tgemm(0, 1 * MB, 2 * MB, hd=16)) == [(0, 2, "transpose_gemm")]
     # T read by a later node
     reader = _node(OpType.RELU, [ARENA + 1 * MB], ARENA + 8 * MB, (16,))
     assert all(k != "transpose_gemm" for _, _, k in _windows(_tgemm(0, 1 * MB, 2 * MB, 3 * MB, later=[reader])))

@@ -131,11 +131,13 @@ def test_gemm_gated_epilogue(monkeypatch, tile, act, gbias, order, mm_bias):
 @pytest.mark.parametrize("tile,ks", [(None, None), ("256x256", "1"), ("128x64", "1"), ("64x64", "1"),
                                      ("128x128", "3")])
 @pytest.mark.parametrize("H,S,hd,N,bias,resid", [(4, 300, 64, 200, True, True), (2, 130, 128, 96, False, True),
-                                                  (8, 64, 32, 520, True, False)])
+                                                  (8, 64, 32, 520, True, False), (4, 40, 16, 64, True, True),
+                                                  (12, 70, 8, 100, False, True)])
 def test_transpose_gemm(monkeypatch, tile, ks, H, S, hd, N, bias, resid):
     """O [1, H, S, hd] → TRANSPOSE(1, 2) → [1, S, H·hd] → MATMUL[_ADD] → [ADD(C, R)]: the GEMM reads
     O in its head layout (the transposed copy is never made).  ks=3 splits K into ranges that
-    start inside a head (e.g. k0 = 96 with hd = 64)."""
+    start inside a head (e.g. k0 = 96 with hd = 64); hd = 16 and 8 put 2 and 4 whole heads in
+    one 32-wide K step."""
     if tile:
         monkeypatch.setenv("LBR_GEMM_TILE", tile)
         monkeypatch.setenv("LBR_GEMM_KSPLIT", ks)
