@@ -219,6 +219,10 @@ int lbr_plan_node_kernel(const lbr_plan* plan, int index, char* name_out,
 #define LBR_FUSE_ATTN_SLICED_V  8 /* SLICE(C, last dim) → TRANSPOSE(S,H) → ATTENTION with it as
                                      V → [TRANSPOSE(H,S)]: the attention kernel reads V rows
                                      straight from C's columns (and writes [B, S, H, hd])        */
+#define LBR_FUSE_TINY           9 /* opt-in (LBR_TINY=1): the whole node array as one workgroup
+                                     of 1024 threads, the intermediates held in LDS (outputs
+                                     spanning at most the CU's LDS less the node records, small
+                                     GEMM/attention work, supported ops)                       */
 
 typedef struct {
     int first;   /* index of the run's first node */
@@ -243,6 +247,11 @@ int lbr_plan_create_fused(const OpNode* nodes, int n_nodes, int use_graph,
 int lbr_plan_num_steps(const lbr_plan* plan);
 int lbr_plan_step_info(const lbr_plan* plan, int step, int* first_node,
                        int* n_nodes, int* kind);
+
+/* x / d by the multiply-shift divisor the single-workgroup plan
+ * (LBR_FUSE_TINY) indexes with, computed on the host exactly as the kernel
+ * does (x < 2^31, d >= 1): test support, no counterpart in the reference. */
+unsigned lbr_tiny_fast_div(unsigned x, unsigned d);
 
 /* The decoded integer launch arguments of step `step` (up to `cap` of them,
  * 40 at most), for tests and reports.  Their meaning is the kernel's: for

@@ -267,6 +267,7 @@ struct lbr_plan {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     void* ws = nullptr;          // shared step workspace (split-K partial sums)
+    void* tiny_buf = nullptr;    // device node copy of a single-workgroup plan
 };
 
 static void run_steps(const std::vector<Step>& steps, hipStream_t st) {
@@ -292,16 +293,30 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
         }
     }
     std::vector<FusedRun> runs;
+    bool tiny = false;
     if (fuse) {
-        int rc = lbr_find_fusions(nodes, n_nodes, live_ptr, live_bytes, n_live, &runs);
+        // a graph small enough for one workgroup becomes a single step
+        Step ts;
+        int rc = lbr_tiny_step(nodes, n_nodes, live_ptr, live_bytes, n_live, n_live > 0, &ts, &p->tiny_buf, &tiny);
         if (rc) {
             delete p;
             return rc;
         }
+        if (tiny) {
+            p->node_step.assign((size_t)n_nodes, -1);
+            p->node_step[0] = 0;
+            p->steps.push_back(ts);
+        } else {
+            rc = lbr_find_fusions(nodes, n_nodes, live_ptr, live_bytes, n_live, &runs);
+            if (rc) {
+                delete p;
+                return rc;
+            }
+        }
     }
-    p->node_step.assign((size_t)n_nodes, -1);
+    if (!tiny) p->node_step.assign((size_t)n_nodes, -1);
     size_t r = 0;
-    for (int i = 0; i < n_nodes;) {
+    for (int i = 0; i < n_nodes && !tiny;) {
         p->node_step[i] = (int)p->steps.size();
         if (r < runs.size() && runs[r].first == i) {
             Step s;
@@ -335,6 +350,7 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
             lbr_set_error("lbr_plan_create: graph capture failed: %s", hipGetErrorString(e));
             if (p->graph) (void)hipGraphDestroy(p->graph);
             if (p->ws) (void)hipFree(p->ws);
+            if (p->tiny_buf) (void)hipFree(p->tiny_buf);
             delete p;
             return LBR_ERR_HIP;
         }
@@ -629,8 +645,12 @@ int lbr_fusion_windows(const OpNode* nodes, int n_nodes, const void* const* live
         return LBR_ERR_INVALID;
     }
     std::vector<FusedRun> runs;
-    int rc = lbr_find_fusions(nodes, n_nodes, live_ptr, live_bytes, n_live, &runs);
-    if (rc) return rc;
+    if (lbr_tiny_eligible(nodes, n_nodes, live_ptr, live_bytes, n_live, n_live > 0)) {
+        runs.push_back({0, n_nodes, LBR_FUSE_TINY});
+    } else {
+        int rc = lbr_find_fusions(nodes, n_nodes, live_ptr, live_bytes, n_live, &runs);
+        if (rc) return rc;
+    }
     for (size_t k = 0; k < runs.size() && (int)k < cap; ++k) {
         out[k].first = runs[k].first;
         out[k].count = runs[k].count;
@@ -668,6 +688,7 @@ int lbr_plan_destroy(lbr_plan* p) {
     if (p->exec) (void)hipGraphExecDestroy(p->exec);
     if (p->graph) (void)hipGraphDestroy(p->graph);
     if (p->ws) (void)hipFree(p->ws);
+    if (p->tiny_buf) (void)hipFree(p->tiny_buf);
     delete p;
     return LBR_OK;
 }

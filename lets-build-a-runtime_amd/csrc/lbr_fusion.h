@@ -54,3 +54,17 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
 
 // Launch record of one fused run.
 int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s);
+
+// Byte range [*lo, *hi) input k of node nd reads (per op, from its shape and
+// extras); *hi = UINTPTR_MAX when the node does not fix it.
+void lbr_input_extent(const OpNode* nd, int k, unsigned long long* lo, unsigned long long* hi);
+
+// Whether lbr_tiny_step would take the node array (host only, no device).
+bool lbr_tiny_eligible(const OpNode* nodes, int n, const void* const* live_ptr, const size_t* live_bytes,
+                       int n_live, bool have_live);
+
+// The whole node array as one single-workgroup step (tiny.hip) when it is
+// small enough; *taken says whether it was, *dev_buf is the device memory the
+// step uses (the plan frees it).
+int lbr_tiny_step(const OpNode* nodes, int n, const void* const* live_ptr, const size_t* live_bytes, int n_live,
+                  bool have_live, Step* s, void** dev_buf, bool* taken);

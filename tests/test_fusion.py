@@ -57,9 +57,8 @@ EXPECTED = {
     # merged QKV → three (slice, bias add, transpose) chains in the GEMM epilogue; the O-proj residual
     # add writes over the GEMM's own A input (refused), the FFN2 one fuses
     # FFN1 → GELU runs in the GEMM epilogue; the attention output transpose → O-proj → residual
-    # ADD is one GEMM reading the [B,H,S,hd] layout (hd = 16 in the toy block: not a multiple of
-    # the GEMM's K step, so the toy keeps its transpose)
-    # hd = 16: a 32-wide K step of the O projection covers two whole heads
+    # ADD is one GEMM reading the [B,H,S,hd] layout (hd = 16 in the toy block: a 32-wide K step
+    # of the O projection covers two whole heads)
     "toy": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1,
                     ("transpose_gemm", 3): 1}),
     "gpt2w": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1, ("transpose_gemm", 3): 1}),
@@ -489,3 +488,71 @@ def test_transpose_gemm_refusals():
     # T read by a later node
     reader = _node(OpType.RELU, [ARENA + 1 * MB], ARENA + 8 * MB, (16,))
     assert all(k != "transpose_gemm" for _, _, k in _windows(_tgemm(0, 1 * MB, 2 * MB, 3 * MB, later=[reader])))
+
+
+# ------------------------------------------------------------ single-workgroup plan
+
+@pytest.mark.tiny
+def test_tiny_plan_takes_the_toy_block_at_its_own_size(monkeypatch):
+    """With LBR_TINY=1 (the `tiny` mark), S = 32: every intermediate of the toy
+    block fits one CU's LDS, and the whole array is one window; at S = 128 the
+    outputs span more than the CU's 160 KiB of LDS and the peephole runs come
+    back; LBR_TINY=0 (the default) leaves the peephole runs."""
+    lib = _lib()
+    arr, order, live = _workload_nodes("toy", 32)
+    assert lib.fusion_windows(arr, len(order), live) == [(0, len(order), "tiny")]
+    assert lib.fusion_windows(arr, len(order), []) == [(0, len(order), "tiny")]
+    arr64, order64, live64 = _workload_nodes("toy", 128)
+    assert "tiny" not in {k for _, _, k in lib.fusion_windows(arr64, len(order64), live64)}
+    monkeypatch.setenv("LBR_TINY", "0")
+    assert "tiny" not in {k for _, _, k in lib.fusion_windows(arr, len(order), live)}
+
+
+def _tiny_chain(x_ptr=EXT, mid=ARENA, out=ARENA + 4096, n=256):
+    """RELU(x) → mid, NEG(mid) → out."""
+    return [_node(OpType.RELU, [x_ptr], mid, (n,)), _node(OpType.NEG, [mid], out, (n,))]
+
+
+@pytest.mark.tiny
+def test_tiny_plan_refusals():
+    assert _windows(_tiny_chain()) == [(0, 2, "tiny")]
+    # one node: its own kernel
+    assert _windows(_tiny_chain()[:1]) == []
+    # an input inside the window that no earlier node wrote (an input placed between outputs)
+    assert _windows(_tiny_chain(x_ptr=ARENA + 2048)) == []
+    # a read that straddles the window's edge
+    nodes = _tiny_chain()
+    nodes[1] = _node(OpType.NEG, [ARENA - 512], ARENA + 4096, (256,))
+    assert _windows(nodes) == []
+    # outputs spanning more than the CU's 160 KiB of LDS less the node records
+    assert _windows(_tiny_chain(out=ARENA + 159 * 1024)) == []
+    assert _windows(_tiny_chain(out=ARENA + 158 * 1024)) == [(0, 2, "tiny")]
+    # an op the interpreter does not run (SUM) anywhere in the array
+    nodes = _tiny_chain() + [_node(OpType.SUM, [ARENA + 4096], ARENA + 8192, (1,), (0, 256))]
+    assert "tiny" not in {k for _, _, k in _windows(nodes)}
+    # GEMM work beyond the single-workgroup budget (2·M·N·K > 32 Mi FLOP)
+    big = [_node(OpType.MATMUL, [A_, W_], ARENA, (64, 64), (8192, 1, 1, 0)),
+           _node(OpType.NEG, [ARENA], ARENA + 16384, (64, 64))]
+    assert _windows(big) == []
+    big[0].extra[0] = 4096
+    assert _windows(big) == [(0, 2, "tiny")]
+
+
+def test_tiny_fast_divisor_matches_integer_division():
+    """The single-workgroup kernel divides by a multiply and a shift (x < 2^31):
+    the host computation of the same (m, s) against plain division on every
+    divisor up to 4096 with the dividends at each multiple's edges, on divisors
+    around powers of two, and on random pairs."""
+    f = _lib().lbr_tiny_fast_div
+    r = np.random.default_rng(11)
+    top = (1 << 31) - 1
+    divisors = list(range(1, 4097)) + [(1 << k) + e for k in range(12, 31) for e in (-1, 0, 1)] + [top]
+    for d in divisors:
+        q_hi = top // d
+        xs = {0, 1, d - 1, d, d + 1, top, top - 1, q_hi * d, q_hi * d - 1}
+        xs |= {int(v) for v in r.integers(0, top, 4)}
+        for x in xs:
+            if 0 <= x <= top:
+                assert f(x, d) == x // d, (x, d)
+    for x, d in zip(r.integers(0, top, 20000), r.integers(1, top, 20000)):
+        assert f(int(x), int(d)) == int(x) // int(d)
