@@ -219,6 +219,11 @@ int lbr_plan_node_kernel(const lbr_plan* plan, int index, char* name_out,
 #define LBR_FUSE_ATTN_SLICED_V  8 /* SLICE(C, last dim) → TRANSPOSE(S,H) → ATTENTION with it as
                                      V → [TRANSPOSE(H,S)]: the attention kernel reads V rows
                                      straight from C's columns (and writes [B, S, H, hd])        */
+#define LBR_FUSE_NORM_GEMM     10 /* RMSNORM | LAYERNORM → GEMM: the GEMM reads the norm's input
+                                     and applies the norm on the fly (DMA kernel, one batch,
+                                     no K split, K ≤ 4096); the other GEMM kinds take the same
+                                     prologue when a norm precedes them (their run then starts
+                                     at the norm)                                               */
 #define LBR_FUSE_TINY           9 /* opt-in (LBR_TINY=1): the whole node array as one workgroup
                                      of 1024 threads, the intermediates held in LDS (outputs
                                      spanning at most the CU's LDS less the node records, small

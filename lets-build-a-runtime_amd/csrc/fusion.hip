@@ -351,8 +351,6 @@ Rng input_rng(const OpNode* nd, int k) {
 
 Rng rng(const void* p, long long bytes) { return {(uintptr_t)p, (uintptr_t)p + (uintptr_t)bytes}; }
 
-bool contains(Rng r, const void* p) { return (uintptr_t)p >= r.lo && (uintptr_t)p < r.hi; }
-
 bool is_f32(const OpNode* n) { return n->elem_size == 4; }
 
 // inter minus w.
@@ -679,6 +677,53 @@ bool match_transpose_gemm(const OpNode* nodes, int n, int i, const std::vector<R
     return false;
 }
 
+// Norm prologue: node p is a RMSNORM / LAYERNORM whose output is the A operand
+// of GEMM node p + 1 and nothing else reads — the GEMM can read the norm's
+// input and apply the norm itself (DMA kernel, one batch, no K split, 16-byte
+// aligned x and weights, K = the norm's columns).  `end` is the end of the
+// run the GEMM heads (p + 2 when it is alone): no output inside it may land
+// on the norm's input or weights, which the GEMM reads to the end.
+bool match_norm_prologue(const OpNode* nodes, int n, int p, int end, const std::vector<Rng>& live, FusedRun* f) {
+    if (p + 1 >= n) return false;
+    const OpNode* nm = &nodes[p];
+    const OpNode* g = &nodes[p + 1];
+    const bool rms = nm->op == OP_RMSNORM;
+    if ((nm->op != OP_LAYERNORM && !rms) || !is_f32(nm) || nm->n_inputs < (rms ? 2 : 3)) return false;
+    Step gs;
+    // the DMA kernel's 256×256 tile (i[14] = 1) has no prologue variant
+    if (!gemm_step(g, &gs) || gs.i[14] < 2 || gs.i[3] != 1 || gs.i[10] > 1 || g->inputs[0] != nm->output) return false;
+    const long long cols = node_last_dim(nm);
+    if (cols <= 0 || gs.i[2] != cols || gs.i[0] * cols != node_total(nm)) return false;
+    // Small GEMMs only: there the norm's own launch is most of its cost.  The
+    // prologue's VALU work and γ/β loads slow a large GEMM by more than the norm
+    // kernel costs (measured, GPT-2 S=1024 body 0.412 → 0.453 ms, Qwen3-4B body
+    // 3.22 → 3.43 ms; the toy block 43.9 → 39.9 µs).  LBR_NORM_PROLOGUE=always
+    // takes it at any size, =0 never.
+    const char* mode = getenv("LBR_NORM_PROLOGUE");
+    if (mode && strcmp(mode, "0") == 0) return false;
+    const bool always = mode && strcmp(mode, "always") == 0;
+    if (!always && gs.i[0] * gs.i[1] * gs.i[2] > (1LL << 26)) return false;
+    const void* x = nm->inputs[0];
+    const void* w = nm->inputs[1];
+    const void* b = rms ? nullptr : nm->inputs[2];
+    if (!lbr_aligned(x, 16) || !lbr_aligned(w, 16) || (b && !lbr_aligned(b, 16))) return false;
+    const std::vector<Rng> reads{rng(x, node_total(nm) * 4), rng(w, cols * 4), rng(b, b ? cols * 4 : 0)};
+    for (int j = p + 1; j < end; ++j)
+        if (any_overlap(out_rng(&nodes[j]), reads)) return false;
+    if (!dead_after(nodes, n, p + 2, {out_rng(nm)}, {}, live)) return false;
+    f->norm = rms ? LBR_NORM_RMS : LBR_NORM_LAYER;
+    f->norm_src = x;
+    f->norm_g = w;
+    f->norm_b = b;
+    f->norm_eps = node_extra_float(nm, 0);
+    return true;
+}
+
+bool gemm_first_kind(int kind) {
+    return kind == LBR_FUSE_GEMM_HEADS || kind == LBR_FUSE_GEMM_GATED || kind == LBR_FUSE_GEMM_ACT ||
+           kind == LBR_FUSE_GEMM_RESID;
+}
+
 }  // namespace
 
 void lbr_input_extent(const OpNode* nd, int k, unsigned long long* lo, unsigned long long* hi) {
@@ -976,6 +1021,37 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
         }
         ++i;
     }
+    // Norm prologues: a norm just before a run that starts with its GEMM joins
+    // the run; one before a GEMM no run took becomes a NORM_GEMM pair.
+    std::vector<FusedRun> runs;
+    size_t r = 0;
+    for (int p = 0; p < n; ++p) {
+        while (r < out->size() && (*out)[r].first < p) runs.push_back((*out)[r++]);
+        if (r < out->size() && (*out)[r].first == p) continue;   // p heads a run: the loop above pushes it
+        const bool in_run = !runs.empty() && runs.back().first + runs.back().count > p;
+        if (in_run || (nodes[p].op != OP_LAYERNORM && nodes[p].op != OP_RMSNORM)) continue;
+        FusedRun f;
+        if (r < out->size() && (*out)[r].first == p + 1 && gemm_first_kind((*out)[r].kind)) {
+            f = (*out)[r];
+            if (match_norm_prologue(nodes, n, p, p + 1 + f.count, live, &f)) {
+                f.first = p;
+                f.count += 1;
+                runs.push_back(f);
+                ++r;
+                ++p;   // the run's GEMM
+            }
+        } else if (r >= out->size() || (*out)[r].first > p + 1) {
+            if (match_norm_prologue(nodes, n, p, p + 2, live, &f)) {
+                f.first = p;
+                f.count = 2;
+                f.kind = LBR_FUSE_NORM_GEMM;
+                runs.push_back(f);
+                ++p;
+            }
+        }
+    }
+    while (r < out->size()) runs.push_back((*out)[r++]);
+    *out = runs;
     return LBR_OK;
 }
 
@@ -1043,8 +1119,12 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
         } else {
             s->name = "gemm_dma_f32_nt+tin";
         }
+    } else if (f.kind == LBR_FUSE_NORM_GEMM) {
+        int rc = decode_matmul(&nodes[f.first + 1], s);
+        if (rc) return rc;
+        s->name = "gemm_dma_f32_nt";
     } else if (f.kind == LBR_FUSE_GEMM_ACT || f.kind == LBR_FUSE_GEMM_GATED) {
-        int rc = decode_matmul(&nodes[f.first], s);
+        int rc = decode_matmul(&nodes[f.first + (f.norm ? 1 : 0)], s);
         if (rc) return rc;
         if (!s->i[14] || (f.kind == LBR_FUSE_GEMM_GATED && (s->i[10] > 1 || s->i[3] != 1))) {
             lbr_set_error("fusion: GEMM node %d is not on the DMA path without a K split", f.first);
@@ -1063,7 +1143,7 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
             s->name = "gemm_dma_f32_nt+gated";
         }
     } else if (f.kind == LBR_FUSE_GEMM_RESID || f.kind == LBR_FUSE_GEMM_HEADS) {
-        int rc = decode_matmul(&nodes[f.first], s);
+        int rc = decode_matmul(&nodes[f.first + (f.norm ? 1 : 0)], s);
         if (rc) return rc;
         if (s->i[13] != 1) {
             lbr_set_error("fusion: GEMM node %d is not on the MFMA path", f.first);
@@ -1128,6 +1208,29 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
             default: s->run = vec ? pick_hp<256, true>(bias, norm, f.rope) : pick_hp<4, false>(bias, norm, f.rope); break;
         }
         s->name = f.rope ? (norm ? "head_norm_rope" : "head_rope") : (norm ? "head_norm" : "head_transpose");
+    }
+    if (f.norm) {   // the GEMM reads the norm's input and applies it (see match_norm_prologue)
+        if (!s->i[14] || s->i[3] != 1 || s->i[10] > 1) {
+            lbr_set_error("fusion: GEMM node %d is not on the single-batch DMA path without a K split", f.first + 1);
+            return LBR_ERR_INVALID;
+        }
+        s->in[0] = f.norm_src;
+        s->i[15] = f.norm;
+        s->i[38] = (long long)(uintptr_t)f.norm_g;
+        s->i[39] = (long long)(uintptr_t)f.norm_b;
+        s->f[1] = f.norm_eps;
+        s->run = gemm_dma_norm_launcher((int)s->i[14] - 1, s->i[6] != 0, f.norm);
+        if (!s->run) {
+            lbr_set_error("fusion: GEMM node %d's tile has no norm prologue", f.first + 1);
+            return LBR_ERR_INVALID;
+        }
+        switch (f.kind) {
+            case LBR_FUSE_GEMM_HEADS: s->name = "gemm_dma_f32_nt+norm+heads"; break;
+            case LBR_FUSE_GEMM_RESID: s->name = "gemm_dma_f32_nt+norm+resid"; break;
+            case LBR_FUSE_GEMM_ACT: s->name = "gemm_dma_f32_nt+norm+act"; break;
+            case LBR_FUSE_GEMM_GATED: s->name = "gemm_dma_f32_nt+norm+gated"; break;
+            default: s->name = "gemm_dma_f32_nt+norm"; break;
+        }
     }
     s->node_index = f.first;
     s->n_nodes = f.count;

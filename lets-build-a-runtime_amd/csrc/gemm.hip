@@ -69,6 +69,12 @@ struct GemmArgs {
     // A in head layout (DMA kernel): A is stored [B, aH, aS, ahd] and read as the
     // [B·aS, aH·ahd] matrix its TRANSPOSE(1, 2) would give (aH = 0: A is row-major)
     int aH, aS, ahd;
+    // Norm prologue (DMA kernel, NORM template argument): A is the input of a
+    // RMSNORM / LAYERNORM over its K columns whose output was this GEMM's A;
+    // nw = weight (γ), nb = LayerNorm bias (β), neps = eps
+    const float* nw;
+    const float* nb;
+    float neps;
 };
 
 // Final store of one C element (row m, column n of batch bz) with the fused
@@ -421,7 +427,16 @@ __device__ __forceinline__ void chunk_schedule() {
     __builtin_amdgcn_sched_group_barrier(0x008, NM - NV - ND, 0);
 }
 
-template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS, bool AHEADS>
+// NORM (norm prologue): 0 none; 1 RMSNORM — the A fragments are multiplied by
+// w[k] and Σx² of each row is accumulated from them, the result is scaled by
+// the row's 1/√(Σx²/K + eps) in the epilogue (= GEMM(x·scale·w)); 2
+// LAYERNORM — with c the row's first element, the fragments become (x − c)·γ
+// and Σ(x − c), Σ(x − c)² accumulate per row, u = Σ γ·B and v = Σ β·B per
+// column, and the epilogue forms r·(acc − ((μ − c)·u) + v with r the row's
+// 1/√(var + eps) (= GEMM((x − μ)·r·γ + β)).  The shift keeps the one-pass
+// variance and the subtraction well conditioned when |μ| ≫ σ.  γ (and β) for
+// each K step ride in the stage behind B, loaded by DMA with it.
+template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS, bool AHEADS, int NORM = 0>
 __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) {
     constexpr int NW = WGM * WGN;
     constexpr int CH = DBK / 4;                 // 16-byte chunks per tile row
@@ -430,7 +445,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
     constexpr int IA = TM / NW / RPI, IB = TN / NW / RPI;
     static_assert(IA * NW * RPI == TM && IB * NW * RPI == TN, "tile rows must split evenly over the waves");
     static_assert(CH == 8 && FM * 16 * WGM == TM && FN * 16 * WGN == TN, "tile shape");
-    constexpr int STAGE = (TM + TN) * DBK;
+    constexpr int GOFF = (TM + TN) * DBK;       // γ, then β, of the step (norm prologue)
+    constexpr int STAGE = GOFF + (NORM ? 2 * DBK : 0);
     constexpr int NCC = CH / 4;                 // 16-wide K chunks per step
     __shared__ __attribute__((aligned(1024))) float lds[2 * STAGE];
 
@@ -479,6 +495,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
         (void*)(g.A + bz * g.sA), (short)0, M * K * 4, 0x00020000);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(g.B + bz * g.sB), (short)0, N * K * 4, 0x00020000);
+    __amdgpu_buffer_rsrc_t rg = rb, rbe = rb;
+    if (NORM) {
+        rg = __builtin_amdgcn_make_buffer_rsrc((void*)g.nw, (short)0, K * 4, 0x00020000);
+        if (NORM == 2) rbe = __builtin_amdgcn_make_buffer_rsrc((void*)g.nb, (short)0, K * 4, 0x00020000);
+    }
     auto issue = [&](int k0, float* st) {
         float* la = st + wave * (TM / NW) * DBK;
         float* lb = st + TM * DBK + wave * (TN / NW) * DBK;
@@ -490,6 +511,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
         for (int t = 0; t < IA; ++t) dma16(ra, la + t * RPI * DBK, offA[t], soffA);
 #pragma unroll
         for (int t = 0; t < IB; ++t) dma16(rb, lb + t * RPI * DBK, offB[t], (unsigned)k0 * 4u);
+        if (NORM && wave == 0) {   // the step's 32 γ (lanes 0-7) and β (lanes 8-15), 16 bytes a lane
+            if (lane < 8) dma16(rg, st + GOFF, (unsigned)lane * 16u, (unsigned)k0 * 4u);
+            if (NORM == 2 && lane >= 8 && lane < 16)
+                dma16(rbe, st + GOFF + DBK - 32, (unsigned)(lane - 8) * 16u, (unsigned)k0 * 4u);
+        }
     };
 
     floatx4 acc[FM][FN];
@@ -508,11 +534,42 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
         rdB[cc] = TM * DBK + wn * (TN / WGN) * DBK + o;
     }
     floatx4 fa[2][FM], fb[2][FN];
+    // norm prologue state: per fragment row (lane row fi of block i) the shift
+    // c and Σ over the lane's k, per fragment column (fi of block j) u and v
+    float nc[FM], ns1[FM], ns2[FM], nu[FN], nv[FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) nc[i] = ns1[i] = ns2[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) nu[j] = nv[j] = 0.f;
     auto frags = [&](const float* st, int cc, floatx4* a, floatx4* b) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const floatx4*>(st + rdA[cc] + i * 16 * DBK);
 #pragma unroll
         for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const floatx4*>(st + rdB[cc] + j * 16 * DBK);
+        if (NORM) {   // k = step start + 16·cc + 4·kq + q for every fragment of the lane
+            const floatx4 w = *reinterpret_cast<const floatx4*>(st + GOFF + cc * 16 + (lane >> 4) * 4);
+            if (NORM == 1) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+                    ns2[i] += (a[i][0] * a[i][0] + a[i][1] * a[i][1]) + (a[i][2] * a[i][2] + a[i][3] * a[i][3]);
+                    a[i] = a[i] * w;
+                }
+            } else {
+                const floatx4 be = *reinterpret_cast<const floatx4*>(st + GOFF + DBK + cc * 16 + (lane >> 4) * 4);
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+                    const floatx4 d = a[i] - nc[i];
+                    ns1[i] += (d[0] + d[1]) + (d[2] + d[3]);
+                    ns2[i] += (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]);
+                    a[i] = d * w;
+                }
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    nu[j] += (w[0] * b[j][0] + w[1] * b[j][1]) + (w[2] * b[j][2] + w[3] * b[j][3]);
+                    nv[j] += (be[0] * b[j][0] + be[1] * b[j][1]) + (be[2] * b[j][2] + be[3] * b[j][3]);
+                }
+            }
+        }
     };
     auto mma = [&](const floatx4* a, const floatx4* b) {
 #pragma unroll
@@ -530,6 +587,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
     const int nk = (min(K, kbeg + g.kchunk) - kbeg) / DBK;
     if (nk > 0) {
         issue(kbeg, lds);
+        if (NORM == 2) {   // each fragment row's shift: its first element (arrives with the first DMA)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                nc[i] = g.A[(long long)min(m0 + wm * (TM / WGM) + i * 16 + fi, M - 1) * K];
+        }
         __builtin_amdgcn_s_waitcnt(0x3F70);   // vmcnt(0)
         __syncthreads();
         if (nk > 1) issue(kbeg + DBK, lds + STAGE);
@@ -565,6 +627,49 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
 
     const int rq = (lane >> 4) * 4, cl = lane & 15;
     const int mw = m0 + wm * (TM / WGM), nw = n0 + wn * (TN / WGN);
+    if (NORM) {
+        // whole rows: sum the four kq lanes of each row and column, then take
+        // each accumulator row's factors from the lane that holds that row
+        const float invK = 1.0f / K;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            ns2[i] += __shfl_xor(ns2[i], 16, 64);
+            ns2[i] += __shfl_xor(ns2[i], 32, 64);
+            if (NORM == 2) {
+                ns1[i] += __shfl_xor(ns1[i], 16, 64);
+                ns1[i] += __shfl_xor(ns1[i], 32, 64);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+            if (NORM == 2) {
+                nu[j] += __shfl_xor(nu[j], 16, 64);
+                nu[j] += __shfl_xor(nu[j], 32, 64);
+                nv[j] += __shfl_xor(nv[j], 16, 64);
+                nv[j] += __shfl_xor(nv[j], 32, 64);
+            }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            // per fragment row fi: RMS scale, or LayerNorm r and μ − c
+            float f0, f1 = 0.f;
+            if (NORM == 1) {
+                f0 = 1.0f / sqrtf(ns2[i] * invK + g.neps);
+            } else {
+                const float dm = ns1[i] * invK;
+                const float var = fmaxf(ns2[i] * invK - dm * dm, 0.f);
+                f0 = 1.0f / sqrtf(var + g.neps);
+                f1 = dm;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float sr = __shfl(f0, rq + r, 64);
+                const float dr = NORM == 2 ? __shfl(f1, rq + r, 64) : 0.f;
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j][r] = NORM == 1 ? acc[i][j][r] * sr : sr * (acc[i][j][r] - dr * nu[j]) + nv[j];
+            }
+        }
+    }
     if (g.ksplit > 1) {
         float* __restrict__ Wp = g.W + ((long long)ks * gridDim.z + bz) * (long long)M * N;
 #pragma unroll
@@ -764,6 +869,10 @@ GemmArgs make_args(const Step& s) {
     g.aH = (int)s.i[35];
     g.aS = (int)s.i[36];
     g.ahd = (int)s.i[37];
+    // i[15] = norm prologue (LBR_NORM_*), i[38] / i[39] = its weight / bias, f[1] = eps
+    g.nw = (const float*)(uintptr_t)s.i[38];
+    g.nb = (const float*)(uintptr_t)s.i[39];
+    g.neps = s.f[1];
     return g;
 }
 
@@ -832,7 +941,7 @@ void launch_gemm_t(const Step& s, hipStream_t st) {
     if (g.ksplit > 1) launch_splitk_reduce<HAS_BIAS>(s, g, st);
 }
 
-template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS, bool AHEADS>
+template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS, bool AHEADS, int NORM = 0>
 void launch_gemm_dma(const Step& s, hipStream_t st) {
     GemmArgs g = make_args(s);
     if (g.M <= 0 || g.N <= 0) return;
@@ -840,7 +949,8 @@ void launch_gemm_dma(const Step& s, hipStream_t st) {
     // a gated pair's tile covers TN/2 output columns (TN/2 gate + TN/2 up columns of C)
     g.tiles_n = g.gF ? (g.gF + TN / 2 - 1) / (TN / 2) : (g.N + TN - 1) / TN;
     dim3 grid(g.tiles_m * g.tiles_n, g.ksplit, (unsigned)s.i[3]);
-    hipLaunchKernelGGL((gemm_dma_f32<TM, TN, WGM, WGN, OCC, HAS_BIAS, AHEADS>), grid, dim3(64 * WGM * WGN), 0, st, g);
+    hipLaunchKernelGGL((gemm_dma_f32<TM, TN, WGM, WGN, OCC, HAS_BIAS, AHEADS, NORM>), grid, dim3(64 * WGM * WGN), 0,
+                       st, g);
     if (g.ksplit > 1) launch_splitk_reduce<HAS_BIAS>(s, g, st);
 }
 
@@ -907,14 +1017,16 @@ void choose_dma(long long M, long long N, int K, long long batches, int cus, int
     }
 }
 
-template <bool HAS_BIAS, bool AHEADS = false>
+template <bool HAS_BIAS, bool AHEADS = false, int NORM = 0>
 step_fn dma_launcher(int tile) {
     switch (tile) {
-        case 0: return launch_gemm_dma<256, 256, 4, 2, 1, HAS_BIAS, AHEADS>;
-        case 1: return launch_gemm_dma<128, 128, 2, 2, 2, HAS_BIAS, AHEADS>;
-        case 2: return launch_gemm_dma<128, 64, 2, 2, 3, HAS_BIAS, AHEADS>;
-        case 3: return launch_gemm_dma<64, 128, 2, 2, 3, HAS_BIAS, AHEADS>;
-        default: return launch_gemm_dma<64, 64, 2, 2, 4, HAS_BIAS, AHEADS>;
+        case 0:   // the norm prologue's registers do not fit beside the 256×256 accumulators
+            if constexpr (NORM != 0) return nullptr;
+            else return launch_gemm_dma<256, 256, 4, 2, 1, HAS_BIAS, AHEADS, NORM>;
+        case 1: return launch_gemm_dma<128, 128, 2, 2, 2, HAS_BIAS, AHEADS, NORM>;
+        case 2: return launch_gemm_dma<128, 64, 2, 2, 3, HAS_BIAS, AHEADS, NORM>;
+        case 3: return launch_gemm_dma<64, 128, 2, 2, 3, HAS_BIAS, AHEADS, NORM>;
+        default: return launch_gemm_dma<64, 64, 2, 2, 4, HAS_BIAS, AHEADS, NORM>;
     }
 }
 
@@ -991,6 +1103,14 @@ void zero_k_fill(const Step& s, hipStream_t st) {
 // fusion): `tile` = Step::i[14] − 1 of the decoded GEMM.
 step_fn gemm_dma_heads_launcher(int tile, bool has_bias) {
     return has_bias ? dma_launcher<true, true>(tile) : dma_launcher<false, true>(tile);
+}
+
+// Launcher of the DMA GEMM with a norm prologue (NORM = LBR_NORM_RMS or
+// LBR_NORM_LAYER), `tile` = Step::i[14] − 1 of the decoded GEMM; null for
+// the 256×256 tile, which has no such variant.
+step_fn gemm_dma_norm_launcher(int tile, bool has_bias, int norm) {
+    if (norm == LBR_NORM_RMS) return has_bias ? dma_launcher<true, false, 1>(tile) : dma_launcher<false, false, 1>(tile);
+    return has_bias ? dma_launcher<true, false, 2>(tile) : dma_launcher<false, false, 2>(tile);
 }
 
 // MATMUL extras [K, trans_b, b_is_2d, alpha_bits] (alpha_bits 0 ⇒ 1.0);

@@ -150,6 +150,10 @@ int decode_embedding(const OpNode* n, Step* s);
 int decode_matmul(const OpNode* n, Step* s);
 // DMA GEMM launcher reading A in head layout (fused TRANSPOSE → GEMM); tile = Step::i[14] − 1
 step_fn gemm_dma_heads_launcher(int tile, bool has_bias);
+// Norm prologue of a DMA GEMM (fused RMSNORM / LAYERNORM → GEMM): Step::i[15]
+#define LBR_NORM_RMS 1
+#define LBR_NORM_LAYER 2
+step_fn gemm_dma_norm_launcher(int tile, bool has_bias, int norm);
 int decode_attention(const OpNode* n, Step* s);
 
 // Helpers over the node record (same meaning as csrc/executor.c:30-48).

@@ -45,6 +45,14 @@ struct FusedRun {
     // reads; taken only under the key-range split, whose merge kernel then writes every
     // row (after the split kernel has finished reading)
     bool defer = false;
+    // Norm prologue (any GEMM kind, and NORM_GEMM alone): node `first` is a RMSNORM /
+    // LAYERNORM over the K columns of `norm_src` whose output was the GEMM's A; the
+    // GEMM is node first + 1 and reads norm_src instead (LBR_NORM_*, 0: none)
+    int norm = 0;
+    const void* norm_src = nullptr;
+    const void* norm_g = nullptr;
+    const void* norm_b = nullptr;
+    float norm_eps = 0.f;
 };
 
 // Fusable runs of nodes[0..n) in stream order; live-out ranges are the

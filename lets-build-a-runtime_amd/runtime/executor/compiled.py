@@ -263,10 +263,10 @@ class CompiledExecutor(Executor):
         return runs
 
     def step_params(self) -> list[dict]:
-        """Every kernel step of the compiled plan: its kernel, the nodes it covers, and the
-        schedule its launch arguments encode (attention: causal fold, key-range split
-        workgroups, deferred output; GEMM: DMA tile index, K ranges; head prologue: float4
-        kernel or one wavefront per row)."""
+        """Every kernel step of the compiled plan: its kernel (and full step name, with the
+        fused parts), the nodes it covers, and the schedule its launch arguments encode
+        (attention: causal fold, key-range split workgroups, deferred output; GEMM: DMA tile
+        index, K ranges, norm prologue; head prologue: float4 kernel or one wavefront per row)."""
         lib, h = self._lib, self._plan_handle
         first, count, kind = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
         ints = (ctypes.c_longlong * 40)()
@@ -276,12 +276,12 @@ class CompiledExecutor(Executor):
             lib.check(lib.lbr_plan_step_info(h, st, ctypes.byref(first), ctypes.byref(count), ctypes.byref(kind)),
                       "lbr_plan_step_info")
             lib.check(lib.lbr_plan_step_args(h, st, ints, 40), "lbr_plan_step_args")
-            d = {"kernel": names[first.value].split("+")[0], "first": first.value, "count": count.value,
-                 "kind": FUSE_KINDS.get(kind.value, "?")}
+            d = {"kernel": names[first.value].split("+")[0], "name": names[first.value], "first": first.value,
+                 "count": count.value, "kind": FUSE_KINDS.get(kind.value, "?")}
             if d["kernel"].startswith("attn_fwd_mfma16"):
                 d.update(fold=bool(ints[6]), split_wg=int(ints[7]), defer=bool(ints[14]))
             elif d["kernel"].startswith("gemm_"):
-                d.update(ksplit=max(1, int(ints[10])), dma_tile=int(ints[14]) - 1)
+                d.update(ksplit=max(1, int(ints[10])), dma_tile=int(ints[14]) - 1, norm=int(ints[15]))
             elif d["kind"] == "head_prologue":
                 d.update(vec=bool(ints[13]))
             out.append(d)

@@ -58,8 +58,9 @@ EXPECTED = {
     # add writes over the GEMM's own A input (refused), the FFN2 one fuses
     # FFN1 → GELU runs in the GEMM epilogue; the attention output transpose → O-proj → residual
     # ADD is one GEMM reading the [B,H,S,hd] layout (hd = 16 in the toy block: a 32-wide K step
-    # of the O projection covers two whole heads)
-    "toy": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1,
+    # of the O projection covers two whole heads); both LayerNorms run inside the (small) GEMM
+    # that reads their output (the heads run and the FFN1 run start at the norm)
+    "toy": Counter({("gemm_heads", 11): 1, ("gemm_resid", 2): 1, ("gemm_act", 3): 1,
                     ("transpose_gemm", 3): 1}),
     "gpt2w": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1, ("transpose_gemm", 3): 1}),
     "7b4k": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1, ("transpose_gemm", 3): 1}),
@@ -556,3 +557,34 @@ def test_tiny_fast_divisor_matches_integer_division():
                 assert f(x, d) == x // d, (x, d)
     for x, d in zip(r.integers(0, top, 20000), r.integers(1, top, 20000)):
         assert f(int(x), int(d)) == int(x) // int(d)
+
+
+# ------------------------------------------------------------ norm prologue
+
+def _norm_gemm(rms=False, K=128, M=256, N=384, x=EXT + (5 << 32), ln_off=0, c_off=MB, later=()):
+    """RMSNORM | LAYERNORM(x) → n, MATMUL(n, W) → C, then `later` nodes."""
+    eps = int(np.float32(1e-5).view(np.int32))
+    ins = [x, EXT + (6 << 32)] if rms else [x, EXT + (6 << 32), EXT + (7 << 32)]
+    nm = _node(OpType.RMSNORM if rms else OpType.LAYERNORM, ins, ARENA + ln_off, (M, K), (eps,))
+    mm = _node(OpType.MATMUL, [ARENA + ln_off, W_], ARENA + c_off, (1, M, N), (K, 1, 1, 0))
+    return [nm, mm, *later]
+
+
+def test_norm_prologue_fuses_layer_and_rms_norms():
+    assert _windows(_norm_gemm()) == [(0, 2, "norm_gemm")]
+    assert _windows(_norm_gemm(rms=True)) == [(0, 2, "norm_gemm")]
+    # a GEMM epilogue run takes the norm at its head
+    act = _node(OpType.GELU, [ARENA + MB], ARENA + 2 * MB, (1, 256, 384))
+    assert _windows(_norm_gemm(later=[act])) == [(0, 3, "gemm_act")]
+
+
+def test_norm_prologue_refusals():
+    # the norm's output is read again later
+    reader = _node(OpType.RELU, [ARENA + 64], ARENA + 4 * MB, (16,))
+    assert _windows(_norm_gemm(later=[reader])) == []
+    # the GEMM's output lands on the norm's input, which the GEMM reads to the end
+    assert _windows(_norm_gemm(x=ARENA + 2 * MB, c_off=2 * MB)) == []
+    # misaligned input rows for the DMA loads
+    assert _windows(_norm_gemm(x=EXT + (5 << 32) + 4)) == []
+    # the norm's output is a declared live-out
+    assert _windows(_norm_gemm(), live=[(ARENA, 256 * 128 * 4)]) == []

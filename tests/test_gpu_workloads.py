@@ -89,8 +89,9 @@ def test_workload_parity_full_size(key, seq, kernels):
 ])
 def test_fused_plan_matches_unfused(monkeypatch, key, seq, kinds):
     """Peephole fusion changes launches, not results: the fused plan's outputs equal the
-    one-kernel-per-node plan's up to the RMSNorm sum order (GEMM epilogues and RoPE keep
-    every rounding step), and the expected runs were fused."""
+    one-kernel-per-node plan's bit for bit (GEMM epilogues keep every rounding step), or
+    within 1e-5 where a norm runs inside a GEMM or RoPE's head kernel (other sum orders);
+    and the expected runs were fused."""
     import copy
     from workloads import export_workload
     from runtime.session import Session
@@ -99,6 +100,7 @@ def test_fused_plan_matches_unfused(monkeypatch, key, seq, kinds):
     fused = Session(graph)
     fused.create()
     runs = fused.executor.fused_runs()
+    reassoc = any(p.get("norm") for p in fused.executor.step_params())
     print(key, [(f, c, k) for f, c, k in runs])
     assert kinds <= {k for _, _, k in runs}
     y = fused.run({graph.inputs[0]: x})[graph.outputs[0]]
@@ -111,7 +113,7 @@ def test_fused_plan_matches_unfused(monkeypatch, key, seq, kinds):
     plain.close()
     e = normwise_rel(y, z)
     print(f"{key}: fused-vs-unfused rel {e:.2e} abs {np.abs(y - z).max():.2e}")
-    if "head_prologue" in kinds:
+    if "head_prologue" in kinds or reassoc:
         assert e <= 1e-5
     else:
         np.testing.assert_array_equal(y, z)
