@@ -63,8 +63,12 @@ struct AttnArgs {
     // are cut into sk_wg contiguous equal shares, one per workgroup.
     int sk_wg;                   // workgroups of the split grid (0: no split)
     int sk_maxseg;               // partial slots per (head, query block)
-    long long sk_tiles;          // key tiles of all heads
+    int sk_tiles;                // key tiles of all heads (sk_wg · sk_tiles < 2³¹)
     int sk_head_tiles;           // key tiles of one head
+    // divisions by sk_wg, sk_tiles and sk_head_tiles as multiply-high and
+    // shift (lbr_fdiv): the share and segment arithmetic stays in a few
+    // scalar instructions instead of 64-bit division routines
+    int sk_wg_m, sk_wg_s, sk_tiles_m, sk_tiles_s, sk_ht_m, sk_ht_s;
     float* part;                 // split partials Σ p·V: [bh][query block][sk_maxseg][128 rows][D]
     float* ml;                   // split running max and Σ p, same slots: [..][128 rows][2]
     int sk_defer;                // 1: every block's rows go through the workspace and
@@ -558,13 +562,13 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
 // its partial to slot (head, block, j) for attn_split_merge.
 
 // First tile of workgroup w's share (sk_bound(sk_wg) = sk_tiles).
-__device__ __forceinline__ long long sk_bound(const AttnArgs& g, long long w) {
-    return w * g.sk_tiles / g.sk_wg;
+__device__ __forceinline__ int sk_bound(const AttnArgs& g, int w) {
+    return (int)lbr_fdiv((unsigned)(w * g.sk_tiles), g.sk_wg_m, g.sk_wg_s);
 }
 
 // Workgroup whose share holds tile G.
-__device__ __forceinline__ long long sk_owner(const AttnArgs& g, long long G) {
-    long long w = G * g.sk_wg / g.sk_tiles;
+__device__ __forceinline__ int sk_owner(const AttnArgs& g, int G) {
+    int w = (int)lbr_fdiv((unsigned)(G * g.sk_wg), g.sk_tiles_m, g.sk_tiles_s);
     while (w + 1 < g.sk_wg && sk_bound(g, w + 1) <= G) ++w;
     while (w > 0 && sk_bound(g, w) > G) --w;
     return w;
@@ -597,24 +601,24 @@ template <int DP, bool CAUSAL, bool HAS_MASK>
 __global__ __launch_bounds__(A16_NT, 4) void attn_fwd_mfma16_split(AttnArgs g) {
     __shared__ float Ks[A16_KB][DP + 4];
     __shared__ float Vs[A16_KB][DP + 4];
-    const long long w = blockIdx.x;
-    const long long end = sk_bound(g, w + 1);
-    long long G = sk_bound(g, w);
+    const int w = blockIdx.x;
+    const int end = sk_bound(g, w + 1);
+    int G = sk_bound(g, w);
     while (G < end) {
-        const long long bh = G / g.sk_head_tiles;
-        int t0 = (int)(G - bh * g.sk_head_tiles);
+        const int bh = (int)lbr_fdiv((unsigned)G, g.sk_ht_m, g.sk_ht_s);
+        int t0 = G - bh * g.sk_head_tiles;
         int qb = 0, nt = attn16_tiles(g, 0, CAUSAL);
         while (t0 >= nt) {
             t0 -= nt;
             nt = attn16_tiles(g, ++qb, CAUSAL);
         }
-        const int t1 = (int)min((long long)nt, t0 + (end - G));
+        const int t1 = min(nt, t0 + (end - G));
         // a block cut by a share boundary (or any block, deferred): segment index = this
         // workgroup − the owner of its first tile
         const long long slot = (g.sk_defer || t0 > 0 || t1 < nt)
-                                   ? (bh * g.n_qblocks + qb) * g.sk_maxseg + (w - sk_owner(g, G - t0))
+                                   ? ((long long)bh * g.n_qblocks + qb) * g.sk_maxseg + (w - sk_owner(g, G - t0))
                                    : -1;
-        attn16_qblock<DP, CAUSAL, HAS_MASK, true>(g, (int)bh, qb, t0, t1, slot, Ks, Vs);
+        attn16_qblock<DP, CAUSAL, HAS_MASK, true>(g, bh, qb, t0, t1, slot, Ks, Vs);
         G += t1 - t0;
     }
 }
@@ -634,9 +638,9 @@ __global__ __launch_bounds__(256) void attn_split_merge(AttnArgs g, int causal) 
     const long long bh = blockIdx.y;
     if (row >= g.S) return;
     const int qb = (int)(row / A16_QB);
-    const long long G0 = bh * g.sk_head_tiles + sk_block_start(g, qb, causal != 0);
-    const long long G1 = G0 + attn16_tiles(g, qb, causal != 0);
-    const int nc = (int)(sk_owner(g, G1 - 1) - sk_owner(g, G0)) + 1;
+    const int G0 = (int)bh * g.sk_head_tiles + sk_block_start(g, qb, causal != 0);
+    const int G1 = G0 + attn16_tiles(g, qb, causal != 0);
+    const int nc = sk_owner(g, G1 - 1) - sk_owner(g, G0) + 1;
     if (nc <= 1 && !g.sk_defer) return;
     const long long r0 = (bh * g.n_qblocks + qb) * g.sk_maxseg * A16_QB + (row - (long long)qb * A16_QB);
     float M = -FLT_MAX;
@@ -784,7 +788,10 @@ void launch_attn16(const Step& s, hipStream_t st) {
     g.sk_wg = (int)s.i[7];
     g.sk_maxseg = (int)s.i[8];
     g.sk_head_tiles = (int)s.i[11];
-    g.sk_tiles = s.i[11] * s.i[0];
+    g.sk_tiles = (int)(s.i[11] * s.i[0]);
+    lbr_fast_divisor((unsigned)g.sk_wg, &g.sk_wg_m, &g.sk_wg_s);
+    lbr_fast_divisor((unsigned)g.sk_tiles, &g.sk_tiles_m, &g.sk_tiles_s);
+    lbr_fast_divisor((unsigned)g.sk_head_tiles, &g.sk_ht_m, &g.sk_ht_s);
     if (g.sk_wg > 0) {
         // workspace: partials, then (m, l) pairs
         const long long rows = s.i[0] * g.n_qblocks * (long long)g.sk_maxseg * A16_QB;
@@ -927,6 +934,8 @@ int decode_attention(const OpNode* n, Step* s) {
             const char* split_wg = getenv("LBR_ATTN_SPLIT_WG");   // forces the workgroup count
             if (split_wg) wg = std::max(0, atoi(split_wg));
             wg = std::min(wg, total);   // every share holds at least one tile
+            // the kernels' share arithmetic is 32-bit: wg · total < 2³¹
+            if (wg > 0 && wg * total >= (1LL << 31)) wg = 0;
             if (wg > 0 && !s->i[6]) {
                 const int maxseg = attn16_max_segments(seq, causal != 0, bh, wg);
                 s->i[7] = wg;

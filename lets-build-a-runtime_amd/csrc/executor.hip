@@ -278,6 +278,78 @@ static bool bad_live(const void* const* live_ptr, const size_t* live_bytes, int 
     return n_live < 0 || (n_live > 0 && (!live_ptr || !live_bytes));
 }
 
+// Measured tile choice for small one-batch, unsplit DMA GEMMs (below 2^34
+// flops; larger ones run on the big tiles, which the model ranks well).  Every
+// tile the step's family has runs once to warm up and three times timed; a
+// tile at least 3% faster than the model's choice replaces it.  Every tile
+// sums each output's K terms in the same order, so the choice never changes a
+// result bit.  The ranges the step writes are saved first and restored after,
+// so plan creation leaves memory as it found it.  LBR_GEMM_AUTOTUNE=0, or a
+// tile forced by LBR_GEMM_TILE, keeps the model's choice.
+static int autotune_gemms(std::vector<Step>& steps) {
+    const char* env = getenv("LBR_GEMM_AUTOTUNE");
+    if ((env && atoi(env) == 0) || getenv("LBR_GEMM_TILE")) return LBR_OK;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    void* save = nullptr;
+    size_t save_cap = 0;
+    hipError_t err = hipEventCreate(&e0);
+    if (err == hipSuccess) err = hipEventCreate(&e1);
+    for (size_t i = 0; i < steps.size() && err == hipSuccess; ++i) {
+        Step& s = steps[i];
+        if (!s.name || strncmp(s.name, "gemm_dma_f32", 12) != 0) continue;
+        int cand[16];
+        const int nc = gemm_dma_tune_candidates(s, cand, 16);
+        if (nc < 2 || 2.0 * (double)s.i[0] * (double)s.i[1] * (double)s.i[2] >= 17179869184.0) continue;
+        void* wp[4];
+        size_t wb[4], total = 0;
+        const int nw = gemm_dma_written(s, wp, wb, 4);
+        for (int k = 0; k < nw; ++k) total += wb[k];
+        if (total > save_cap) {
+            if (save) (void)hipFree(save);
+            save = nullptr;
+            save_cap = 0;
+            if ((err = hipMalloc(&save, total)) != hipSuccess) break;
+            save_cap = total;
+        }
+        for (int k = 0, off = 0; k < nw && err == hipSuccess; off += (int)(wb[k] / sizeof(float)), ++k)
+            err = hipMemcpyAsync((float*)save + off, wp[k], wb[k], hipMemcpyDeviceToDevice, g_stream);
+        const int model_tile = (int)s.i[14] - 1;
+        int best = model_tile;
+        float best_ms = 0.f, model_ms = 0.f;
+        for (int c = 0; c < nc && err == hipSuccess; ++c) {
+            Step t = s;
+            if (!gemm_dma_retile(&t, cand[c])) continue;
+            t.run(t, g_stream);   // warm-up
+            err = hipEventRecord(e0, g_stream);
+            for (int r = 0; r < 3 && err == hipSuccess; ++r) t.run(t, g_stream);
+            if (err == hipSuccess) err = hipEventRecord(e1, g_stream);
+            if (err == hipSuccess) err = hipEventSynchronize(e1);
+            if (err == hipSuccess) err = hipGetLastError();
+            float ms = 0.f;
+            if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+            if (err != hipSuccess) break;
+            if (cand[c] == model_tile) model_ms = ms;
+            if (best_ms == 0.f || ms < best_ms) {
+                best_ms = ms;
+                best = cand[c];
+            }
+        }
+        if (err != hipSuccess) break;
+        if (best != model_tile && model_ms > 0.f && best_ms < 0.97f * model_ms) gemm_dma_retile(&s, best);
+        for (int k = 0, off = 0; k < nw && err == hipSuccess; off += (int)(wb[k] / sizeof(float)), ++k)
+            err = hipMemcpyAsync(wp[k], (float*)save + off, wb[k], hipMemcpyDeviceToDevice, g_stream);
+    }
+    if (err == hipSuccess) err = hipStreamSynchronize(g_stream);
+    if (save) (void)hipFree(save);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (err != hipSuccess) {
+        lbr_set_error("lbr_plan_create: GEMM tile timing failed: %s", hipGetErrorString(err));
+        return LBR_ERR_HIP;
+    }
+    return LBR_OK;
+}
+
 // Decode every node (so each is validated exactly as without fusion), then
 // replace the fused runs by their steps; capture a hipGraph if asked.
 static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fuse, const void* const* live_ptr,
@@ -335,7 +407,10 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
         }
     }
     int rc = assign_workspace(p->steps, &p->ws);
+    if (!rc) rc = autotune_gemms(p->steps);
     if (rc) {
+        if (p->ws) (void)hipFree(p->ws);
+        if (p->tiny_buf) (void)hipFree(p->tiny_buf);
         delete p;
         return rc;
     }

@@ -690,8 +690,10 @@ bool match_norm_prologue(const OpNode* nodes, int n, int p, int end, const std::
     const bool rms = nm->op == OP_RMSNORM;
     if ((nm->op != OP_LAYERNORM && !rms) || !is_f32(nm) || nm->n_inputs < (rms ? 2 : 3)) return false;
     Step gs;
-    // the DMA kernel's 256×256 tile (i[14] = 1) has no prologue variant
-    if (!gemm_step(g, &gs) || gs.i[14] < 2 || gs.i[3] != 1 || gs.i[10] > 1 || g->inputs[0] != nm->output) return false;
+    // DMA path only, and a tile with a prologue variant (not the 256×256 tile,
+    // nor the deeper-pipelined ones)
+    if (!gemm_step(g, &gs) || !gs.i[14] || gs.i[3] != 1 || gs.i[10] > 1 || g->inputs[0] != nm->output) return false;
+    if (!gemm_dma_norm_launcher((int)gs.i[14] - 1, gs.i[6] != 0, rms ? LBR_NORM_RMS : LBR_NORM_LAYER)) return false;
     const long long cols = node_last_dim(nm);
     if (cols <= 0 || gs.i[2] != cols || gs.i[0] * cols != node_total(nm)) return false;
     // Small GEMMs only: there the norm's own launch is most of its cost.  The
@@ -796,7 +798,8 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
             }
             // GEMM_GATED: C [rows, 2F] → SLICE(C, last dim) × 2 → GATED_ACT(gate, [bias], up), one
             // slice the column half [0, F) and the other [F, 2F); DMA kernel, one batch, no K split
-            if (gs.i[14] && gs.i[3] == 1 && gs.i[10] <= 1 && gs.i[1] % 2 == 0 && i + 3 < n && is_f32(nd)) {
+            if (gs.i[14] && gemm_dma_tile_pairs((int)gs.i[14] - 1) && gs.i[3] == 1 && gs.i[10] <= 1 &&
+                gs.i[1] % 2 == 0 && i + 3 < n && is_f32(nd)) {
                 const long long rows = gs.i[0];
                 const int N = (int)gs.i[1], F = N / 2;
                 const OpNode* s1 = &nodes[i + 1];
@@ -1126,7 +1129,8 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
     } else if (f.kind == LBR_FUSE_GEMM_ACT || f.kind == LBR_FUSE_GEMM_GATED) {
         int rc = decode_matmul(&nodes[f.first + (f.norm ? 1 : 0)], s);
         if (rc) return rc;
-        if (!s->i[14] || (f.kind == LBR_FUSE_GEMM_GATED && (s->i[10] > 1 || s->i[3] != 1))) {
+        if (!s->i[14] || (f.kind == LBR_FUSE_GEMM_GATED &&
+                          (s->i[10] > 1 || s->i[3] != 1 || !gemm_dma_tile_pairs((int)s->i[14] - 1)))) {
             lbr_set_error("fusion: GEMM node %d is not on the DMA path without a K split", f.first);
             return LBR_ERR_INVALID;
         }

@@ -436,7 +436,17 @@ __device__ __forceinline__ void chunk_schedule() {
 // 1/√(var + eps) (= GEMM((x − μ)·r·γ + β)).  The shift keeps the one-pass
 // variance and the subtraction well conditioned when |μ| ≫ σ.  γ (and β) for
 // each K step ride in the stage behind B, loaded by DMA with it.
-template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS, bool AHEADS, int NORM = 0>
+// s_waitcnt immediate that waits until at most n vector-memory operations of
+// the wave are outstanding (gfx9 encoding: vmcnt bits [3:0] and [15:14]; the
+// other counters at their maximum, as in 0x3F70 = vmcnt(0)).
+constexpr int waitcnt_vm(int n) {
+    return 0x3F70 | (n & 15) | (((n >> 4) & 3) << 14);
+}
+
+// NS: LDS stages of the K pipeline.  Step kt+NS−1 is in flight while step kt
+// is consumed, so a grid that leaves one or two workgroups on a CU (nothing
+// else to hide a load round trip) can take more stages.
+template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS, bool AHEADS, int NORM = 0, int NS = 2>
 __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) {
     constexpr int NW = WGM * WGN;
     constexpr int CH = DBK / 4;                 // 16-byte chunks per tile row
@@ -448,7 +458,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
     constexpr int GOFF = (TM + TN) * DBK;       // γ, then β, of the step (norm prologue)
     constexpr int STAGE = GOFF + (NORM ? 2 * DBK : 0);
     constexpr int NCC = CH / 4;                 // 16-wide K chunks per step
-    __shared__ __attribute__((aligned(1024))) float lds[2 * STAGE];
+    static_assert(NS >= 2, "pipeline stages");
+    // DMA instructions per wave per step: the A and B rows, plus the norm's γ
+    // (and β) in wave 0
+    constexpr int PER_STEP = IA + IB;
+    constexpr int PER_STEP0 = IA + IB + (NORM == 1 ? 1 : NORM == 2 ? 2 : 0);
+    static_assert((NS - 1) * PER_STEP0 <= 63, "vmcnt holds at most 63");
+    __shared__ __attribute__((aligned(1024))) float lds[NS * STAGE];
 
     int tm, tn;
     tile_coords(g, tm, tn);
@@ -586,36 +602,46 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
     const int kbeg = ks * g.kchunk;
     const int nk = (min(K, kbeg + g.kchunk) - kbeg) / DBK;
     if (nk > 0) {
-        issue(kbeg, lds);
-        if (NORM == 2) {   // each fragment row's shift: its first element (arrives with the first DMA)
+        // NS stages: steps 0 .. NS−1 issued up front; at the end of step kt, step
+        // kt+1 must have landed while kt+2 .. kt+NS−1 may still be in flight, then
+        // step kt+NS goes into the stage step kt leaves.  Steps past the last are
+        // re-fetches of the last step into stages no later step reads, so a wave
+        // always has the same number of DMA instructions per step outstanding and
+        // fixed vmcnt thresholds hold (wave 0 issues the norm's γ/β DMAs too).
+        if (NORM == 2) {   // each fragment row's shift, its first element: issued first, so it
+                           // has landed whenever step 0 has (loads complete in order)
 #pragma unroll
             for (int i = 0; i < FM; ++i)
                 nc[i] = g.A[(long long)min(m0 + wm * (TM / WGM) + i * 16 + fi, M - 1) * K];
         }
-        __builtin_amdgcn_s_waitcnt(0x3F70);   // vmcnt(0)
+#pragma unroll
+        for (int st = 0; st < NS; ++st) issue(kbeg + min(st, nk - 1) * DBK, lds + st * STAGE);
+        if (wave == 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 1) * PER_STEP0));   // step 0 landed
+        else __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 1) * PER_STEP));
         __syncthreads();
-        if (nk > 1) issue(kbeg + DBK, lds + STAGE);
         frags(lds, 0, fa[0], fb[0]);
+        int cur = 0;
         for (int kt = 0; kt < nk - 1; ++kt) {
-            const int cur = (kt & 1) * STAGE;
+            const int nxt = cur + STAGE == NS * STAGE ? 0 : cur + STAGE;
 #pragma unroll
             for (int cc = 0; cc < NCC; ++cc) {
                 if (cc + 1 < NCC) {
                     frags(lds + cur, cc + 1, fa[(cc + 1) & 1], fb[(cc + 1) & 1]);
                 } else {
                     __builtin_amdgcn_sched_barrier(0);
-                    __builtin_amdgcn_s_waitcnt(0x3F70);   // step kt+1 landed (this wave's DMA) ...
-                    __syncthreads();                      // ... and every wave's; stage cur fully read
-                    // two steps ahead, clamped to the last step (re-fetched into a stage not read again)
-                    issue(kbeg + min(kt + 2, nk - 1) * DBK, lds + cur);
-                    frags(lds + (STAGE - cur), 0, fa[0], fb[0]);
+                    // step kt+1 landed (this wave's DMA) ...
+                    if (wave == 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * PER_STEP0));
+                    else __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * PER_STEP));
+                    __syncthreads();   // ... and every wave's; stage cur fully read
+                    issue(kbeg + min(kt + NS, nk - 1) * DBK, lds + cur);
+                    frags(lds + nxt, 0, fa[0], fb[0]);
                 }
                 mma(fa[cc & 1], fb[cc & 1]);
                 if (cc + 1 < NCC) chunk_schedule<0, FM + FN, 4 * FM * FN>();
                 else chunk_schedule<IA + IB, FM + FN, 4 * FM * FN>();
             }
+            cur = nxt;
         }
-        const int cur = ((nk - 1) & 1) * STAGE;
 #pragma unroll
         for (int cc = 0; cc < NCC; ++cc) {
             if (cc + 1 < NCC) frags(lds + cur, cc + 1, fa[(cc + 1) & 1], fb[(cc + 1) & 1]);
@@ -941,7 +967,7 @@ void launch_gemm_t(const Step& s, hipStream_t st) {
     if (g.ksplit > 1) launch_splitk_reduce<HAS_BIAS>(s, g, st);
 }
 
-template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS, bool AHEADS, int NORM = 0>
+template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS, bool AHEADS, int NORM = 0, int NS = 2>
 void launch_gemm_dma(const Step& s, hipStream_t st) {
     GemmArgs g = make_args(s);
     if (g.M <= 0 || g.N <= 0) return;
@@ -949,7 +975,7 @@ void launch_gemm_dma(const Step& s, hipStream_t st) {
     // a gated pair's tile covers TN/2 output columns (TN/2 gate + TN/2 up columns of C)
     g.tiles_n = g.gF ? (g.gF + TN / 2 - 1) / (TN / 2) : (g.N + TN - 1) / TN;
     dim3 grid(g.tiles_m * g.tiles_n, g.ksplit, (unsigned)s.i[3]);
-    hipLaunchKernelGGL((gemm_dma_f32<TM, TN, WGM, WGN, OCC, HAS_BIAS, AHEADS, NORM>), grid, dim3(64 * WGM * WGN), 0,
+    hipLaunchKernelGGL((gemm_dma_f32<TM, TN, WGM, WGN, OCC, HAS_BIAS, AHEADS, NORM, NS>), grid, dim3(64 * WGM * WGN), 0,
                        st, g);
     if (g.ksplit > 1) launch_splitk_reduce<HAS_BIAS>(s, g, st);
 }
@@ -960,13 +986,25 @@ struct DmaTile {
     int tm, tn, occ, waves;
     double eff;
     const char* name;
+    bool model;    // chosen by choose_dma's model; the others only by measurement
+                   // (gemm_dma_tune_candidates) or by name (LBR_GEMM_TILE)
+    bool pairs;    // an even number of 16-column blocks per wavefront (gated pairs)
 };
 constexpr DmaTile kDmaTiles[] = {
-    {256, 256, 1, 8, 0.94, "256x256"},   // 8 wavefronts (4×2), 128 KB LDS
-    {128, 128, 2, 4, 0.92, "128x128"},   // 4 wavefronts (2×2), 64 KB LDS
-    {128, 64, 3, 4, 0.9225, "128x64"},   // 4 wavefronts (2×2), 48 KB LDS
-    {64, 128, 3, 4, 0.9225, "64x128"},
-    {64, 64, 4, 4, 0.90, "64x64"},       // 4 wavefronts (2×2) of 32×32, 32 KB LDS
+    {256, 256, 1, 8, 0.94, "256x256", true, true},   // 8 wavefronts (4×2), 128 KB LDS
+    {128, 128, 2, 4, 0.92, "128x128", true, true},   // 4 wavefronts (2×2), 64 KB LDS
+    {128, 64, 3, 4, 0.9225, "128x64", true, true},   // 4 wavefronts (2×2), 48 KB LDS
+    {64, 128, 3, 4, 0.9225, "64x128", true, true},
+    {64, 64, 4, 4, 0.90, "64x64", true, true},       // 4 wavefronts (2×2) of 32×32, 32 KB LDS
+    // Small-grid tiles.  The model cannot rank them against 64×64 (its error on
+    // GPT-2-width GEMMs, ~18%, exceeds their differences, 5–20%): a 32×48 grid
+    // wins where 64×64 leaves a fractional last round (1024×2304×768: 40.6 µs
+    // with 4 stages vs 43.8; 512×2304×768: 24.9 vs 31.0; 512×3072×768: 26.8 vs
+    // 31.3) and loses where it leaves two 2-wavefront workgroups per CU
+    // (1024×768×768: 24.8 vs 20.0), so they are picked by timing.
+    {32, 48, 8, 2, 0.80, "32x48", false, false},     // 2 wavefronts (2×1) of 16×48, 20 KB LDS
+    {32, 48, 5, 2, 0.80, "32x48s4", false, false},   // the same with 4 LDS stages, 40 KB
+    {64, 96, 4, 4, 0.85, "64x96", false, true},      // 4 wavefronts (4×1) of 16×96, 40 KB LDS
 };
 constexpr int kNumDmaTiles = sizeof(kDmaTiles) / sizeof(kDmaTiles[0]);
 
@@ -991,7 +1029,7 @@ void choose_dma(long long M, long long N, int K, long long batches, int cus, int
     if (cus <= 0) cus = 256;
     for (int t = 0; t < kNumDmaTiles; ++t) {
         const DmaTile& d = kDmaTiles[t];
-        if (force_tile && strcmp(force_tile, d.name) != 0) continue;
+        if (force_tile ? strcmp(force_tile, d.name) != 0 : !d.model) continue;
         const long long tiles = ((M + d.tm - 1) / d.tm) * ((N + d.tn - 1) / d.tn) * batches;
         for (int s = 1; s <= 16; ++s) {
             const int chunk = ((K + s - 1) / s + DBK - 1) / DBK * DBK;
@@ -1026,6 +1064,11 @@ step_fn dma_launcher(int tile) {
         case 1: return launch_gemm_dma<128, 128, 2, 2, 2, HAS_BIAS, AHEADS, NORM>;
         case 2: return launch_gemm_dma<128, 64, 2, 2, 3, HAS_BIAS, AHEADS, NORM>;
         case 3: return launch_gemm_dma<64, 128, 2, 2, 3, HAS_BIAS, AHEADS, NORM>;
+        // the 5th argument is the waves per SIMD the registers must allow: the
+        // LDS-bound workgroups per CU × wavefronts per workgroup / 4, rounded up
+        case 5: return launch_gemm_dma<32, 48, 2, 1, 4, HAS_BIAS, AHEADS, NORM>;
+        case 6: return launch_gemm_dma<32, 48, 2, 1, 2, HAS_BIAS, AHEADS, NORM, 4>;
+        case 7: return launch_gemm_dma<64, 96, 4, 1, 3, HAS_BIAS, AHEADS, NORM>;
         default: return launch_gemm_dma<64, 64, 2, 2, 4, HAS_BIAS, AHEADS, NORM>;
     }
 }
@@ -1111,6 +1154,56 @@ step_fn gemm_dma_heads_launcher(int tile, bool has_bias) {
 step_fn gemm_dma_norm_launcher(int tile, bool has_bias, int norm) {
     if (norm == LBR_NORM_RMS) return has_bias ? dma_launcher<true, false, 1>(tile) : dma_launcher<false, false, 1>(tile);
     return has_bias ? dma_launcher<true, false, 2>(tile) : dma_launcher<false, false, 2>(tile);
+}
+
+// Launcher of a decoded or fused DMA GEMM step for another tile: the same
+// family (norm prologue i[15], A in head layout i[35], or plain) and bias;
+// null when the tile has no such variant or cannot hold a gated pair
+// (i[32]: two 16-column blocks per wavefront).
+static step_fn dma_family_launcher(const Step& s, int tile) {
+    if (tile < 0 || tile >= kNumDmaTiles || (s.i[32] && !kDmaTiles[tile].pairs)) return nullptr;
+    const bool bias = s.i[6] != 0;
+    if (s.i[15]) return gemm_dma_norm_launcher(tile, bias, (int)s.i[15]);
+    if (s.i[35]) return gemm_dma_heads_launcher(tile, bias);
+    return bias ? dma_launcher<true>(tile) : dma_launcher<false>(tile);
+}
+
+bool gemm_dma_tile_pairs(int tile) {
+    return tile >= 0 && tile < kNumDmaTiles && kDmaTiles[tile].pairs;
+}
+
+int gemm_dma_tune_candidates(const Step& s, int* tiles, int cap) {
+    int n = 0;
+    if (!s.i[14] || s.i[10] > 1 || s.i[3] != 1) return 0;   // one batch, no K split
+    for (int t = 0; t < kNumDmaTiles && n < cap; ++t)
+        if (dma_family_launcher(s, t)) tiles[n++] = t;
+    return n;
+}
+
+bool gemm_dma_retile(Step* s, int tile) {
+    const step_fn run = dma_family_launcher(*s, tile);
+    if (!run) return false;
+    s->run = run;
+    s->i[14] = tile + 1;
+    return true;
+}
+
+// Byte ranges a one-batch DMA GEMM step writes: the head-split outputs, or C
+// (M × gated F columns, or M × N).
+int gemm_dma_written(const Step& s, void** ptr, size_t* bytes, int cap) {
+    const long long M = s.i[0], N = s.i[1];
+    int n = 0;
+    if (s.i[19] > 0) {
+        for (int k = 0; k < s.i[19] && k < 4 && n < cap; ++k) {
+            ptr[n] = (void*)s.in[4 + k];
+            bytes[n++] = (size_t)(M * s.i[25 + k] * s.i[29]) * sizeof(float);
+        }
+        return n;
+    }
+    if (cap < 1) return 0;
+    ptr[0] = s.out;
+    bytes[0] = (size_t)(M * (s.i[32] ? s.i[32] : N)) * sizeof(float);
+    return 1;
 }
 
 // MATMUL extras [K, trans_b, b_is_2d, alpha_bits] (alpha_bits 0 ⇒ 1.0);

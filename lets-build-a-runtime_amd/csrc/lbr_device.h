@@ -119,6 +119,28 @@ struct Step {
 // Number of compute units of the initialised device (0 before lbr_init).
 int lbr_device_cus();
 
+// x / d as ((x · m) >> 32) >> s for 0 ≤ x < 2³¹ (Granlund and Montgomery,
+// "Division by invariant integers using multiplication", 1994, with 31-bit
+// dividends: for 2^(l−1) < d ≤ 2^l, m = ⌈2^(31+l) / d⌉ < 2³² and s = l − 1).
+// d = 1 is m = 0 (lbr_fdiv passes x through).  The host computes (m, s) once;
+// a kernel divides by a uniform d with one multiply-high and a shift.
+static inline void lbr_fast_divisor(unsigned d, int* m, int* s) {
+    if (d <= 1) {
+        *m = 0;
+        *s = 0;
+        return;
+    }
+    int l = 0;
+    while ((1ULL << l) < d) ++l;
+    const unsigned long long mm = ((1ULL << (31 + l)) + d - 1) / d;
+    *m = (int)(unsigned)mm;
+    *s = l - 1;
+}
+
+__device__ __forceinline__ unsigned lbr_fdiv(unsigned x, int m, int s) {
+    return m == 0 ? x : __umulhi(x, (unsigned)m) >> s;
+}
+
 static inline bool lbr_aligned(const void* p, size_t a) {
     return (reinterpret_cast<uintptr_t>(p) % a) == 0;
 }
@@ -154,6 +176,15 @@ step_fn gemm_dma_heads_launcher(int tile, bool has_bias);
 #define LBR_NORM_RMS 1
 #define LBR_NORM_LAYER 2
 step_fn gemm_dma_norm_launcher(int tile, bool has_bias, int norm);
+
+// Measured tile choice (plan creation): the DMA tiles a one-batch, unsplit
+// GEMM step can run with (its family: plain, norm prologue, head-layout A,
+// gated pair); switch the step to one of them; the byte ranges it writes.
+int gemm_dma_tune_candidates(const Step& s, int* tiles, int cap);
+// Whether a DMA tile (Step::i[14] − 1) holds gated pairs (GEMM_GATED fusion).
+bool gemm_dma_tile_pairs(int tile);
+bool gemm_dma_retile(Step* s, int tile);
+int gemm_dma_written(const Step& s, void** ptr, size_t* bytes, int cap);
 int decode_attention(const OpNode* n, Step* s);
 
 // Helpers over the node record (same meaning as csrc/executor.c:30-48).

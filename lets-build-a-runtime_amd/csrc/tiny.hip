@@ -119,10 +119,6 @@ __device__ __forceinline__ Node read_node(const TyOp* op) {
     return d;
 }
 
-__device__ __forceinline__ unsigned fdiv(unsigned x, int m, int s) {
-    return m == 0 ? x : __umulhi(x, (unsigned)m) >> s;
-}
-
 __device__ __forceinline__ float* opnd(const Node& d, char* lds, int k) {
     return ((d.lds >> k) & 1) ? reinterpret_cast<float*>(lds + d.p[k]) : reinterpret_cast<float*>(d.p[k]);
 }
@@ -199,7 +195,7 @@ __device__ __forceinline__ void t_binary(const TyOp& o, const Node& d, char* lds
         case TY_BIN_ROW: {
             const unsigned N = d.n[0];
             const int m = d.n[1], sh = d.n[2];
-            each<4>(d.total, [&](int i) { return binop_f<B>(a[i], b[i - fdiv(i, m, sh) * N]); }, st);
+            each<4>(d.total, [&](int i) { return binop_f<B>(a[i], b[i - lbr_fdiv(i, m, sh) * N]); }, st);
             break;
         }
         default: {   // TY_BIN_BCAST
@@ -211,7 +207,7 @@ __device__ __forceinline__ void t_binary(const TyOp& o, const Node& d, char* lds
                 for (int d = 3; d >= 0; --d) {
                     if (d >= nd) continue;
                     const int* e = o.n + 1 + 5 * d;   // LDS record
-                    const unsigned q = fdiv(r, rf(e[3]), rf(e[4]));
+                    const unsigned q = lbr_fdiv(r, rf(e[3]), rf(e[4]));
                     const int c = (int)(r - q * (unsigned)rf(e[0]));
                     r = q;
                     ai += c * rf(e[1]);
@@ -232,7 +228,7 @@ __device__ __forceinline__ void t_bias_relu(const TyOp& o, const Node& d, char* 
     const unsigned N = d.n[0];
     const int m = d.n[1], sh = d.n[2];
     each<4>(d.total, [&](int i) {
-        const float v = x[i] + bias[i - fdiv(i, m, sh) * N];
+        const float v = x[i] + bias[i - lbr_fdiv(i, m, sh) * N];
         return v > 0.f ? v : 0.f;
     }, [&](int i, float v) { y[i] = v; });
 }
@@ -248,7 +244,7 @@ __device__ __forceinline__ void t_gated(const TyOp& o, const Node& d, char* lds)
     const unsigned N = d.n[0];
     const int m = d.n[1], sh = d.n[2];
     each<4>(d.total, [&](int i) {
-        const float v = BIAS ? x[i] + bias[i - fdiv(i, m, sh) * N] : x[i];
+        const float v = BIAS ? x[i] + bias[i - lbr_fdiv(i, m, sh) * N] : x[i];
         return (SILU ? lbr_silu(v) : lbr_gelu_tanh(v)) * up[i];
     }, [&](int i, float v) { y[i] = v; });
 }
@@ -353,7 +349,7 @@ __device__ __forceinline__ void row_softmax(const float* x, float* y, int rows, 
     const int j = threadIdx.x & (lpr - 1);
     for (int r = threadIdx.x >> lg; r < rows; r += TY_NT >> lg) {
         const float* xr = x + r * ld;
-        const int q = ATTN ? r - (int)fdiv(r, qm, qs) * cols : 0;
+        const int q = ATTN ? r - (int)lbr_fdiv(r, qm, qs) * cols : 0;
         float v[TY_CPL];
         float m = -INFINITY;
 #pragma unroll
@@ -448,8 +444,8 @@ __device__ __forceinline__ void mm_direct(int Z, int M, int N, int K, const floa
     const bool bvec = BT && ((unsigned long long)B & 15) == 0 && ldb % 4 == 0 && sB % 4 == 0;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     for (int blk = wave; blk < nblk; blk += TY_WAVES) {
-        const int z = (int)fdiv(blk, zm, zs), rem = blk - z * bm * bn;
-        const int mb = (int)fdiv(rem, nm, ns);
+        const int z = (int)lbr_fdiv(blk, zm, zs), rem = blk - z * bm * bn;
+        const int mb = (int)lbr_fdiv(rem, nm, ns);
         const int m0 = mb * 16, n0 = (rem - mb * bn) * 16;
         const float* Ar = A + z * sA + min(m0 + li, M - 1) * lda;
         const float* Bb = B + ((zoff + z) / zdiv) * sB;
@@ -566,9 +562,9 @@ __device__ __forceinline__ void t_gemm(const TyOp& o, const Node& d, char* lds) 
             for (int b = 0; b < TY_BPW; ++b) {
                 const int item = pass + wave + b * TY_WAVES;
                 if (item >= items) continue;   // uniform per wavefront
-                const int split = (int)fdiv(item, sm, ss), blk = item - split * nblk;
-                const int bz = (int)fdiv(blk, zm, zs), rem = blk - bz * bm * bn;
-                const int mb = (int)fdiv(rem, bnm, bns);
+                const int split = (int)lbr_fdiv(item, sm, ss), blk = item - split * nblk;
+                const int bz = (int)lbr_fdiv(blk, zm, zs), rem = blk - bz * bm * bn;
+                const int mb = (int)lbr_fdiv(rem, bnm, bns);
                 const int m0 = mb * 16, n0 = (rem - mb * bn) * 16;
                 const int ma = min(m0 + li, M - 1), nb = min(n0 + li, N - 1);
                 const float* Bz = B + (b2d ? 0 : bz * N * K);
@@ -617,8 +613,8 @@ __device__ __forceinline__ void t_gemm(const TyOp& o, const Node& d, char* lds) 
         for (int b = 0; b < TY_BPW; ++b) {
             const int item = pass + wave + b * TY_WAVES;
             if (item >= items || item >= nblk) continue;   // split 0 writes
-            const int bz = (int)fdiv(item, zm, zs), rem = item - bz * bm * bn;
-            const int mb = (int)fdiv(rem, bnm, bns);
+            const int bz = (int)lbr_fdiv(item, zm, zs), rem = item - bz * bm * bn;
+            const int mb = (int)lbr_fdiv(rem, bnm, bns);
             const int m0 = mb * 16, nn = (rem - mb * bn) * 16 + li;
             if (nn >= N) continue;
             const float bi = has_bias ? bias[nn] : 0.f;
@@ -684,8 +680,8 @@ __device__ __forceinline__ void t_copy(const TyOp& o, const Node& d, char* lds) 
         case TY_SLICE: {   // index arithmetic per element: 2 per thread per round
             const unsigned inner = d.n[0], len = d.n[1], orig = d.n[2], start = d.n[3];
             each<2>(d.total, [&](int i) {
-                const unsigned r = fdiv(i, d.n[4], d.n[5]), x = (unsigned)i - r * inner;
-                const unsigned ob = fdiv(r, d.n[6], d.n[7]), l = r - ob * len;
+                const unsigned r = lbr_fdiv(i, d.n[4], d.n[5]), x = (unsigned)i - r * inner;
+                const unsigned ob = lbr_fdiv(r, d.n[6], d.n[7]), l = r - ob * len;
                 return in[(ob * orig + start + l) * inner + x];
             }, st);
             break;
@@ -694,7 +690,7 @@ __device__ __forceinline__ void t_copy(const TyOp& o, const Node& d, char* lds) 
             const unsigned rows = d.n[0], cols = d.n[1], lw = d.n[2];
             each<2>(d.total, [&](int i) {
                 const unsigned e = (unsigned)i >> lw, x = (unsigned)i & ((1u << lw) - 1);
-                const unsigned c = fdiv(e, d.n[3], d.n[4]), r = e - c * rows;
+                const unsigned c = lbr_fdiv(e, d.n[3], d.n[4]), r = e - c * rows;
                 return in[((r * cols + c) << lw) + x];
             }, st);
             break;
@@ -704,16 +700,16 @@ __device__ __forceinline__ void t_copy(const TyOp& o, const Node& d, char* lds) 
             const int m8 = rf(o.n[8]), s9 = rf(o.n[9]), m10 = rf(o.n[10]), s11 = rf(o.n[11]);
             each<2>(d.total, [&](int i) {
                 unsigned r = (unsigned)i, q;
-                q = fdiv(r, d.n[4], d.n[5]);
+                q = lbr_fdiv(r, d.n[4], d.n[5]);
                 const unsigned x = r - q * inner;
                 r = q;
-                q = fdiv(r, d.n[6], d.n[7]);
+                q = lbr_fdiv(r, d.n[6], d.n[7]);
                 const unsigned a = r - q * A;
                 r = q;
-                q = fdiv(r, m8, s9);
+                q = lbr_fdiv(r, m8, s9);
                 const unsigned m = r - q * mid;
                 r = q;
-                q = fdiv(r, m10, s11);
+                q = lbr_fdiv(r, m10, s11);
                 const unsigned b = r - q * B;
                 return in[(((q * A + a) * mid + m) * B + b) * inner + x];
             }, st);
@@ -730,7 +726,7 @@ __device__ __forceinline__ void t_copy(const TyOp& o, const Node& d, char* lds) 
                 const int* e = o.n + 2 + 4 * k;
                 const unsigned seg = rf(e[0]), off = rf(e[3]);
                 each<2>(outer * (int)seg, [&](int i) { return src[i]; }, [&](int i, unsigned v) {
-                    const unsigned ob = fdiv(i, rf(e[1]), rf(e[2]));
+                    const unsigned ob = lbr_fdiv(i, rf(e[1]), rf(e[2]));
                     out[ob * row + off + ((unsigned)i - ob * seg)] = v;
                 });
             }
@@ -887,23 +883,6 @@ int reads_of(const OpNode* nd) {
     }
 }
 
-// x / d as ((x · m) >> 32) >> s for 0 ≤ x < 2³¹ (Granlund and Montgomery,
-// "Division by invariant integers using multiplication", 1994, with 31-bit
-// dividends: for 2^(l−1) < d ≤ 2^l, m = ⌈2^(31+l) / d⌉ < 2³² and s = l − 1).
-// d = 1 is m = 0 (the kernel passes x through).
-void fast_divisor(unsigned d, int* m, int* s) {
-    if (d <= 1) {
-        *m = 0;
-        *s = 0;
-        return;
-    }
-    int l = 0;
-    while ((1ULL << l) < d) ++l;
-    const unsigned long long mm = ((1ULL << (31 + l)) + d - 1) / d;
-    *m = (int)(unsigned)mm;
-    *s = l - 1;
-}
-
 int log2_of(int x) {
     int l = 0;
     while ((1 << l) < x) ++l;
@@ -963,7 +942,7 @@ bool pack_bcast(const OpNode* nd_, TyOp* o) {
     for (int d = 0; d < cn; ++d) {
         int* e = o->n + 1 + 5 * d;
         e[0] = (int)cs[d], e[1] = (int)ca[d], e[2] = (int)cb[d];
-        fast_divisor((unsigned)cs[d], &e[3], &e[4]);
+        lbr_fast_divisor((unsigned)cs[d], &e[3], &e[4]);
     }
     return true;
 }
@@ -1041,9 +1020,9 @@ bool plan_gemm(const OpNode* nd, const Ctx& c, TyOp* o) {
     o->n[12] = c.stage_off;
     o->n[13] = c.stage_off + (int)((sb ? b_floats(kc) : 0) * 4);
     o->n[14] = o->n[13] + (int)((sa ? a_floats(kc) : 0) * 4);
-    fast_divisor((unsigned)(bm * bn), &o->n[15], &o->n[16]);
-    fast_divisor((unsigned)bn, &o->n[17], &o->n[18]);
-    fast_divisor((unsigned)nblk, &o->n[19], &o->n[20]);
+    lbr_fast_divisor((unsigned)(bm * bn), &o->n[15], &o->n[16]);
+    lbr_fast_divisor((unsigned)bn, &o->n[17], &o->n[18]);
+    lbr_fast_divisor((unsigned)nblk, &o->n[19], &o->n[20]);
     o->f[0] = nd->op == OP_MATMUL_ADD ? 1.0f : (nd->extra[3] ? __builtin_bit_cast(float, nd->extra[3]) : 1.0f);
     set_opnd(o, 0, nd->inputs[0], c);
     set_opnd(o, 1, nd->inputs[1], c);
@@ -1069,11 +1048,11 @@ bool plan_attention(const OpNode* nd, const Ctx& c, TyOp* o) {
     o->n[0] = (int)bh, o->n[1] = S, o->n[2] = hd, o->n[3] = group, o->n[4] = nd->extra[2] != 0;
     o->n[5] = nd->extra[3] != 0, o->n[6] = (int)hg, o->n[7] = ld, o->n[8] = lpr, o->n[9] = log2_of(lpr);
     o->n[10] = cpl, o->n[11] = c.stage_off, o->n[12] = bm, o->n[13] = bn2;
-    fast_divisor((unsigned)S, &o->n[14], &o->n[15]);
-    fast_divisor((unsigned)(bm * bm), &o->n[16], &o->n[17]);
-    fast_divisor((unsigned)bm, &o->n[18], &o->n[19]);
-    fast_divisor((unsigned)(bm * bn2), &o->n[20], &o->n[21]);
-    fast_divisor((unsigned)bn2, &o->n[22], &o->n[23]);
+    lbr_fast_divisor((unsigned)S, &o->n[14], &o->n[15]);
+    lbr_fast_divisor((unsigned)(bm * bm), &o->n[16], &o->n[17]);
+    lbr_fast_divisor((unsigned)bm, &o->n[18], &o->n[19]);
+    lbr_fast_divisor((unsigned)(bm * bn2), &o->n[20], &o->n[21]);
+    lbr_fast_divisor((unsigned)bn2, &o->n[22], &o->n[23]);
     o->f[0] = 1.0f / sqrtf((float)hd);   // attn.c:68/242
     for (int k = 0; k < 3 + (nd->extra[3] != 0); ++k) set_opnd(o, k, nd->inputs[k], c);
     return true;
@@ -1109,7 +1088,7 @@ bool build_op(const OpNode* nd, const Ctx& c, TyOp* o) {
             set_opnd(o, 1, nd->inputs[1], c);
             if (o->kind == TY_BIN_ROW) {
                 o->n[0] = N;
-                fast_divisor((unsigned)N, &o->n[1], &o->n[2]);
+                lbr_fast_divisor((unsigned)N, &o->n[1], &o->n[2]);
             } else if (o->kind == TY_BIN_BCAST) {
                 ok = pack_bcast(nd, o);
             }
@@ -1118,7 +1097,7 @@ bool build_op(const OpNode* nd, const Ctx& c, TyOp* o) {
         case OP_FUSED_BIAS_RELU:
             o->kind = TY_BIAS_RELU;
             o->n[0] = N;
-            fast_divisor((unsigned)N, &o->n[1], &o->n[2]);
+            lbr_fast_divisor((unsigned)N, &o->n[1], &o->n[2]);
             set_opnd(o, 0, nd->inputs[0], c);
             set_opnd(o, 1, nd->inputs[1], c);
             break;
@@ -1127,7 +1106,7 @@ bool build_op(const OpNode* nd, const Ctx& c, TyOp* o) {
             o->kind = TY_GATED;
             o->sub = nd->extra[1] == 0 ? 0 : 1;
             o->n[0] = N;
-            fast_divisor((unsigned)N, &o->n[1], &o->n[2]);
+            lbr_fast_divisor((unsigned)N, &o->n[1], &o->n[2]);
             o->n[3] = hb;
             set_opnd(o, 0, nd->inputs[0], c);
             set_opnd(o, 1, hb ? nd->inputs[2] : nd->inputs[1], c);
@@ -1172,8 +1151,8 @@ bool build_op(const OpNode* nd, const Ctx& c, TyOp* o) {
         if (inner <= 0 || nd->extra[3] <= 0) return false;
         o->kind = TY_SLICE;
         o->n[0] = (int)inner, o->n[1] = nd->extra[3], o->n[2] = nd->extra[1], o->n[3] = nd->extra[2];
-        fast_divisor((unsigned)inner, &o->n[4], &o->n[5]);
-        fast_divisor((unsigned)nd->extra[3], &o->n[6], &o->n[7]);
+        lbr_fast_divisor((unsigned)inner, &o->n[4], &o->n[5]);
+        lbr_fast_divisor((unsigned)nd->extra[3], &o->n[6], &o->n[7]);
         o->total = (int)((long long)nd->extra[0] * nd->extra[3] * inner);
         return true;
     }
@@ -1182,17 +1161,17 @@ bool build_op(const OpNode* nd, const Ctx& c, TyOp* o) {
             if (nd->extra[0] <= 0 || nd->extra[1] <= 0) return false;
             o->kind = TY_TRANS2D;
             o->n[0] = nd->extra[0], o->n[1] = nd->extra[1], o->n[2] = ew == 2 ? 1 : 0;
-            fast_divisor((unsigned)nd->extra[0], &o->n[3], &o->n[4]);
+            lbr_fast_divisor((unsigned)nd->extra[0], &o->n[3], &o->n[4]);
             return true;
         }
         const long long A = nd->extra[1], mid = nd->extra[2], B = nd->extra[3], inner = (long long)nd->extra[4] * ew;
         if (A <= 0 || mid <= 0 || B <= 0 || inner <= 0) return false;
         o->kind = TY_SWAP;
         o->n[0] = (int)A, o->n[1] = (int)mid, o->n[2] = (int)B, o->n[3] = (int)inner;
-        fast_divisor((unsigned)inner, &o->n[4], &o->n[5]);
-        fast_divisor((unsigned)A, &o->n[6], &o->n[7]);
-        fast_divisor((unsigned)mid, &o->n[8], &o->n[9]);
-        fast_divisor((unsigned)B, &o->n[10], &o->n[11]);
+        lbr_fast_divisor((unsigned)inner, &o->n[4], &o->n[5]);
+        lbr_fast_divisor((unsigned)A, &o->n[6], &o->n[7]);
+        lbr_fast_divisor((unsigned)mid, &o->n[8], &o->n[9]);
+        lbr_fast_divisor((unsigned)B, &o->n[10], &o->n[11]);
         return true;
     }
     // CAT
@@ -1208,7 +1187,7 @@ bool build_op(const OpNode* nd, const Ctx& c, TyOp* o) {
     for (int k = 0; k < nin; ++k) {
         int* e = o->n + 2 + 4 * k;
         e[0] = (int)(nd->extra[1 + k] * inner);
-        fast_divisor((unsigned)std::max(1, e[0]), &e[1], &e[2]);
+        lbr_fast_divisor((unsigned)std::max(1, e[0]), &e[1], &e[2]);
         e[3] = (int)off;
         off += e[0];
         set_opnd(o, k, nd->inputs[k], c);
@@ -1422,7 +1401,7 @@ int lbr_tiny_step(const OpNode* nodes, int n, const void* const* live_ptr, const
 
 extern "C" unsigned lbr_tiny_fast_div(unsigned x, unsigned d) {
     int m = 0, sh = 0;
-    fast_divisor(d, &m, &sh);
+    lbr_fast_divisor(d, &m, &sh);
     if (m == 0) return x;
     return (unsigned)(((unsigned long long)x * (unsigned)m) >> 32) >> sh;
 }

@@ -96,7 +96,7 @@ def test_gemm_activation_epilogue(monkeypatch, op, bias, tile, ks, M, N, K):
     _check(g, {"a": a}, ACTS[op](c), "gemm_act")
 
 
-@pytest.mark.parametrize("tile", [None, "256x256", "128x128", "128x64", "64x128", "64x64"])
+@pytest.mark.parametrize("tile", [None, "256x256", "128x128", "128x64", "64x128", "64x64", "64x96"])
 @pytest.mark.parametrize("act,gbias,order,mm_bias", [("silu", False, 0, False), ("gelu", True, 1, True),
                                                       ("silu", True, 0, True), ("gelu", False, 1, False)])
 def test_gemm_gated_epilogue(monkeypatch, tile, act, gbias, order, mm_bias):
@@ -129,6 +129,7 @@ def test_gemm_gated_epilogue(monkeypatch, tile, act, gbias, order, mm_bias):
 
 
 @pytest.mark.parametrize("tile,ks", [(None, None), ("256x256", "1"), ("128x64", "1"), ("64x64", "1"),
+                                     ("32x48", "1"), ("32x48s4", "1"), ("64x96", "1"),
                                      ("128x128", "3")])
 @pytest.mark.parametrize("H,S,hd,N,bias,resid", [(4, 300, 64, 200, True, True), (2, 130, 128, 96, False, True),
                                                   (8, 64, 32, 520, True, False), (4, 40, 16, 64, True, True),

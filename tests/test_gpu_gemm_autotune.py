@@ -1,0 +1,104 @@
+"""Measured GEMM tile choice at plan creation (LBR_GEMM_AUTOTUNE, on by
+default): small one-batch, unsplit DMA GEMMs are timed over every tile their
+launcher family has, and the fastest replaces the model's choice.
+
+Every DMA tile sums each output's K terms in the same order (K steps in
+order, the same 4-wide MFMA reduction inside a step), so a tuned plan and
+the model's plan give bit-identical outputs; plan creation restores the
+ranges the timed launches wrote, so memory is as the caller left it.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import normwise_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _gemm_node(M, N, K, a, b, bias, c):
+    from runtime.executor.common import COpNode
+    from runtime.ir import OpType
+    node = (COpNode * 1)()
+    node[0].op = OpType.MATMUL_ADD.value
+    node[0].n_inputs = 3
+    node[0].inputs[0] = a
+    node[0].inputs[1] = b
+    node[0].inputs[2] = bias
+    node[0].output = c
+    node[0].n_dims = 3
+    node[0].out_shape[0] = 1
+    node[0].out_shape[1] = M
+    node[0].out_shape[2] = N
+    node[0].elem_size = 4
+    node[0].extra[0] = K
+    node[0].extra[1] = 1   # trans_b
+    node[0].extra[2] = 1   # b_is_2d
+    return node
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 2304, 768), (1024, 2304, 768), (512, 3072, 768), (1024, 768, 768)])
+def test_autotune_restores_memory_and_matches_model(hip_lib, monkeypatch, M, N, K):
+    lib = hip_lib
+    r = np.random.default_rng(M + N + K)
+    a_h = r.standard_normal((M, K)).astype(np.float32)
+    b_h = (0.05 * r.standard_normal((N, K))).astype(np.float32)
+    bias_h = r.standard_normal(N).astype(np.float32)
+    a, b, bias, c = (lib.alloc(x) for x in (a_h.nbytes, b_h.nbytes, bias_h.nbytes, M * N * 4))
+    try:
+        for dev, host in ((a, a_h), (b, b_h), (bias, bias_h)):
+            lib.h2d(dev, host.ctypes.data, host.nbytes)
+        node = _gemm_node(M, N, K, a, b, bias, c)
+        outs = {}
+        for tune in ("1", "0"):
+            monkeypatch.setenv("LBR_GEMM_AUTOTUNE", tune)
+            lib.check(lib.lbr_memset(ctypes.c_void_p(c), 0x7f, M * N * 4), "lbr_memset")
+            plan = ctypes.c_void_p()
+            lib.check(lib.lbr_plan_create(node, 1, 1, ctypes.byref(plan)), "lbr_plan_create")
+            try:
+                host = np.empty(M * N, dtype=np.uint8)
+                lib.d2h(host.ctypes.data, c, host.nbytes)
+                assert (host == 0x7f).all(), "plan creation left the output changed"
+                lib.check(lib.lbr_plan_launch(plan), "lbr_plan_launch")
+                lib.check(lib.lbr_synchronize(), "lbr_synchronize")
+                y = np.empty((M, N), dtype=np.float32)
+                lib.d2h(y.ctypes.data, c, y.nbytes)
+                outs[tune] = y
+            finally:
+                lib.check(lib.lbr_plan_destroy(plan), "lbr_plan_destroy")
+    finally:
+        for p in (a, b, bias, c):
+            lib.free(p)
+    ref = a_h.astype(np.float64) @ b_h.T.astype(np.float64) + bias_h
+    print(f"{M}x{N}x{K}: tuned == model bitwise {np.array_equal(outs['1'], outs['0'])}, "
+          f"vs float64 {normwise_rel(outs['1'], ref):.2e}")
+    np.testing.assert_array_equal(outs["1"], outs["0"])
+    assert normwise_rel(outs["1"], ref) <= 1e-5
+
+
+@pytest.mark.parametrize("key,seq", [("gpt2w", 512), ("gpt2", 256), ("toy", 32)])
+def test_autotune_workload_bitwise(monkeypatch, key, seq):
+    """Whole fused bodies (head scatter, activation, residual, norm prologue
+    epilogues): the tuned plan's output equals the model plan's bit for bit."""
+    from runtime.executor.compiled import CompiledExecutor
+    from runtime.passes import run_pipeline
+    from runtime.planner import plan
+    from workloads import export_workload
+    _, x, graph = export_workload(key, seq_len=seq)
+    run_pipeline(graph, None)
+    mp = plan(graph)
+    name_in, name_out = graph.inputs[0], graph.outputs[0]
+    outs, tiles = {}, {}
+    for tune in ("1", "0"):
+        monkeypatch.setenv("LBR_GEMM_AUTOTUNE", tune)
+        ex = CompiledExecutor()
+        ex.compile(mp)
+        try:
+            tiles[tune] = [p["dma_tile"] for p in ex.step_params() if p["kernel"].startswith("gemm_dma")]
+            outs[tune] = ex.run({name_in: x})[name_out]
+        finally:
+            ex.close()
+    print(f"{key} S={seq}: DMA tiles tuned {tiles['1']} model {tiles['0']}")
+    np.testing.assert_array_equal(outs["1"], outs["0"])
