@@ -224,6 +224,11 @@ int lbr_plan_node_kernel(const lbr_plan* plan, int index, char* name_out,
                                      no K split, K ≤ 4096); the other GEMM kinds take the same
                                      prologue when a norm precedes them (their run then starts
                                      at the norm)                                               */
+#define LBR_FUSE_MLP           11 /* [RMSNORM | LAYERNORM →] MATMUL[_ADD] → RELU | GELU | SILU →
+                                     MATMUL[_ADD] [→ ADD(y, R)], small: one kernel per 16 rows
+                                     with the hidden activations in LDS (D ≤ 1024, D, H and
+                                     the output width multiples of 16, (D + H + 8)·64 B ≤ 64
+                                     KiB, 2·M·(H·D + D2·H) ≤ 2^25 flops)                        */
 #define LBR_FUSE_TINY           9 /* opt-in (LBR_TINY=1): the whole node array as one workgroup
                                      of 1024 threads, the intermediates held in LDS (outputs
                                      spanning at most the CU's LDS less the node records, small

@@ -721,6 +721,102 @@ bool match_norm_prologue(const OpNode* nodes, int n, int p, int end, const std::
     return true;
 }
 
+int act_code(const OpNode* ac) {
+    return ac->op == OP_RELU ? LBR_ACT_RELU : ac->op == OP_GELU ? LBR_ACT_GELU : ac->op == OP_SILU ? LBR_ACT_SILU
+                                                                                                 : LBR_ACT_NONE;
+}
+
+// MLP at node i: GEMM1 → activation → GEMM2 [→ ADD(y, R)], one batch, B [N, K],
+// small enough for mlp_rows (the hidden rows of 16 tokens in LDS, at most 2^25
+// flops: a launch-bound chain).  A RMSNORM / LAYERNORM at node i−1 (`free`:
+// no earlier run took it) whose output is only GEMM1's A joins the run: the
+// kernel then reads the norm's input x and normalises its rows itself.  The
+// kernel writes only y and reads x (or GEMM1's A), the weights, the biases
+// and R: x and R may coincide with y row for row (each workgroup reads its
+// rows before it writes them), nothing it reads may overlap y otherwise; the
+// norm's output, GEMM1's, the activation's and (with the ADD) GEMM2's must be
+// dead after the run.  LBR_MLP_FUSE=0 disables.
+bool match_mlp(const OpNode* nodes, int n, int i, bool free, const std::vector<Rng>& live, FusedRun* f) {
+    if (i + 2 >= n) return false;
+    const char* mode = getenv("LBR_MLP_FUSE");
+    if (mode && strcmp(mode, "0") == 0) return false;
+    const OpNode* g1 = &nodes[i];
+    const OpNode* ac = &nodes[i + 1];
+    const OpNode* g2 = &nodes[i + 2];
+    const int act = act_code(ac);
+    if (act == LBR_ACT_NONE || ac->n_inputs < 1 || ac->inputs[0] != g1->output || !is_f32(ac) || !is_f32(g1) ||
+        !is_f32(g2) || node_total(ac) != node_total(g1) || g2->n_inputs < 2 || g2->inputs[0] != ac->output)
+        return false;
+    Step s1, s2;
+    if (!gemm_step(g1, &s1) || !gemm_step(g2, &s2)) return false;
+    const long long M = s1.i[0], D = s1.i[2], H = s1.i[1], D2 = s2.i[1];
+    if (s1.i[3] != 1 || s2.i[3] != 1 || !s1.i[4] || !s2.i[4] || s2.i[0] != M || s2.i[2] != H) return false;
+    if (!mlp_shape_ok(M, D, H, D2) || 2.0 * (double)M * (double)(H * D + D2 * H) > 33554432.0) return false;
+    const OpNode* ad = nullptr;
+    const void* R = nullptr;
+    if (i + 3 < n) {
+        const OpNode* a = &nodes[i + 3];
+        if (a->op == OP_ADD && a->n_inputs >= 2 && a->extra[0] == 1 && is_f32(a) && node_total(a) == node_total(g2) &&
+            (a->inputs[0] == g2->output) != (a->inputs[1] == g2->output)) {
+            ad = a;
+            R = a->inputs[0] == g2->output ? a->inputs[1] : a->inputs[0];
+        }
+    }
+    const int count = ad ? 4 : 3;
+    const void* y = ad ? ad->output : g2->output;
+    const Rng y_r = rng(y, M * D2 * 4);
+    const void* b1 = g1->op == OP_MATMUL_ADD ? g1->inputs[2] : nullptr;
+    const void* b2 = g2->op == OP_MATMUL_ADD ? g2->inputs[2] : nullptr;
+    const void* ptrs[] = {g1->inputs[1], b1, g2->inputs[1], b2, R, y};
+    for (const void* q : ptrs)
+        if (q && !lbr_aligned(q, 16)) return false;
+    const std::vector<Rng> consts{rng(g1->inputs[1], H * D * 4), rng(b1, b1 ? H * 4 : 0),
+                                  rng(g2->inputs[1], D2 * H * 4), rng(b2, b2 ? D2 * 4 : 0)};
+    if (any_overlap(y_r, consts)) return false;
+    if (R && overlap(y_r, rng(R, M * D2 * 4)) && y != R) return false;
+    // what the kernel reads as its rows: x (rows read, then overwritten only row for row)
+    auto rows_ok = [&](const void* x) {
+        return lbr_aligned(x, 16) && (!overlap(y_r, rng(x, M * D * 4)) || (y == x && D2 == D));
+    };
+    std::vector<Rng> inter{out_rng(g1), out_rng(ac)};
+    if (ad) inter.push_back(out_rng(g2));
+    // the norm before GEMM1
+    const OpNode* nm = i > 0 && free ? &nodes[i - 1] : nullptr;
+    if (nm && (nm->op == OP_LAYERNORM || nm->op == OP_RMSNORM)) {
+        const bool rms = nm->op == OP_RMSNORM;
+        const void* x = nm->inputs[0];
+        const void* w = nm->inputs[1];
+        const void* b = rms ? nullptr : nm->inputs[2];
+        std::vector<Rng> inter_n = inter;
+        inter_n.push_back(out_rng(nm));
+        if (is_f32(nm) && nm->n_inputs >= (rms ? 2 : 3) && g1->inputs[0] == nm->output &&
+            node_last_dim(nm) == D && node_total(nm) == M * D && rows_ok(x) && lbr_aligned(w, 16) &&
+            (!b || lbr_aligned(b, 16)) && !overlap(y_r, rng(w, D * 4)) && !(b && overlap(y_r, rng(b, D * 4))) &&
+            dead_after(nodes, n, i + count, inter_n, {y_r}, live)) {
+            f->first = i - 1;
+            f->count = count + 1;
+            f->kind = LBR_FUSE_MLP;
+            f->act = act;
+            f->resid = R;
+            f->out = y;
+            f->norm = rms ? LBR_NORM_RMS : LBR_NORM_LAYER;
+            f->norm_src = x;
+            f->norm_g = w;
+            f->norm_b = b;
+            f->norm_eps = node_extra_float(nm, 0);
+            return true;
+        }
+    }
+    if (!rows_ok(g1->inputs[0]) || !dead_after(nodes, n, i + count, inter, {y_r}, live)) return false;
+    f->first = i;
+    f->count = count;
+    f->kind = LBR_FUSE_MLP;
+    f->act = act;
+    f->resid = R;
+    f->out = y;
+    return true;
+}
+
 bool gemm_first_kind(int kind) {
     return kind == LBR_FUSE_GEMM_HEADS || kind == LBR_FUSE_GEMM_GATED || kind == LBR_FUSE_GEMM_ACT ||
            kind == LBR_FUSE_GEMM_RESID;
@@ -745,6 +841,15 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
         const OpNode* nd = &nodes[i];
         Step gs;
         if (gemm_step(nd, &gs)) {
+            {
+                FusedRun f;
+                const bool free = out->empty() || out->back().first + out->back().count < i;
+                if (match_mlp(nodes, n, i, free, live, &f)) {
+                    out->push_back(f);
+                    i = f.first + f.count;
+                    continue;
+                }
+            }
             std::vector<Rng> gin;
             gemm_input_rngs(nd, gs, &gin);
             const Rng c_r = out_rng(nd);
@@ -1122,6 +1227,36 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
         } else {
             s->name = "gemm_dma_f32_nt+tin";
         }
+    } else if (f.kind == LBR_FUSE_MLP) {
+        const int g1 = f.first + (f.norm ? 1 : 0);
+        Step s1, s2;
+        int rc = decode_matmul(&nodes[g1], &s1);
+        if (!rc) rc = decode_matmul(&nodes[g1 + 2], &s2);
+        if (rc) return rc;
+        if (!mlp_shape_ok(s1.i[0], s1.i[2], s1.i[1], s2.i[1])) {
+            lbr_set_error("fusion: MLP at node %d does not fit the one-kernel form", g1);
+            return LBR_ERR_INVALID;
+        }
+        s->in[0] = f.norm ? f.norm_src : nodes[g1].inputs[0];
+        s->in[1] = nodes[g1].inputs[1];
+        s->in[2] = s1.i[6] ? nodes[g1].inputs[2] : nullptr;
+        s->in[3] = nodes[g1 + 2].inputs[1];
+        s->in[4] = s2.i[6] ? nodes[g1 + 2].inputs[2] : nullptr;
+        s->in[5] = f.resid;
+        s->in[6] = f.norm_g;
+        s->in[7] = f.norm_b;
+        s->out = (void*)f.out;
+        s->i[0] = s1.i[0];
+        s->i[1] = s1.i[2];
+        s->i[2] = s1.i[1];
+        s->i[3] = s2.i[1];
+        s->i[4] = f.act;
+        s->i[5] = f.norm;
+        s->f[0] = s1.f[0];
+        s->f[1] = s2.f[0];
+        s->f[2] = f.norm_eps;
+        s->run = mlp_launcher(s1.i[2], f.act);
+        s->name = f.norm ? "mlp_rows+norm" : "mlp_rows";
     } else if (f.kind == LBR_FUSE_NORM_GEMM) {
         int rc = decode_matmul(&nodes[f.first + 1], s);
         if (rc) return rc;
@@ -1213,7 +1348,7 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
         }
         s->name = f.rope ? (norm ? "head_norm_rope" : "head_rope") : (norm ? "head_norm" : "head_transpose");
     }
-    if (f.norm) {   // the GEMM reads the norm's input and applies it (see match_norm_prologue)
+    if (f.norm && f.kind != LBR_FUSE_MLP) {   // the GEMM reads the norm's input and applies it (see match_norm_prologue)
         if (!s->i[14] || s->i[3] != 1 || s->i[10] > 1) {
             lbr_set_error("fusion: GEMM node %d is not on the single-batch DMA path without a K split", f.first + 1);
             return LBR_ERR_INVALID;

@@ -33,6 +33,28 @@ __device__ __forceinline__ float lbr_gelu_tanh(float x) {
 // x·σ(x) = x / (1 + e^(−x)), same evaluation
 __device__ __forceinline__ float lbr_silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
+// Row-norm arithmetic shared by norm_wave_rows and the fused MLP's prologue,
+// with contraction off (the compiler may otherwise form a different fused
+// multiply-add in each kernel: fma(y, y, x·x) in one, fma(x, x, y·y) in the
+// other), so both kernels normalise a row to the same bits: the float4
+// partial sum of x or x², and (x − μ)·r·γ + β / x·s·w.
+__device__ __forceinline__ float lbr_sum4(float4 v) {
+#pragma clang fp contract(off)
+    return (v.x + v.y) + (v.z + v.w);
+}
+__device__ __forceinline__ float lbr_sumsq4(float4 v) {
+#pragma clang fp contract(off)
+    return (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+}
+__device__ __forceinline__ float4 lbr_norm_affine(float4 d, float r, float4 w, float4 b) {
+#pragma clang fp contract(off)
+    return make_float4(d.x * r * w.x + b.x, d.y * r * w.y + b.y, d.z * r * w.z + b.z, d.w * r * w.w + b.w);
+}
+__device__ __forceinline__ float4 lbr_norm_scale(float4 x, float s, float4 w) {
+#pragma clang fp contract(off)
+    return make_float4(x.x * s * w.x, x.y * s * w.y, x.z * s * w.z, x.w * s * w.w);
+}
+
 // GEMM epilogue activation codes (fused MATMUL → RELU / GELU / SILU)
 #define LBR_ACT_NONE 0
 #define LBR_ACT_RELU 1
@@ -186,6 +208,10 @@ bool gemm_dma_tile_pairs(int tile);
 bool gemm_dma_retile(Step* s, int tile);
 int gemm_dma_written(const Step& s, void** ptr, size_t* bytes, int cap);
 int decode_attention(const OpNode* n, Step* s);
+// Fused MLP (mlp.hip): whether rows of width D, hidden H and output D2 fit
+// the one-kernel form; its launcher (Step layout in mlp.hip).
+bool mlp_shape_ok(long long M, long long D, long long H, long long D2);
+step_fn mlp_launcher(long long D, int act);
 
 // Helpers over the node record (same meaning as csrc/executor.c:30-48).
 static inline long long node_total(const OpNode* n) {

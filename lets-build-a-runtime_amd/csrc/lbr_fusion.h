@@ -45,6 +45,9 @@ struct FusedRun {
     // reads; taken only under the key-range split, whose merge kernel then writes every
     // row (after the split kernel has finished reading)
     bool defer = false;
+    // MLP: the run's GEMM1 is node first (+1 with a norm), its activation `act`,
+    // GEMM2 after it, `resid` / `out` the fused residual ADD's other input and output
+    // (`out` is GEMM2's output without it)
     // Norm prologue (any GEMM kind, and NORM_GEMM alone): node `first` is a RMSNORM /
     // LAYERNORM over the K columns of `norm_src` whose output was the GEMM's A; the
     // GEMM is node first + 1 and reads norm_src instead (LBR_NORM_*, 0: none)

@@ -47,10 +47,7 @@ __global__ __launch_bounds__(NB) void norm_wave_rows(const float* __restrict__ x
     }
     float s = 0.f;
 #pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-        if (!RMS) s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
-        else s += (v[k].x * v[k].x + v[k].y * v[k].y) + (v[k].z * v[k].z + v[k].w * v[k].w);
-    }
+    for (int k = 0; k < VPL; ++k) s += RMS ? lbr_sumsq4(v[k]) : lbr_sum4(v[k]);
     s = wave_sum(s);
     float4* o4 = reinterpret_cast<float4*>(out + row * cols);
     if (RMS) {
@@ -58,15 +55,7 @@ __global__ __launch_bounds__(NB) void norm_wave_rows(const float* __restrict__ x
 #pragma unroll
         for (int k = 0; k < VPL; ++k) {
             const int idx = lane + k * 64;
-            if (idx < c4) {
-                const float4 w = wv[k];
-                float4 r;
-                r.x = v[k].x * scale * w.x;
-                r.y = v[k].y * scale * w.y;
-                r.z = v[k].z * scale * w.z;
-                r.w = v[k].w * scale * w.w;
-                o4[idx] = r;
-            }
+            if (idx < c4) o4[idx] = lbr_norm_scale(v[k], scale, wv[k]);
         }
     } else {
         const float mean = s / cols;
@@ -76,7 +65,7 @@ __global__ __launch_bounds__(NB) void norm_wave_rows(const float* __restrict__ x
             const int idx = lane + k * 64;
             if (idx < c4) {
                 v[k].x -= mean; v[k].y -= mean; v[k].z -= mean; v[k].w -= mean;
-                var += (v[k].x * v[k].x + v[k].y * v[k].y) + (v[k].z * v[k].z + v[k].w * v[k].w);
+                var += lbr_sumsq4(v[k]);
             }
         }
         var = wave_sum(var);
@@ -84,15 +73,7 @@ __global__ __launch_bounds__(NB) void norm_wave_rows(const float* __restrict__ x
 #pragma unroll
         for (int k = 0; k < VPL; ++k) {
             const int idx = lane + k * 64;
-            if (idx < c4) {
-                const float4 w = wv[k], bb = bv[k];
-                float4 r;
-                r.x = v[k].x * inv_std * w.x + bb.x;
-                r.y = v[k].y * inv_std * w.y + bb.y;
-                r.z = v[k].z * inv_std * w.z + bb.z;
-                r.w = v[k].w * inv_std * w.w + bb.w;
-                o4[idx] = r;
-            }
+            if (idx < c4) o4[idx] = lbr_norm_affine(v[k], inv_std, wv[k], bv[k]);
         }
     }
 }

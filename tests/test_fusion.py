@@ -60,8 +60,7 @@ EXPECTED = {
     # ADD is one GEMM reading the [B,H,S,hd] layout (hd = 16 in the toy block: a 32-wide K step
     # of the O projection covers two whole heads); both LayerNorms run inside the (small) GEMM
     # that reads their output (the heads run and the FFN1 run start at the norm)
-    "toy": Counter({("gemm_heads", 11): 1, ("gemm_resid", 2): 1, ("gemm_act", 3): 1,
-                    ("transpose_gemm", 3): 1}),
+    "toy": Counter({("gemm_heads", 11): 1, ("mlp", 5): 1, ("transpose_gemm", 3): 1}),
     "gpt2w": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1, ("transpose_gemm", 3): 1}),
     "7b4k": Counter({("gemm_heads", 10): 1, ("gemm_resid", 2): 1, ("gemm_act", 2): 1, ("transpose_gemm", 3): 1}),
     # c_attn is MATMUL_ADD (bias already in the GEMM): three (slice, transpose) chains per layer;
@@ -588,3 +587,51 @@ def test_norm_prologue_refusals():
     assert _windows(_norm_gemm(x=EXT + (5 << 32) + 4)) == []
     # the norm's output is a declared live-out
     assert _windows(_norm_gemm(), live=[(ARENA, 256 * 128 * 4)]) == []
+
+
+# ---------------------------------------------------------------- MLP
+
+def _mlp(M=32, D=64, H=256, norm="layer", resid=True, act=OpType.GELU, y_off=None, x=EXT + (8 << 32), later=()):
+    """[norm(x) → n,] n·W1ᵀ + b1 → c1, act → h, h·W2ᵀ + b2 → c2, [ADD(x, c2) → y], then `later`."""
+    W1, B1, W2, B2 = (EXT + (k << 32) for k in (9, 10, 11, 12))
+    eps = int(np.float32(1e-5).view(np.int32))
+    nodes = []
+    a = x
+    if norm:
+        ins = [x, EXT + (6 << 32)] if norm == "rms" else [x, EXT + (6 << 32), EXT + (7 << 32)]
+        nodes.append(_node(OpType.RMSNORM if norm == "rms" else OpType.LAYERNORM, ins, ARENA, (1, M, D), (eps,)))
+        a = ARENA
+    nodes.append(_node(OpType.MATMUL_ADD, [a, W1, B1], ARENA + MB, (1, M, H), (D, 1, 1, 0)))
+    nodes.append(_node(act, [ARENA + MB], ARENA + 2 * MB, (1, M, H)))
+    nodes.append(_node(OpType.MATMUL_ADD, [ARENA + 2 * MB, W2, B2], ARENA + 3 * MB, (1, M, D), (H, 1, 1, 0)))
+    if resid:
+        nodes.append(_node(OpType.ADD, [x, ARENA + 3 * MB], ARENA + (y_off if y_off is not None else 4 * MB),
+                           (1, M, D), (1,)))
+    return nodes + list(later)
+
+
+def test_mlp_fuses(monkeypatch):
+    assert _windows(_mlp()) == [(0, 5, "mlp")]
+    assert _windows(_mlp(norm="rms", act=OpType.SILU)) == [(0, 5, "mlp")]
+    assert _windows(_mlp(norm=None)) == [(0, 4, "mlp")]
+    assert _windows(_mlp(resid=False)) == [(0, 4, "mlp")]
+    # the output written row for row over the norm's input (the residual)
+    assert _windows(_mlp(x=ARENA + 8 * MB, y_off=8 * MB)) == [(0, 5, "mlp")]
+    monkeypatch.setenv("LBR_MLP_FUSE", "0")
+    assert "mlp" not in {k for _, _, k in _windows(_mlp())}
+
+
+def test_mlp_refusals():
+    # hidden rows too wide for LDS ((D + H + 8) · 64 B > 64 KiB)
+    assert "mlp" not in {k for _, _, k in _windows(_mlp(D=256, H=1024))}
+    # too much work for one launch-bound kernel (2·M·(H·D + D·H) > 2^25)
+    assert "mlp" not in {k for _, _, k in _windows(_mlp(M=2048))}
+    # widths not multiples of 16
+    assert "mlp" not in {k for _, _, k in _windows(_mlp(D=72, H=256))}
+    # the hidden activation is read again later
+    reader = _node(OpType.RELU, [ARENA + 2 * MB], ARENA + 9 * MB, (1, 32, 256))
+    assert "mlp" not in {k for _, _, k in _windows(_mlp(later=[reader]))}
+    # the output partly over the norm's input (other rows than its own)
+    assert "mlp" not in {k for _, _, k in _windows(_mlp(x=ARENA + 8 * MB, y_off=8 * MB + 256))}
+    # the norm's output is a declared live-out: the MLP runs without it
+    assert _windows(_mlp(), live=[(ARENA, 32 * 64 * 4)]) == [(1, 4, "mlp")]
