@@ -1172,11 +1172,28 @@ bool gemm_dma_tile_pairs(int tile) {
     return tile >= 0 && tile < kNumDmaTiles && kDmaTiles[tile].pairs;
 }
 
+// The model's time for one K range on tile t (choose_dma's terms).
+static double dma_model_time(long long M, long long N, int K, int cus, int t) {
+    const DmaTile& d = kDmaTiles[t];
+    const double peak_cu = 157.3e12 / 256.0;
+    if (cus <= 0) cus = 256;
+    const long long tiles = ((M + d.tm - 1) / d.tm) * ((N + d.tn - 1) / d.tn);
+    const long long per_cu = (tiles + cus - 1) / cus;
+    const double eff = std::min<long long>(per_cu, d.occ) * d.waves < 8 ? 0.9 * d.eff : d.eff;
+    return (double)per_cu * 2.0 * d.tm * d.tn * K / (eff * peak_cu) + (double)((per_cu + d.occ - 1) / d.occ) * 3e-6;
+}
+
 int gemm_dma_tune_candidates(const Step& s, int* tiles, int cap) {
     int n = 0;
     if (!s.i[14] || s.i[10] > 1 || s.i[3] != 1) return 0;   // one batch, no K split
+    // tiles the model prices at more than twice its best are not timed (the
+    // 256×256 tile on a 1024-row GEMM, say): only near-ties need measuring
+    double best = 1e30;
+    for (int t = 0; t < kNumDmaTiles; ++t)
+        if (dma_family_launcher(s, t)) best = std::min(best, dma_model_time(s.i[0], s.i[1], (int)s.i[2], lbr_device_cus(), t));
     for (int t = 0; t < kNumDmaTiles && n < cap; ++t)
-        if (dma_family_launcher(s, t)) tiles[n++] = t;
+        if (dma_family_launcher(s, t) && dma_model_time(s.i[0], s.i[1], (int)s.i[2], lbr_device_cus(), t) <= 2.0 * best)
+            tiles[n++] = t;
     return n;
 }
 
