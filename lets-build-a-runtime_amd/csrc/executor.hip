@@ -398,9 +398,23 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
                 return rc;
             }
             s.fuse_kind = runs[r].kind;
-            p->steps.push_back(s);
             i += runs[r].count;
             ++r;
+            // the K prologue right after the Q prologue of a layer joins its launch
+            if (r < runs.size() && runs[r].first == i && runs[r].kind == LBR_FUSE_HEAD_PROLOGUE) {
+                Step s2;
+                rc = lbr_fused_step(nodes, runs[r], &s2);
+                if (rc) {
+                    delete p;
+                    return rc;
+                }
+                s2.fuse_kind = runs[r].kind;
+                if (lbr_merge_head_steps(&s, s2)) {
+                    i += runs[r].count;
+                    ++r;
+                }
+            }
+            p->steps.push_back(s);
         } else {
             p->steps.push_back(decoded[i]);
             ++i;

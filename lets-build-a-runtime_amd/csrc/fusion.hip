@@ -131,63 +131,129 @@ __global__ __launch_bounds__(256) void head_prologue(HeadArgs a) {
     }
 }
 
-// float4 form for 16-byte aligned rows: a row of HD floats is LPR = HD/4
-// lanes holding one float4 each, so a 64-lane wavefront carries 64/LPR rows
-// (2 at HD = 128) and a 256-thread block 256/LPR rows; every load is a
-// 16-byte vector.  The rotate-half partner of a lane's four values sits
-// LPR/2 lanes away in the same row group (d ± HD/2), and the RMSNorm sum
-// reduces over the row's LPR lanes.
+// float4 form for 16-byte aligned rows.  A row of HD floats is LPR = HD/4
+// lanes holding one float4 each, so one float4 slot of a wavefront covers
+// HPS = 64/LPR rows (2 at HD = 128), and each lane holds R slots: a
+// wavefront task is R·HPS heads of one token.  Every load of the task (R
+// rows, their biases, the norm weight, the RoPE rows) issues before any
+// arithmetic; RoPE tables that do not vary over heads are loaded once.  The
+// RMSNorm sum over the row's LPR lanes and the rotate-half partner LPR/2
+// lanes away (d ± HD/2) move through DPP and row swaps, not LDS.
 //
-// Grid: x = token (b·S + s), y = group of RPB heads of that token, so the
-// (token, head) coordinates come from the block indices without divisions.
-template <int HD, bool BIAS, bool NORM, bool ROPE>
-__global__ __launch_bounds__(256) void head_prologue4(HeadArgs a) {
+// Up to two parts share a launch: the Q and K prologues of one attention
+// layer, sliced from the same projection output with the same RoPE tables.
+// Tasks run head group by head group (G0 groups of part 0, then G1 of part
+// 1), each over all tokens, so neighbouring wavefronts write neighbouring
+// rows of the same heads.
+struct HeadPart {
+    int col0, H, G;           // first column in the source, heads, tasks per token
+    const float* bias;        // [H·hd] or null
+    const float* w;           // RMSNorm weight [hd] or null
+    float* out;               // [B, H, S, hd]
+    float eps;
+};
+
+struct HeadArgs4 {
+    const float* src;
+    long long ld;
+    int S, T;                 // tokens per batch, tasks per token (G0 + G1)
+    int N_m, N_s, S_m, S_s;   // divisors by the token count and S (lbr_fdiv)
+    unsigned tokens, tasks;   // B·S, B·S·T
+    const float* cos;
+    const float* sin;
+    long long cst[3], sst[3];
+    bool shared_tables;       // cst[1] == sst[1] == 0: one RoPE row per token
+    HeadPart p[2];
+};
+
+template <int HD, bool BIAS, bool NORM, bool ROPE, int R>
+__global__ __launch_bounds__(256) void head_rows4(HeadArgs4 a) {
     constexpr int LPR = HD / 4;
-    constexpr int RPB = 256 / LPR;
-    const int l = threadIdx.x % LPR;
-    const int h = blockIdx.y * RPB + threadIdx.x / LPR;
-    if (h >= a.H) return;        // whole row groups leave together: shuffles stay inside live groups
-    const unsigned bs = blockIdx.x;
-    const int s = (int)(bs % (unsigned)a.S), b = (int)(bs / (unsigned)a.S);
+    constexpr int HPS = 64 / LPR;
+    const int lane = threadIdx.x & 63;
+    const unsigned task = blockIdx.x * 4u + (unsigned)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (task >= a.tasks) return;   // whole wavefronts leave: shuffles stay inside live ones
+    const unsigned rg = lbr_fdiv(task, a.N_m, a.N_s);              // head group of the parts
+    const unsigned bs = task - rg * a.tokens;                       // token b·S + s
+    const int r = (int)rg;
+    const unsigned b = lbr_fdiv(bs, a.S_m, a.S_s);
+    const int s = (int)(bs - b * (unsigned)a.S);
+    const bool second = r >= a.p[0].G;
+    const int col0 = second ? a.p[1].col0 : a.p[0].col0;
+    const int H = second ? a.p[1].H : a.p[0].H;
+    const float* __restrict__ bias = second ? a.p[1].bias : a.p[0].bias;
+    const float* __restrict__ w = second ? a.p[1].w : a.p[0].w;
+    float* __restrict__ out = second ? a.p[1].out : a.p[0].out;
+    const float eps = second ? a.p[1].eps : a.p[0].eps;
+    const int grp = second ? r - a.p[0].G : r;
+    const int l = lane % LPR;
     const int d = 4 * l;
-    const float4 xv = *reinterpret_cast<const float4*>(a.src + (long long)bs * a.ld + a.col0 + (long long)h * HD + d);
-    float4 wv, cv, sv;
-    if (NORM) wv = *reinterpret_cast<const float4*>(a.w + d);
+    const int h0 = grp * (R * HPS) + lane / LPR;                   // slot k holds head h0 + k·HPS
+    const float* __restrict__ x = a.src + (long long)bs * a.ld + col0 + d;
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 xv[R], cv[R], sv[R], wv = zero;
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        const int h = h0 + k * HPS;
+        xv[k] = h < H ? *reinterpret_cast<const float4*>(x + (long long)h * HD) : zero;
+    }
+    if (NORM) wv = *reinterpret_cast<const float4*>(w + d);
     if (ROPE) {
-        cv = *reinterpret_cast<const float4*>(a.cos + b * a.cst[0] + h * a.cst[1] + s * a.cst[2] + d);
-        sv = *reinterpret_cast<const float4*>(a.sin + b * a.sst[0] + h * a.sst[1] + s * a.sst[2] + d);
-    }
-    float v[4] = {xv.x, xv.y, xv.z, xv.w};
-    if (BIAS) {
-        const float4 bv = *reinterpret_cast<const float4*>(a.bias + h * HD + d);
-        v[0] = v[0] + bv.x;
-        v[1] = v[1] + bv.y;
-        v[2] = v[2] + bv.z;
-        v[3] = v[3] + bv.w;
-    }
-    if (NORM) {   // norm.c:100-107 order: x · (1/sqrt(Σx²/n + eps)) · w
-        float ss = (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+        if (a.shared_tables) {
+            const float4 c = *reinterpret_cast<const float4*>(a.cos + b * a.cst[0] + s * a.cst[2] + d);
+            const float4 sn = *reinterpret_cast<const float4*>(a.sin + b * a.sst[0] + s * a.sst[2] + d);
 #pragma unroll
-        for (int off = LPR / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
-        const float scale = 1.0f / sqrtf(ss / HD + a.eps);
-        v[0] = v[0] * scale * wv.x;
-        v[1] = v[1] * scale * wv.y;
-        v[2] = v[2] * scale * wv.z;
-        v[3] = v[3] * scale * wv.w;
-    }
-    float4* o = reinterpret_cast<float4*>(a.out + (((long long)b * a.H + h) * a.S + s) * HD + d);
-    if (ROPE) {   // y = x·cos + rotate_half(x)·sin, rotate_half = cat(−x[half:], x[:half])
-        const float sign = l < LPR / 2 ? -1.0f : 1.0f;
-        const float c[4] = {cv.x, cv.y, cv.z, cv.w}, sn[4] = {sv.x, sv.y, sv.z, sv.w};
-        float r[4];
+            for (int k = 0; k < R; ++k) {
+                cv[k] = c;
+                sv[k] = sn;
+            }
+        } else {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const float rot = sign * __shfl_xor(v[k], LPR / 2, 64);
-            r[k] = __fadd_rn(__fmul_rn(v[k], c[k]), __fmul_rn(rot, sn[k]));
+            for (int k = 0; k < R; ++k) {
+                const int h = min(h0 + k * HPS, H - 1);
+                cv[k] = *reinterpret_cast<const float4*>(a.cos + b * a.cst[0] + h * a.cst[1] + s * a.cst[2] + d);
+                sv[k] = *reinterpret_cast<const float4*>(a.sin + b * a.sst[0] + h * a.sst[1] + s * a.sst[2] + d);
+            }
         }
-        *o = make_float4(r[0], r[1], r[2], r[3]);
-    } else {
-        *o = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    if (BIAS) {
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const int h = min(h0 + k * HPS, H - 1);
+            const float4 bv = *reinterpret_cast<const float4*>(bias + h * HD + d);
+            xv[k].x = xv[k].x + bv.x;
+            xv[k].y = xv[k].y + bv.y;
+            xv[k].z = xv[k].z + bv.z;
+            xv[k].w = xv[k].w + bv.w;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        float v[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
+        if (NORM) {   // norm.c:100-107 order: x · (1/sqrt(Σx²/n + eps)) · w
+            const float ss = lbr_group_sum<LPR>((v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]));
+            const float scale = 1.0f / sqrtf(ss / HD + eps);
+            v[0] = v[0] * scale * wv.x;
+            v[1] = v[1] * scale * wv.y;
+            v[2] = v[2] * scale * wv.z;
+            v[3] = v[3] * scale * wv.w;
+        }
+        float4 y;
+        if (ROPE) {   // y = x·cos + rotate_half(x)·sin, rotate_half = cat(−x[half:], x[:half])
+            const float sign = l < LPR / 2 ? -1.0f : 1.0f;
+            const float c[4] = {cv[k].x, cv[k].y, cv[k].z, cv[k].w}, sn[4] = {sv[k].x, sv[k].y, sv[k].z, sv[k].w};
+            float o[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float rot = sign * lbr_half_partner<LPR>(v[q], lane);
+                o[q] = __fadd_rn(__fmul_rn(v[q], c[q]), __fmul_rn(rot, sn[q]));
+            }
+            y = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+            y = make_float4(v[0], v[1], v[2], v[3]);
+        }
+        const int h = h0 + k * HPS;
+        if (h < H) *reinterpret_cast<float4*>(out + (((long long)b * H + h) * a.S + s) * HD + d) = y;
     }
 }
 
@@ -225,21 +291,53 @@ void launch_head_prologue(const Step& s, hipStream_t st) {
                        a);
 }
 
+constexpr int kHeadSlots = 2;   // R: row slots per lane of the float4 kernel
+
+// The float4 kernel's step: the scalar step's fields for part 0, and
+// i[14] = parts (1 or 2), i[15] = H, i[16] = col0 of part 1, in[5..7] = its
+// bias, weight and output, f[1] = its eps (set by lbr_merge_head_steps).
 template <int HD, bool BIAS, bool NORM, bool ROPE>
-void launch_head_prologue4(const Step& s, hipStream_t st) {
-    const HeadArgs a = head_args(s);
-    constexpr int RPB = 256 / (HD / 4);
-    if (a.rows <= 0) return;
-    hipLaunchKernelGGL((head_prologue4<HD, BIAS, NORM, ROPE>), dim3((unsigned)((long long)a.B * a.S),
-                       (unsigned)((a.H + RPB - 1) / RPB)), dim3(256), 0, st, a);
+void launch_head_rows4(const Step& s, hipStream_t st) {
+    constexpr int HPT = kHeadSlots * (256 / HD);   // heads per wavefront task
+    const long long tokens = s.i[2] * s.i[3];
+    if (tokens <= 0 || s.i[4] <= 0) return;
+    HeadArgs4 a;
+    a.src = (const float*)s.in[0];
+    a.ld = s.i[0];
+    a.S = (int)s.i[3];
+    a.cos = (const float*)s.in[3];
+    a.sin = (const float*)s.in[4];
+    for (int k = 0; k < 3; ++k) {
+        a.cst[k] = s.i[6 + k];
+        a.sst[k] = s.i[9 + k];
+    }
+    a.shared_tables = a.cst[1] == 0 && a.sst[1] == 0;
+    const int parts = s.i[14] == 2 ? 2 : 1;
+    for (int p = 0; p < 2; ++p) {
+        const bool on = p < parts;
+        HeadPart& q = a.p[p];
+        q.col0 = (int)(p ? s.i[16] : s.i[1]);
+        q.H = on ? (int)(p ? s.i[15] : s.i[4]) : 0;
+        q.G = (q.H + HPT - 1) / HPT;
+        q.bias = (const float*)(p ? s.in[5] : s.in[1]);
+        q.w = (const float*)(p ? s.in[6] : s.in[2]);
+        q.out = (float*)(p ? (void*)s.in[7] : s.out);
+        q.eps = p ? s.f[1] : s.f[0];
+    }
+    a.T = a.p[0].G + a.p[1].G;
+    a.tokens = (unsigned)tokens;
+    a.tasks = (unsigned)(tokens * a.T);
+    lbr_fast_divisor(a.tokens, &a.N_m, &a.N_s);
+    lbr_fast_divisor((unsigned)a.S, &a.S_m, &a.S_s);
+    hipLaunchKernelGGL((head_rows4<HD, BIAS, NORM, ROPE, kHeadSlots>), dim3((a.tasks + 3) / 4), dim3(256), 0, st, a);
 }
 
 // W = VPL (scalar kernel, 64·VPL = hd) or HD (float4 kernel)
 template <int W, bool BIAS, bool VEC>
 step_fn pick_hp2(bool norm, bool rope) {
     if constexpr (VEC) {
-        if (norm) return rope ? launch_head_prologue4<W, BIAS, true, true> : launch_head_prologue4<W, BIAS, true, false>;
-        return rope ? launch_head_prologue4<W, BIAS, false, true> : launch_head_prologue4<W, BIAS, false, false>;
+        if (norm) return rope ? launch_head_rows4<W, BIAS, true, true> : launch_head_rows4<W, BIAS, true, false>;
+        return rope ? launch_head_rows4<W, BIAS, false, true> : launch_head_rows4<W, BIAS, false, false>;
     } else {
         if (norm) return rope ? launch_head_prologue<W, BIAS, true, true> : launch_head_prologue<W, BIAS, true, false>;
         return rope ? launch_head_prologue<W, BIAS, false, true> : launch_head_prologue<W, BIAS, false, false>;
@@ -1338,9 +1436,13 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
             vec = vec && lbr_aligned(f.cos, 16) && lbr_aligned(f.sin, 16);
             for (int k = 0; k < 3; ++k) vec = vec && f.cst[k] % 4 == 0 && f.sst[k] % 4 == 0;
         }
+        // the float4 kernel's task index (token, heads group) stays below 2³¹
+        const long long hpt = kHeadSlots * (256 / f.hd);
+        vec = vec && (long long)f.B * f.S * 2 * ((f.Hs[0] + hpt - 1) / hpt) < (1LL << 31);
         const char* force = getenv("LBR_HEAD_PROLOGUE");   // "scalar" keeps the one-row-per-wave kernel
         if (force && strcmp(force, "scalar") == 0) vec = false;
         s->i[13] = vec;
+        s->i[14] = 1;   // parts (lbr_merge_head_steps joins a second)
         switch (f.hd / 64) {
             case 1: s->run = vec ? pick_hp<64, true>(bias, norm, f.rope) : pick_hp<1, false>(bias, norm, f.rope); break;
             case 2: s->run = vec ? pick_hp<128, true>(bias, norm, f.rope) : pick_hp<2, false>(bias, norm, f.rope); break;
@@ -1375,3 +1477,51 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
     s->n_nodes = f.count;
     return LBR_OK;
 }
+
+// Joins step b, the HEAD_PROLOGUE run right after a's in the stream, into a
+// (both float4 kernels of the same form, the same source rows and RoPE
+// tables): one launch then covers both parts.  Taken only when neither
+// output overlaps anything either part reads, or the other output, so the
+// joined launch computes what the two did in order.
+bool lbr_merge_head_steps(Step* a, const Step& b) {
+    if (a->fuse_kind != LBR_FUSE_HEAD_PROLOGUE || b.fuse_kind != LBR_FUSE_HEAD_PROLOGUE) return false;
+    if (!a->i[13] || !b.i[13] || a->i[14] != 1 || b.i[14] != 1 || a->run != b.run) return false;
+    if (getenv("LBR_HEAD_MERGE") && strcmp(getenv("LBR_HEAD_MERGE"), "0") == 0) return false;
+    if (a->node_index + a->n_nodes != b.node_index) return false;
+    if (a->in[0] != b.in[0] || a->in[3] != b.in[3] || a->in[4] != b.in[4]) return false;
+    for (int k = 0; k <= 11; ++k)   // ld, B, S, hd and the table strides; k = 1, 4 are col0 and H
+        if (k != 1 && k != 4 && a->i[k] != b.i[k]) return false;
+    const long long B = a->i[2], S = a->i[3], hd = a->i[5];
+    const long long hpt = kHeadSlots * (256 / hd);
+    if (B * S * ((a->i[4] + hpt - 1) / hpt + (b.i[4] + hpt - 1) / hpt) >= (1LL << 31)) return false;
+    auto out_rng = [&](const Step& t) { return Rng{(uintptr_t)t.out, (uintptr_t)t.out + (uintptr_t)(B * t.i[4] * S * hd * 4)}; };
+    auto reads = [&](const Step& t) {
+        std::vector<Rng> r{Rng{(uintptr_t)t.in[0], (uintptr_t)t.in[0] + (uintptr_t)(B * S * t.i[0] * 4)}};
+        if (t.in[1]) r.push_back(Rng{(uintptr_t)t.in[1], (uintptr_t)t.in[1] + (uintptr_t)(t.i[4] * hd * 4)});
+        if (t.in[2]) r.push_back(Rng{(uintptr_t)t.in[2], (uintptr_t)t.in[2] + (uintptr_t)(hd * 4)});
+        for (int k = 0; k < 2; ++k) {
+            const void* tab = t.in[3 + k];
+            if (!tab) continue;
+            const long long* st = &t.i[6 + 3 * k];
+            const long long ext = ((B - 1) * st[0] + (t.i[4] - 1) * st[1] + (S - 1) * st[2] + hd) * 4;
+            r.push_back(Rng{(uintptr_t)tab, (uintptr_t)tab + (uintptr_t)ext});
+        }
+        return r;
+    };
+    const Rng oa = out_rng(*a), ob = out_rng(b);
+    if (overlap(oa, ob)) return false;
+    for (const Rng& r : reads(*a))
+        if (overlap(ob, r)) return false;
+    for (const Rng& r : reads(b))
+        if (overlap(oa, r)) return false;
+    a->i[14] = 2;
+    a->i[15] = b.i[4];
+    a->i[16] = b.i[1];
+    a->in[5] = b.in[1];
+    a->in[6] = b.in[2];
+    a->in[7] = b.out;
+    a->f[1] = b.f[0];
+    a->n_nodes += b.n_nodes;
+    return true;
+}
+

@@ -80,6 +80,58 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// DPP / row-swap lane exchanges (VALU; no LDS round trip).  lbr_dpp<CTRL>
+// returns v of the lane that the DPP control selects: 0xB1 quad_perm
+// [1,0,3,2] (lane ^ 1), 0x4E quad_perm [2,3,0,1] (lane ^ 2), 0x141
+// row_half_mirror (7 − i within 8 lanes), 0x140 row_mirror (15 − i within
+// 16), 0x128 row_ror:8 (lane ^ 8 within 16).
+template <int CTRL>
+__device__ __forceinline__ float lbr_dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of G lanes (G = 16, 32 or 64); every lane of a
+// group gets the same value.  Pairs are combined as x + y = y + x, so the
+// lanes agree bit for bit.  v_permlane16_swap(u, u) returns {u of the even
+// 16-lane row, u of the odd row} of each row pair (v_permlane32_swap: of
+// each 32-lane half).
+template <int G>
+__device__ __forceinline__ float lbr_group_sum(float s) {
+    static_assert(G == 16 || G == 32 || G == 64, "group of 16, 32 or 64 lanes");
+    s += lbr_dpp<0xB1>(s);
+    s += lbr_dpp<0x4E>(s);
+    s += lbr_dpp<0x141>(s);
+    s += lbr_dpp<0x140>(s);
+    if (G >= 32) {
+        const unsigned u = __float_as_uint(s);
+        auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    }
+    if (G == 64) {
+        const unsigned u = __float_as_uint(s);
+        auto b = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        s = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+    }
+    return s;
+}
+
+// v of lane ^ (G/2) for G = 16, 32 or 64.
+template <int G>
+__device__ __forceinline__ float lbr_half_partner(float v, int lane) {
+    static_assert(G == 16 || G == 32 || G == 64, "group of 16, 32 or 64 lanes");
+    if constexpr (G == 16) {
+        return lbr_dpp<0x128>(v);
+    } else if constexpr (G == 32) {
+        const unsigned u = __float_as_uint(v);
+        auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return __uint_as_float((lane & 16) ? a[0] : a[1]);
+    } else {
+        const unsigned u = __float_as_uint(v);
+        auto b = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        return __uint_as_float((lane & 32) ? b[0] : b[1]);
+    }
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, LBR_WAVE));

@@ -66,6 +66,12 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
 // Launch record of one fused run.
 int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s);
 
+// Joins the HEAD_PROLOGUE step b (the run right after a's) into a as the
+// second part of one float4 launch, when both are the same kernel over the
+// same source rows and tables and neither output overlaps what the other
+// reads; false leaves a unchanged.
+bool lbr_merge_head_steps(Step* a, const Step& b);
+
 // Byte range [*lo, *hi) input k of node nd reads (per op, from its shape and
 // extras); *hi = UINTPTR_MAX when the node does not fix it.
 void lbr_input_extent(const OpNode* nd, int k, unsigned long long* lo, unsigned long long* hi);
