@@ -1354,6 +1354,10 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
         s->f[1] = s2.f[0];
         s->f[2] = f.norm_eps;
         s->run = mlp_launcher(s1.i[2], f.act);
+        if (!s->run) {
+            lbr_set_error("fusion: the MLP kernel's LDS limit could not be raised (node %d)", f.first + 1);
+            return LBR_ERR_HIP;
+        }
         s->name = f.norm ? "mlp_rows+norm" : "mlp_rows";
     } else if (f.kind == LBR_FUSE_NORM_GEMM) {
         int rc = decode_matmul(&nodes[f.first + 1], s);

@@ -409,7 +409,7 @@ constexpr int DBK = 32;
 // 16-byte DMA into LDS: lane l's dword4 at r + voff + soff lands at lds + 16·l.
 // (A plain device function: the builtin has no host-side form inside kernel templates.)
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, float* lds, unsigned voff, unsigned soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, soff, 0, 0);
+    lbr_dma16(r, lds, voff, soff);
 }
 
 template <int NV, int ND, int NM>
@@ -436,12 +436,7 @@ __device__ __forceinline__ void chunk_schedule() {
 // 1/√(var + eps) (= GEMM((x − μ)·r·γ + β)).  The shift keeps the one-pass
 // variance and the subtraction well conditioned when |μ| ≫ σ.  γ (and β) for
 // each K step ride in the stage behind B, loaded by DMA with it.
-// s_waitcnt immediate that waits until at most n vector-memory operations of
-// the wave are outstanding (gfx9 encoding: vmcnt bits [3:0] and [15:14]; the
-// other counters at their maximum, as in 0x3F70 = vmcnt(0)).
-constexpr int waitcnt_vm(int n) {
-    return 0x3F70 | (n & 15) | (((n >> 4) & 3) << 14);
-}
+constexpr int waitcnt_vm(int n) { return lbr_waitcnt_vm(n); }
 
 // NS: LDS stages of the K pipeline.  Step kt+NS−1 is in flight while step kt
 // is consumed, so a grid that leaves one or two workgroups on a CU (nothing

@@ -74,10 +74,16 @@ __device__ __forceinline__ float lbr_act(int act, float v) {
 // Wave / block reductions (64-lane wavefronts)
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, LBR_WAVE);
-    return v;
+// s_waitcnt immediate that waits until at most n vector-memory operations of
+// the wave are outstanding (gfx9 encoding: vmcnt bits [3:0] and [15:14]; the
+// other counters at their maximum, as in 0x3F70 = vmcnt(0)).
+constexpr int lbr_waitcnt_vm(int n) { return 0x3F70 | (n & 15) | (((n >> 4) & 3) << 14); }
+
+// Direct-to-LDS load of 16 bytes a lane: lane l's bytes at voff + soff of the
+// buffer land at lds + 16·l (lds wave-uniform), so one instruction fills a
+// contiguous 1 KB of LDS.  Counts in vmcnt like any vector load.
+__device__ __forceinline__ void lbr_dma16(__amdgpu_buffer_rsrc_t r, float* lds, unsigned voff, unsigned soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, soff, 0, 0);
 }
 
 // DPP / row-swap lane exchanges (VALU; no LDS round trip).  lbr_dpp<CTRL>
@@ -132,11 +138,31 @@ __device__ __forceinline__ float lbr_half_partner(float v, int lane) {
     }
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, LBR_WAVE));
-    return v;
+// Max over aligned groups of G lanes, as lbr_group_sum.
+template <int G>
+__device__ __forceinline__ float lbr_group_max(float s) {
+    static_assert(G == 16 || G == 32 || G == 64, "group of 16, 32 or 64 lanes");
+    s = fmaxf(s, lbr_dpp<0xB1>(s));
+    s = fmaxf(s, lbr_dpp<0x4E>(s));
+    s = fmaxf(s, lbr_dpp<0x141>(s));
+    s = fmaxf(s, lbr_dpp<0x140>(s));
+    if (G >= 32) {
+        const unsigned u = __float_as_uint(s);
+        auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        s = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    }
+    if (G == 64) {
+        const unsigned u = __float_as_uint(s);
+        auto b = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        s = fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+    }
+    return s;
 }
+
+// Whole-wavefront sum / max (every lane active); every lane gets the result.
+__device__ __forceinline__ float wave_sum(float v) { return lbr_group_sum<LBR_WAVE>(v); }
+
+__device__ __forceinline__ float wave_max(float v) { return lbr_group_max<LBR_WAVE>(v); }
 
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024).  `red` must hold
 // at least blockDim.x/64 floats.  All threads get the result.

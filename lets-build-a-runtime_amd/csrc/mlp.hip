@@ -6,9 +6,10 @@
 // 296-308 and the element-wise cases) when its hidden activations fit in
 // LDS: one 4-wavefront workgroup per 16 rows normalises its rows into LDS,
 // computes h = act(x·W1ᵀ + b1) into LDS, then y = h·W2ᵀ + b2 (+ R) to HBM.
-// For the launch-bound sizes it serves, each wavefront's share of both
-// weight matrices (at most 16 float4 fragments per lane per GEMM, 4 column
-// blocks) is loaded into registers at the start.
+// For the launch-bound sizes it serves, both weight matrices (at most 64 KB
+// each) are staged whole in LDS by direct-to-LDS DMA issued at the start,
+// and each wavefront reads its fragments (at most 16 float4 per lane per GEMM,
+// 4 column blocks) from there.
 // The hidden activations never leave the CU and the chain is one launch;
 // for the toy block's 32 rows the two GEMMs and the norm otherwise cost
 // three launches and two HBM round trips of h.
@@ -30,9 +31,19 @@ namespace {
 
 constexpr int MLP_NT = 256;     // 4 wavefronts
 constexpr int MLP_RB = 16;      // rows per workgroup (one MFMA row block)
-constexpr int MLP_FR = 16;      // B fragments (float4) per wave per GEMM: all loaded up front
+constexpr int MLP_FR = 16;      // B fragments (float4) per wave per GEMM: all read from LDS up front
+constexpr int MLP_DMA = 16;     // weight DMA instructions per wave per GEMM (≤ 64 KB of weight)
+constexpr int MLP_WMAX = 4 * MLP_DMA * 256;   // floats of one staged weight (64 KB)
 constexpr int MLP_NBW = 4;      // column blocks per wave per GEMM (its biases, loaded up front)
-constexpr size_t MLP_LDS_MAX = 64 * 1024;   // dynamic LDS without a launch attribute
+constexpr size_t MLP_LDS_MAX = 160 * 1024;  // gfx950's LDS per workgroup (the launcher raises the dynamic limit)
+constexpr int MLP_HAS_B1 = 1, MLP_HAS_B2 = 2, MLP_HAS_RESID = 4;
+
+// W [R, K] as staged in LDS (mlp_stage_weight): its shape, the chunk swizzle
+// mask and the divisor by K/4.
+struct MlpWeight {
+    int R, K, mask;
+    int kc_m, kc_s;   // divisor by K/4 (lbr_fdiv)
+};
 
 struct MlpArgs {
     const float* x;     // [M, D]: the norm's input, or GEMM1's A
@@ -44,28 +55,55 @@ struct MlpArgs {
     const float* g;     // norm weight [D] (norm != 0)
     const float* be;    // LayerNorm bias [D]
     float* y;           // [M, D2]
+    int has;            // MLP_HAS_*: which of b1, b2, r are present (absent ones, and g / be, point at x)
     int M, D, H, D2, act, norm;
     float alpha1, alpha2, eps;
+    MlpWeight w1s, w2s;   // W1 [H, D] and W2 [D2, H] as staged in LDS
 };
 
-// This wave's B fragments of C = A·Wᵀ, W [cols, K] row-major: the wave takes
+// A weight W [R, K] (row-major) staged in LDS by direct-to-LDS DMA.  In LDS
+// the rows keep their order and length, and 16-byte chunk q of row r holds
+// W's chunk q ^ (r & mask) of that row (mask + 1 = the largest power of two
+// ≤ 16 dividing K/4), so the 16 rows of a fragment read fall in distinct bank
+// groups.  One DMA instruction fills 64 consecutive LDS chunks from 64
+// global chunks of the same rows, permuted within each row: a coalesced 1 KB
+// read, where loading fragments straight from HBM gathers 16 rows × 64 B per
+// instruction (2.2× slower measured at the toy block's 128 KB).  Each wave
+// issues MLP_DMA instructions (R·K/256 in all, at most 4·MLP_DMA; a wave
+// past the end repeats the last one, writing the same bytes again), so every
+// wave has the same count in flight.
+
+__device__ __forceinline__ void mlp_stage_weight(const float* __restrict__ W, const MlpWeight& w, float* lds) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kc = w.K / 4, n = w.R * kc / 64;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, w.R * w.K * 4, 0x00020000);
+#pragma unroll
+    for (int t = 0; t < MLP_DMA; ++t) {
+        const int ins = min(wave + 4 * t, n - 1);
+        const int L = ins * 64 + lane;                        // LDS chunk: row r, position q
+        const int r = (int)lbr_fdiv((unsigned)L, w.kc_m, w.kc_s);
+        const int q = L - r * kc;
+        lbr_dma16(rs, lds + ins * 256, (unsigned)(r * w.K + 4 * (q ^ (r & w.mask))) * 4u, 0u);
+    }
+}
+
+// This wave's B fragments of C = A·Wᵀ from the staged W: the wave takes
 // column blocks wave, wave + 4, …; fragment p = (block j, 16-wide K chunk c),
 // block-major; lane (kq, lr) holds W[16·(wave + 4j) + lr][16c + 4kq .. +3].
-// All P ≤ MLP_FR of them are issued together (P is wave-uniform).
-__device__ __forceinline__ void mlp_load_frags(const float* __restrict__ W, int K, int P, float4 (&f)[MLP_FR]) {
+// All MLP_FR reads issue (past P the last fragment repeats; a wave with no
+// block reads row R − 1), with no branch around them.
+__device__ __forceinline__ void mlp_read_frags(const float* __restrict__ lds, const MlpWeight& w, int P,
+                                               float4 (&f)[MLP_FR]) {
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const float* __restrict__ wl = W + (long long)(16 * wave + (lane & 15)) * K + 4 * (lane >> 4);
-    const int nch = K / 16;
+    const int nch = w.K / 16;
     int j = 0, c = 0;
 #pragma unroll
     for (int p = 0; p < MLP_FR; ++p) {
-        if (p < P) {
-            f[p] = *reinterpret_cast<const float4*>(wl + (long long)j * 64 * K + 16 * c);
-            if (++c == nch) {
-                c = 0;
-                ++j;
-            }
-        }
+        const int r = min(16 * (wave + 4 * j) + (lane & 15), w.R - 1);
+        f[p] = *reinterpret_cast<const float4*>(lds + r * w.K + 4 * ((4 * c + (lane >> 4)) ^ (r & w.mask)));
+        const bool step = p + 1 < P;   // wave-uniform: stay on the last fragment past P
+        c = step ? (c + 1 == nch ? 0 : c + 1) : c;
+        j = step && c == 0 ? j + 1 : j;
     }
 }
 
@@ -115,7 +153,10 @@ __device__ __forceinline__ void mlp_norm_row(const MlpArgs& g, float4 (&v)[VPL],
     const bool rms = g.norm == LBR_NORM_RMS;
     float s = 0.f;
 #pragma unroll
-    for (int k = 0; k < VPL; ++k) s += rms ? lbr_sumsq4(v[k]) : lbr_sum4(v[k]);
+    for (int k = 0; k < VPL; ++k) {   // a lane past the row adds 0, as norm_wave_rows' zeroed values do
+        const float t = rms ? lbr_sumsq4(v[k]) : lbr_sum4(v[k]);
+        s += lane + k * 64 < c4 ? t : 0.f;
+    }
     s = wave_sum(s);
     if (rms) {
         const float scale = 1.0f / sqrtf(s / g.D + g.eps);
@@ -147,19 +188,25 @@ __device__ __forceinline__ void mlp_norm_row(const MlpArgs& g, float4 (&v)[VPL],
     }
 }
 
-// LDS: xs [16][D + 4] (normalised rows), hs [16][H + 4] (hidden rows); the
-// 4-float row padding puts the 16 rows of a fragment read in distinct banks.
-// Every global load (the wave's 4 rows, the norm's weight and bias, both
-// weights' fragments, both biases, the residual) is issued before the rows
-// are normalised, so the kernel waits for one memory round trip.  The output
-// is written only after the workgroup has read all of its residual rows (the
+// LDS: W1 [H][D] and W2 [D2][H] (staged, chunk-swizzled; static), xs [16][D + 4]
+// (normalised rows), hs [16][H + 4] (hidden rows); the 4-float row padding
+// puts the 16 rows of an A fragment read in distinct banks.  Every global
+// load (the wave's 4 rows, the norm's weight and bias, both biases, the
+// residual, then both weights' DMAs) is issued before the rows are
+// normalised, so the kernel waits for one memory round trip.  The output is
+// written only after the workgroup has read all of its residual rows (the
 // residual may lie under the output, row for row).
 template <int ACT, int VPL>
 __global__ __launch_bounds__(MLP_NT) void mlp_rows(MlpArgs g) {
+    // the staged weights in LDS variables of their own: the compiler then
+    // knows the norm's and GEMM1's LDS stores do not touch what the weight
+    // DMAs still in flight write, and does not wait for them
+    __shared__ __attribute__((aligned(1024))) float w1l[MLP_WMAX];
+    __shared__ __attribute__((aligned(1024))) float w2l[MLP_WMAX];
     extern __shared__ float smem[];
     const int ldx = g.D + 4, ldh = g.H + 4;
     float* xs = smem;
-    float* hs = smem + MLP_RB * ldx;
+    float* hs = xs + MLP_RB * ldx;
     const long long r0 = (long long)blockIdx.x * MLP_RB;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lr = lane & 15, kq = lane >> 4;
@@ -168,38 +215,48 @@ __global__ __launch_bounds__(MLP_NT) void mlp_rows(MlpArgs g) {
     // the wave's 4 rows and the norm's weight and bias first (needed first), then
     // both weights' fragments, the biases and the residual; a lane past the row's
     // D/4 float4s holds 0, as in norm_wave_rows, so the row sums see exactly the row
+    // Every load issues unconditionally from a clamped address (the host
+    // replaces an absent input by x and says so in g.has), so no branch hides
+    // a load from the compiler's count: the norm waits only for the rows,
+    // GEMM1 for W1's fragments.  Values loaded from outside the data are never
+    // used: the norm counts only lanes inside the row, and the epilogues use
+    // a bias or residual value only for a present input, a block of the wave
+    // and a row below M.
     const int c4 = g.D / 4;
     float4 xv[MLP_RB / 4][VPL], nw[VPL], nbv[VPL];
 #pragma unroll
     for (int i = 0; i < MLP_RB / 4; ++i) {
-        const long long row = r0 + wave + 4 * i;
+        const long long row = min(r0 + wave + 4 * i, (long long)g.M - 1);
         const float4* xr = reinterpret_cast<const float4*>(g.x + row * g.D);
 #pragma unroll
-        for (int k = 0; k < VPL; ++k)
-            xv[i][k] = row < g.M && lane + 64 * k < c4 ? xr[lane + 64 * k] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int k = 0; k < VPL; ++k) xv[i][k] = xr[min(lane + 64 * k, c4 - 1)];
     }
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
-        const bool in = g.norm && lane + 64 * k < c4;
-        nw[k] = in ? reinterpret_cast<const float4*>(g.g)[lane + 64 * k] : make_float4(0.f, 0.f, 0.f, 0.f);
-        nbv[k] = in && g.norm == LBR_NORM_LAYER ? reinterpret_cast<const float4*>(g.be)[lane + 64 * k]
-                                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int idx = min(lane + 64 * k, c4 - 1);
+        nw[k] = reinterpret_cast<const float4*>(g.g)[idx];
+        nbv[k] = reinterpret_cast<const float4*>(g.be)[idx];
     }
-    float4 f1[MLP_FR], f2[MLP_FR];
-    mlp_load_frags(g.w1, g.D, nb1 * (g.D / 16), f1);
-    mlp_load_frags(g.w2, g.H, nb2 * (g.H / 16), f2);
     float bias1[MLP_NBW], bias2[MLP_NBW], res[MLP_NBW][4];
 #pragma unroll
     for (int j = 0; j < MLP_NBW; ++j) {
         const int col = 16 * (wave + 4 * j) + lr;
-        bias1[j] = g.b1 && j < nb1 ? g.b1[col] : 0.f;
-        bias2[j] = g.b2 && j < nb2 ? g.b2[col] : 0.f;
+        // an absent bias or residual reads element 0 of x
+        bias1[j] = g.b1[(g.has & MLP_HAS_B1) ? min(col, g.H - 1) : 0];
+        bias2[j] = g.b2[(g.has & MLP_HAS_B2) ? min(col, g.D2 - 1) : 0];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const long long row = r0 + 4 * kq + r;
-            res[j][r] = g.r && j < nb2 && row < g.M ? g.r[row * g.D2 + col] : 0.f;
+            const long long row = min(r0 + 4 * kq + r, (long long)g.M - 1);
+            res[j][r] = g.r[(g.has & MLP_HAS_RESID) ? row * g.D2 + min(col, g.D2 - 1) : 0];
         }
     }
+    // the weights last: W1's MLP_DMA instructions, then W2's (their order fixes
+    // the vmcnt thresholds below)
+    __builtin_amdgcn_sched_barrier(0);
+    mlp_stage_weight(g.w1, g.w1s, w1l);
+    __builtin_amdgcn_sched_barrier(0);
+    mlp_stage_weight(g.w2, g.w2s, w2l);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < MLP_RB / 4; ++i) {
         if (r0 + wave + 4 * i < g.M) {
@@ -211,22 +268,28 @@ __global__ __launch_bounds__(MLP_NT) void mlp_rows(MlpArgs g) {
                 if (lane + 64 * k < g.D / 4) d4[lane + 64 * k] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
     }
+    // this wave's W1 DMAs have landed (at most W2's are still out), then every wave's
+    __builtin_amdgcn_s_waitcnt(lbr_waitcnt_vm(MLP_DMA));
     __syncthreads();
+    float4 f[MLP_FR];
+    mlp_read_frags(w1l, g.w1s, nb1 * (g.D / 16), f);
     // h = act(xs·W1ᵀ + b1): D[4·kq + r][lr] of block j is h[4·kq + r][16·(wave + 4j) + lr]
-    mlp_gemm(xs, ldx, g.D, nb1 * (g.D / 16), f1, [&](int j, const floatx4& acc) {
+    mlp_gemm(xs, ldx, g.D, nb1 * (g.D / 16), f, [&](int j, const floatx4& acc) {
         const int col = 16 * (wave + 4 * j) + lr;
         float bv = 0.f;
 #pragma unroll
         for (int t = 0; t < MLP_NBW; ++t) bv = t == j ? bias1[t] : bv;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float v = g.b1 ? acc[r] + bv : g.alpha1 * acc[r];
+            const float v = (g.has & MLP_HAS_B1) ? acc[r] + bv : g.alpha1 * acc[r];
             hs[(4 * kq + r) * ldh + col] = lbr_act(ACT, v);
         }
     });
+    __builtin_amdgcn_s_waitcnt(lbr_waitcnt_vm(0));   // W2's DMAs too
     __syncthreads();
+    mlp_read_frags(w2l, g.w2s, nb2 * (g.H / 16), f);
     // y = hs·W2ᵀ + b2 (+ R)
-    mlp_gemm(hs, ldh, g.H, nb2 * (g.H / 16), f2, [&](int j, const floatx4& acc) {
+    mlp_gemm(hs, ldh, g.H, nb2 * (g.H / 16), f, [&](int j, const floatx4& acc) {
         const int col = 16 * (wave + 4 * j) + lr;
         float bv = 0.f, rv[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -239,12 +302,25 @@ __global__ __launch_bounds__(MLP_NT) void mlp_rows(MlpArgs g) {
         for (int r = 0; r < 4; ++r) {
             const long long row = r0 + 4 * kq + r;
             if (row >= g.M) continue;
-            float v = g.b2 ? acc[r] + bv : g.alpha2 * acc[r];
-            if (g.r) v = v + rv[r];
+            float v = (g.has & MLP_HAS_B2) ? acc[r] + bv : g.alpha2 * acc[r];
+            if (g.has & MLP_HAS_RESID) v = v + rv[r];
             g.y[row * g.D2 + col] = v;
         }
     });
 }
+
+MlpWeight mlp_weight(int R, int K) {
+    MlpWeight w;
+    w.R = R;
+    w.K = K;
+    const int kc = K / 4;
+    w.mask = (kc & -kc) >= 16 ? 15 : (kc & -kc) - 1;
+    lbr_fast_divisor((unsigned)kc, &w.kc_m, &w.kc_s);
+    return w;
+}
+
+// Dynamic LDS (xs, hs); the two staged weights take 2·MLP_WMAX floats more.
+size_t mlp_lds_bytes(long long D, long long H) { return (size_t)(MLP_RB * (D + 4 + H + 4)) * sizeof(float); }
 
 // Step: in[0] x, in[1] W1, in[2] b1, in[3] W2, in[4] b2, in[5] R, in[6] norm
 // weight, in[7] LayerNorm bias; i[0] M, i[1] D, i[2] H, i[3] D2, i[4] act
@@ -272,8 +348,18 @@ void launch_mlp(const Step& s, hipStream_t st) {
     g.alpha2 = s.f[1];
     g.eps = s.f[2];
     if (g.M <= 0) return;
-    const size_t lds = (size_t)MLP_RB * (g.D + 4 + g.H + 4) * sizeof(float);
-    hipLaunchKernelGGL((mlp_rows<ACT, VPL>), dim3((unsigned)((g.M + MLP_RB - 1) / MLP_RB)), dim3(MLP_NT), lds, st, g);
+    // absent inputs: a flag, and x in place of the pointer (every lane loads from
+    // a valid address and the kernel discards the value)
+    g.has = (g.b1 ? MLP_HAS_B1 : 0) | (g.b2 ? MLP_HAS_B2 : 0) | (g.r ? MLP_HAS_RESID : 0);
+    if (!g.b1) g.b1 = g.x;
+    if (!g.b2) g.b2 = g.x;
+    if (!g.r) g.r = g.x;
+    if (!g.g) g.g = g.x;
+    if (!g.be) g.be = g.x;
+    g.w1s = mlp_weight(g.H, g.D);
+    g.w2s = mlp_weight(g.D2, g.H);
+    hipLaunchKernelGGL((mlp_rows<ACT, VPL>), dim3((unsigned)((g.M + MLP_RB - 1) / MLP_RB)), dim3(MLP_NT),
+                       mlp_lds_bytes(g.D, g.H), st, g);
 }
 
 }  // namespace
@@ -284,12 +370,25 @@ static long long mlp_frags(long long cols, long long K) { return (cols / 16 + 3)
 bool mlp_shape_ok(long long M, long long D, long long H, long long D2) {
     return M > 0 && D > 0 && H > 0 && D2 > 0 && D % 16 == 0 && H % 16 == 0 && D2 % 16 == 0 && D <= 1024 &&
            (H / 16 + 3) / 4 <= MLP_NBW && (D2 / 16 + 3) / 4 <= MLP_NBW && mlp_frags(H, D) <= MLP_FR &&
-           mlp_frags(D2, H) <= MLP_FR && (size_t)MLP_RB * (D + 4 + H + 4) * sizeof(float) <= MLP_LDS_MAX;
+           mlp_frags(D2, H) <= MLP_FR && H * D <= MLP_WMAX && D2 * H <= MLP_WMAX &&
+           mlp_lds_bytes(D, H) + 2 * MLP_WMAX * sizeof(float) <= MLP_LDS_MAX;
+}
+
+// The kernel's LDS (128 KB static + xs, hs) exceeds the default: the dynamic
+// limit is raised once per instantiation, at plan creation (outside any graph
+// capture).
+template <int ACT, int VPL>
+static step_fn mlp_prepared() {
+    static const bool raised =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&mlp_rows<ACT, VPL>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)(MLP_LDS_MAX - 2 * MLP_WMAX * sizeof(float))) == hipSuccess;
+    return raised ? launch_mlp<ACT, VPL> : nullptr;
 }
 
 template <int ACT>
 static step_fn mlp_launcher_act(long long D) {
-    return D <= 256 ? launch_mlp<ACT, 1> : D <= 512 ? launch_mlp<ACT, 2> : launch_mlp<ACT, 4>;
+    return D <= 256 ? mlp_prepared<ACT, 1>() : D <= 512 ? mlp_prepared<ACT, 2>() : mlp_prepared<ACT, 4>();
 }
 
 step_fn mlp_launcher(long long D, int act) {
