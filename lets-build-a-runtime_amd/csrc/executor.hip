@@ -414,6 +414,23 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
                     ++r;
                 }
             }
+            // an attention output projection whose output only feeds the MLP
+            // right after it runs inside the MLP's kernel
+            if (r < runs.size() && runs[r].first == i && runs[r].kind == LBR_FUSE_MLP &&
+                s.fuse_kind == LBR_FUSE_TRANSPOSE_GEMM) {
+                Step s2;
+                rc = lbr_fused_step(nodes, runs[r], &s2);
+                if (rc) {
+                    delete p;
+                    return rc;
+                }
+                s2.fuse_kind = runs[r].kind;
+                if (lbr_merge_proj_mlp(&s2, s)) {
+                    s = s2;
+                    i += runs[r].count;
+                    ++r;
+                }
+            }
             p->steps.push_back(s);
         } else {
             p->steps.push_back(decoded[i]);

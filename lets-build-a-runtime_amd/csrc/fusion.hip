@@ -1529,3 +1529,58 @@ bool lbr_merge_head_steps(Step* a, const Step& b) {
     return true;
 }
 
+// Joins the TRANSPOSE_GEMM step t (attention output projection, O in head
+// layout, with its bias and residual) into the MLP step u right after it
+// whose input x is t's output: the MLP kernel computes x itself (and still
+// writes it), which saves a launch.  Every workgroup reads all of O and only
+// its own rows of R0, x and R, so the written ranges (x, y) may meet R0, x and
+// R only at the same base (row for row) and never O or a weight.
+bool lbr_merge_proj_mlp(Step* u, const Step& t) {
+    if (t.fuse_kind != LBR_FUSE_TRANSPOSE_GEMM || u->fuse_kind != LBR_FUSE_MLP) return false;
+    if (getenv("LBR_PROJ_MLP") && strcmp(getenv("LBR_PROJ_MLP"), "0") == 0) return false;
+    if (t.node_index + t.n_nodes != u->node_index) return false;
+    const long long M = u->i[0], D = u->i[1], H = u->i[2], D2 = u->i[3], K0 = t.i[2];
+    const long long oH = t.i[35], oS = t.i[36], ohd = t.i[37];
+    if (t.i[10] > 1 || t.i[3] != 1 || t.i[0] != M || t.i[1] != D || u->in[0] != t.out || oH * ohd != K0 ||
+        oS <= 0 || M % oS != 0 || !mlp_proj_ok(D, H, K0, ohd))
+        return false;
+    auto rg = [](const void* p, long long bytes) { return Rng{(uintptr_t)p, (uintptr_t)p + (uintptr_t)bytes}; };
+    const Rng x = rg(t.out, M * D * 4), y = rg(u->out, M * D2 * 4);
+    std::vector<Rng> fixed{rg(t.in[0], M * K0 * 4), rg(t.in[1], D * K0 * 4), rg(u->in[1], H * D * 4),
+                           rg(u->in[3], D2 * H * 4)};
+    if (t.in[2]) fixed.push_back(rg(t.in[2], D * 4));
+    if (u->in[2]) fixed.push_back(rg(u->in[2], H * 4));
+    if (u->in[4]) fixed.push_back(rg(u->in[4], D2 * 4));
+    if (u->in[6]) fixed.push_back(rg(u->in[6], D * 4));
+    if (u->in[7]) fixed.push_back(rg(u->in[7], D * 4));
+    if (any_overlap(x, fixed) || any_overlap(y, fixed)) return false;
+    // row-for-row: the same base and the same row width, else no overlap
+    auto rows_ok = [&](const Rng& a, long long wa, const void* b, long long wb) {
+        const Rng rb = rg(b, M * wb * 4);
+        return a.lo == rb.lo ? wa == wb : !overlap(a, rb);
+    };
+    const bool res_x = u->in[5] == t.out;
+    if (res_x && D2 != D) return false;
+    if (t.in[3] && (!rows_ok(x, D, t.in[3], D) || !rows_ok(y, D2, t.in[3], D))) return false;
+    if (!rows_ok(y, D2, t.out, D)) return false;
+    if (u->in[5] && !res_x && (!rows_ok(x, D, u->in[5], D2) || !rows_ok(y, D2, u->in[5], D2))) return false;
+    const step_fn run = mlp_launcher(D, (int)u->i[4], true);
+    if (!run) return false;
+    u->run = run;
+    u->i[6] = 1;
+    u->i[7] = K0;
+    u->i[8] = oH;
+    u->i[9] = oS;
+    u->i[10] = ohd;
+    u->i[11] = (t.i[6] ? 1 : 0) | (t.in[3] ? 4 : 0) | (res_x ? 8 : 0);   // MLP_HAS_B1, MLP_HAS_RESID, MLP_RES_X
+    u->f[3] = t.f[0];
+    u->in[8] = t.in[0];
+    u->in[9] = t.in[1];
+    u->in[10] = t.i[6] ? t.in[2] : nullptr;
+    u->in[11] = t.in[3];
+    u->node_index = t.node_index;
+    u->n_nodes += t.n_nodes;
+    u->name = u->i[5] ? "mlp_rows+proj+norm" : "mlp_rows+proj";
+    return true;
+}
+

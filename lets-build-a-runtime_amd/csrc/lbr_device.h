@@ -289,7 +289,10 @@ int decode_attention(const OpNode* n, Step* s);
 // Fused MLP (mlp.hip): whether rows of width D, hidden H and output D2 fit
 // the one-kernel form; its launcher (Step layout in mlp.hip).
 bool mlp_shape_ok(long long M, long long D, long long H, long long D2);
-step_fn mlp_launcher(long long D, int act);
+step_fn mlp_launcher(long long D, int act, bool oproj = false);
+// Whether the MLP kernel can also compute its input rows x = O·Woᵀ (+ bo)
+// (+ R0) from O in head layout (head dim hd, K0 = O's row width).
+bool mlp_proj_ok(long long D, long long H, long long K0, long long hd);
 
 // Helpers over the node record (same meaning as csrc/executor.c:30-48).
 static inline long long node_total(const OpNode* n) {

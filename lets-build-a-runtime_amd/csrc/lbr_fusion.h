@@ -72,6 +72,11 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s);
 // reads; false leaves a unchanged.
 bool lbr_merge_head_steps(Step* a, const Step& b);
 
+// Joins the TRANSPOSE_GEMM step t (the run right before u's) into the MLP
+// step u when u's input is t's output: u's kernel then computes that input
+// (and still writes it); false leaves u unchanged.
+bool lbr_merge_proj_mlp(Step* u, const Step& t);
+
 // Byte range [*lo, *hi) input k of node nd reads (per op, from its shape and
 // extras); *hi = UINTPTR_MAX when the node does not fix it.
 void lbr_input_extent(const OpNode* nd, int k, unsigned long long* lo, unsigned long long* hi);

@@ -36,7 +36,9 @@ constexpr int MLP_DMA = 16;     // weight DMA instructions per wave per GEMM (â‰
 constexpr int MLP_WMAX = 4 * MLP_DMA * 256;   // floats of one staged weight (64 KB)
 constexpr int MLP_NBW = 4;      // column blocks per wave per GEMM (its biases, loaded up front)
 constexpr size_t MLP_LDS_MAX = 160 * 1024;  // gfx950's LDS per workgroup (the launcher raises the dynamic limit)
-constexpr int MLP_HAS_B1 = 1, MLP_HAS_B2 = 2, MLP_HAS_RESID = 4;
+constexpr int MLP_HAS_B1 = 1, MLP_HAS_B2 = 2, MLP_HAS_RESID = 4, MLP_RES_X = 8;
+constexpr int MLP_OC = 8;       // projection prologue: K0/16 chunks a lane holds (K0 â‰¤ 128)
+constexpr int MLP_OB = 2;       // projection prologue: column blocks per wave (D â‰¤ 128)
 
 // W [R, K] as staged in LDS (mlp_stage_weight): its shape, the chunk swizzle
 // mask and the divisor by K/4.
@@ -59,6 +61,15 @@ struct MlpArgs {
     int M, D, H, D2, act, norm;
     float alpha1, alpha2, eps;
     MlpWeight w1s, w2s;   // W1 [H, D] and W2 [D2, H] as staged in LDS
+    // projection prologue (OPROJ): x = OÂ·Woáµ€ (+ bo) (+ R0) computed here and
+    // written to x, O in head layout [B, oH, oS, ohd] (columns hÂ·ohd + d)
+    const float* oa;      // O
+    const float* ow;      // Wo [D, K0]
+    const float* ob;      // bo [D] (or x)
+    const float* orr;     // R0 [M, D] (or x)
+    float* ox;            // x, written
+    int K0, oH, oS, ohd, ohas;   // ohas: MLP_HAS_B1 (bo), MLP_HAS_RESID (R0), MLP_RES_X (r is x)
+    float oalpha;
 };
 
 // A weight W [R, K] (row-major) staged in LDS by direct-to-LDS DMA.  In LDS
@@ -196,7 +207,7 @@ __device__ __forceinline__ void mlp_norm_row(const MlpArgs& g, float4 (&v)[VPL],
 // normalised, so the kernel waits for one memory round trip.  The output is
 // written only after the workgroup has read all of its residual rows (the
 // residual may lie under the output, row for row).
-template <int ACT, int VPL>
+template <int ACT, int VPL, bool OPROJ>
 __global__ __launch_bounds__(MLP_NT) void mlp_rows(MlpArgs g) {
     // the staged weights in LDS variables of their own: the compiler then
     // knows the norm's and GEMM1's LDS stores do not touch what the weight
@@ -207,29 +218,62 @@ __global__ __launch_bounds__(MLP_NT) void mlp_rows(MlpArgs g) {
     const int ldx = g.D + 4, ldh = g.H + 4;
     float* xs = smem;
     float* hs = xs + MLP_RB * ldx;
+    float* xin = hs + MLP_RB * ldh;   // OPROJ: the projected rows x
     const long long r0 = (long long)blockIdx.x * MLP_RB;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lr = lane & 15, kq = lane >> 4;
     const int nb1 = g.H / 16 > wave ? (g.H / 16 - wave + 3) / 4 : 0;
     const int nb2 = g.D2 / 16 > wave ? (g.D2 / 16 - wave + 3) / 4 : 0;
-    // the wave's 4 rows and the norm's weight and bias first (needed first), then
-    // both weights' fragments, the biases and the residual; a lane past the row's
-    // D/4 float4s holds 0, as in norm_wave_rows, so the row sums see exactly the row
     // Every load issues unconditionally from a clamped address (the host
     // replaces an absent input by x and says so in g.has), so no branch hides
     // a load from the compiler's count: the norm waits only for the rows,
     // GEMM1 for W1's fragments.  Values loaded from outside the data are never
     // used: the norm counts only lanes inside the row, and the epilogues use
     // a bias or residual value only for a present input, a block of the wave
-    // and a row below M.
+    // and a row below M.  The rows come first (needed first), the weights' DMAs
+    // last.
     const int c4 = g.D / 4;
     float4 xv[MLP_RB / 4][VPL], nw[VPL], nbv[VPL];
+    // OPROJ: lane (kq, lr) holds O's row r0 + lr, columns 16c + 4kq .. +3 (one
+    // head's run of 4: ohd % 4 == 0), chunk-major Wo fragments of the wave's
+    // blocks wave, wave + 4 (f0[cÂ·MLP_OB + j]), the bias and R0 in the
+    // accumulator layout (rows 4kq + r, column 16Â·(wave + 4j) + lr)
+    float4 a0[OPROJ ? MLP_OC : 1], f0[OPROJ ? MLP_OC * MLP_OB : 1];
+    float bias0[MLP_OB], r0v[MLP_OB][4];
+    const int nch0 = g.K0 / 16;
+    const int nb0 = g.D / 16 > wave ? (g.D / 16 - wave + 3) / 4 : 0;
+    if constexpr (OPROJ) {
+        const int row = (int)min(r0 + lr, (long long)g.M - 1);
+        const int b = row / g.oS, sq = row - b * g.oS;
 #pragma unroll
-    for (int i = 0; i < MLP_RB / 4; ++i) {
-        const long long row = min(r0 + wave + 4 * i, (long long)g.M - 1);
-        const float4* xr = reinterpret_cast<const float4*>(g.x + row * g.D);
+        for (int c = 0; c < MLP_OC; ++c) {
+            const int k = 16 * min(c, nch0 - 1) + 4 * kq, h = k / g.ohd;
+            a0[c] = *reinterpret_cast<const float4*>(
+                g.oa + ((long long)(b * g.oH + h) * g.oS + sq) * g.ohd + (k - h * g.ohd));
 #pragma unroll
-        for (int k = 0; k < VPL; ++k) xv[i][k] = xr[min(lane + 64 * k, c4 - 1)];
+            for (int j = 0; j < MLP_OB; ++j) {
+                const int wr = min(16 * (wave + 4 * j) + lr, g.D - 1);
+                f0[c * MLP_OB + j] = *reinterpret_cast<const float4*>(g.ow + (long long)wr * g.K0 + k);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < MLP_OB; ++j) {
+            const int col = min(16 * (wave + 4 * j) + lr, g.D - 1);
+            bias0[j] = g.ob[(g.ohas & MLP_HAS_B1) ? col : 0];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const long long rr = min(r0 + 4 * kq + r, (long long)g.M - 1);
+                r0v[j][r] = g.orr[(g.ohas & MLP_HAS_RESID) ? rr * g.D + col : 0];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < MLP_RB / 4; ++i) {
+            const long long row = min(r0 + wave + 4 * i, (long long)g.M - 1);
+            const float4* xr = reinterpret_cast<const float4*>(g.x + row * g.D);
+#pragma unroll
+            for (int k = 0; k < VPL; ++k) xv[i][k] = xr[min(lane + 64 * k, c4 - 1)];
+        }
     }
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
@@ -247,7 +291,7 @@ __global__ __launch_bounds__(MLP_NT) void mlp_rows(MlpArgs g) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const long long row = min(r0 + 4 * kq + r, (long long)g.M - 1);
-            res[j][r] = g.r[(g.has & MLP_HAS_RESID) ? row * g.D2 + min(col, g.D2 - 1) : 0];
+            res[j][r] = g.r[(g.has & MLP_HAS_RESID) && !(g.ohas & MLP_RES_X) ? row * g.D2 + min(col, g.D2 - 1) : 0];
         }
     }
     // the weights last: W1's MLP_DMA instructions, then W2's (their order fixes
@@ -257,6 +301,49 @@ __global__ __launch_bounds__(MLP_NT) void mlp_rows(MlpArgs g) {
     __builtin_amdgcn_sched_barrier(0);
     mlp_stage_weight(g.w2, g.w2s, w2l);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (OPROJ) {
+        // x = OÂ·Woáµ€ (+ bo) (+ R0) in the transposed-A GEMM's order: 16-wide
+        // chunks in order, MFMA q over k = 16c + 4kq + q; bias, then residual
+        floatx4 acc0[MLP_OB];
+#pragma unroll
+        for (int j = 0; j < MLP_OB; ++j) acc0[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < MLP_OC; ++c) {
+            if (c < nch0) {
+#pragma unroll
+                for (int j = 0; j < MLP_OB; ++j) {
+                    if (j < nb0) {
+                        const float4 fb = f0[c * MLP_OB + j];
+                        acc0[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[c].x, fb.x, acc0[j], 0, 0, 0);
+                        acc0[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[c].y, fb.y, acc0[j], 0, 0, 0);
+                        acc0[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[c].z, fb.z, acc0[j], 0, 0, 0);
+                        acc0[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[c].w, fb.w, acc0[j], 0, 0, 0);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < MLP_OB; ++j) {
+            if (j >= nb0) continue;
+            const int col = 16 * (wave + 4 * j) + lr;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = (g.ohas & MLP_HAS_B1) ? acc0[j][r] + bias0[j] : g.oalpha * acc0[j][r];
+                if (g.ohas & MLP_HAS_RESID) v = v + r0v[j][r];
+                const long long row = r0 + 4 * kq + r;
+                xin[(4 * kq + r) * ldx + col] = v;
+                if (row < g.M) g.ox[row * g.D + col] = v;
+                if (g.ohas & MLP_RES_X) res[j][r] = v;   // the MLP's residual is x (D2 == D)
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < MLP_RB / 4; ++i) {
+            const float4* xr = reinterpret_cast<const float4*>(xin + (wave + 4 * i) * ldx);
+#pragma unroll
+            for (int k = 0; k < VPL; ++k) xv[i][k] = xr[min(lane + 64 * k, c4 - 1)];
+        }
+    }
 #pragma unroll
     for (int i = 0; i < MLP_RB / 4; ++i) {
         if (r0 + wave + 4 * i < g.M) {
@@ -319,14 +406,20 @@ MlpWeight mlp_weight(int R, int K) {
     return w;
 }
 
-// Dynamic LDS (xs, hs); the two staged weights take 2Â·MLP_WMAX floats more.
-size_t mlp_lds_bytes(long long D, long long H) { return (size_t)(MLP_RB * (D + 4 + H + 4)) * sizeof(float); }
+// Dynamic LDS (xs, hs, and with the projection prologue xin); the two
+// staged weights take 2Â·MLP_WMAX floats more.
+size_t mlp_lds_bytes(long long D, long long H, bool oproj) {
+    return (size_t)(MLP_RB * (D + 4 + H + 4 + (oproj ? D + 4 : 0))) * sizeof(float);
+}
 
 // Step: in[0] x, in[1] W1, in[2] b1, in[3] W2, in[4] b2, in[5] R, in[6] norm
 // weight, in[7] LayerNorm bias; i[0] M, i[1] D, i[2] H, i[3] D2, i[4] act
 // (LBR_ACT_*), i[5] norm (LBR_NORM_*, 0 none); f[0] alpha1, f[1] alpha2,
-// f[2] eps.
-template <int ACT, int VPL>
+// f[2] eps.  Projection prologue (lbr_merge_proj_mlp): i[6] = 1, i[7] K0,
+// i[8..10] O's heads, tokens per batch and head dim, i[11] MLP_HAS_B1 /
+// MLP_HAS_RESID / MLP_RES_X, f[3] alpha; in[8] O, in[9] Wo, in[10] bo,
+// in[11] R0 (x = in[0] is then written).
+template <int ACT, int VPL, bool OPROJ>
 void launch_mlp(const Step& s, hipStream_t st) {
     MlpArgs g;
     g.x = (const float*)s.in[0];
@@ -348,18 +441,38 @@ void launch_mlp(const Step& s, hipStream_t st) {
     g.alpha2 = s.f[1];
     g.eps = s.f[2];
     if (g.M <= 0) return;
-    // absent inputs: a flag, and x in place of the pointer (every lane loads from
-    // a valid address and the kernel discards the value)
+    // absent inputs: a flag, and a read-only input with at least D floats in
+    // place of the pointer (x, or Wo when x is written here): every lane loads
+    // from a valid address and the kernel discards the value
+    const float* stand_in = OPROJ ? (const float*)s.in[9] : g.x;
     g.has = (g.b1 ? MLP_HAS_B1 : 0) | (g.b2 ? MLP_HAS_B2 : 0) | (g.r ? MLP_HAS_RESID : 0);
-    if (!g.b1) g.b1 = g.x;
-    if (!g.b2) g.b2 = g.x;
-    if (!g.r) g.r = g.x;
-    if (!g.g) g.g = g.x;
-    if (!g.be) g.be = g.x;
+    g.ohas = OPROJ ? (int)s.i[11] : 0;
+    if (!g.b1) g.b1 = stand_in;
+    if (!g.b2) g.b2 = stand_in;
+    if (!g.r || (g.ohas & MLP_RES_X)) g.r = stand_in;   // MLP_RES_X: the residual comes from registers
+    if (!g.g) g.g = stand_in;
+    if (!g.be) g.be = stand_in;
     g.w1s = mlp_weight(g.H, g.D);
     g.w2s = mlp_weight(g.D2, g.H);
-    hipLaunchKernelGGL((mlp_rows<ACT, VPL>), dim3((unsigned)((g.M + MLP_RB - 1) / MLP_RB)), dim3(MLP_NT),
-                       mlp_lds_bytes(g.D, g.H), st, g);
+    g.oa = g.ow = g.ob = g.orr = stand_in;
+    g.ox = nullptr;
+    g.K0 = 16;
+    g.oH = g.oS = g.ohd = 1;
+    g.oalpha = 1.f;
+    if (OPROJ) {
+        g.K0 = (int)s.i[7];
+        g.oH = (int)s.i[8];
+        g.oS = (int)s.i[9];
+        g.ohd = (int)s.i[10];
+        g.oalpha = s.f[3];
+        g.oa = (const float*)s.in[8];
+        g.ow = (const float*)s.in[9];
+        g.ob = s.in[10] ? (const float*)s.in[10] : stand_in;
+        g.orr = s.in[11] ? (const float*)s.in[11] : stand_in;
+        g.ox = (float*)s.in[0];
+    }
+    hipLaunchKernelGGL((mlp_rows<ACT, VPL, OPROJ>), dim3((unsigned)((g.M + MLP_RB - 1) / MLP_RB)), dim3(MLP_NT),
+                       mlp_lds_bytes(g.D, g.H, OPROJ), st, g);
 }
 
 }  // namespace
@@ -371,30 +484,38 @@ bool mlp_shape_ok(long long M, long long D, long long H, long long D2) {
     return M > 0 && D > 0 && H > 0 && D2 > 0 && D % 16 == 0 && H % 16 == 0 && D2 % 16 == 0 && D <= 1024 &&
            (H / 16 + 3) / 4 <= MLP_NBW && (D2 / 16 + 3) / 4 <= MLP_NBW && mlp_frags(H, D) <= MLP_FR &&
            mlp_frags(D2, H) <= MLP_FR && H * D <= MLP_WMAX && D2 * H <= MLP_WMAX &&
-           mlp_lds_bytes(D, H) + 2 * MLP_WMAX * sizeof(float) <= MLP_LDS_MAX;
+           mlp_lds_bytes(D, H, false) + 2 * MLP_WMAX * sizeof(float) <= MLP_LDS_MAX;
 }
 
 // The kernel's LDS (128 KB static + xs, hs) exceeds the default: the dynamic
 // limit is raised once per instantiation, at plan creation (outside any graph
 // capture).
-template <int ACT, int VPL>
+template <int ACT, int VPL, bool OPROJ>
 static step_fn mlp_prepared() {
     static const bool raised =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&mlp_rows<ACT, VPL>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&mlp_rows<ACT, VPL, OPROJ>),
                             hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)(MLP_LDS_MAX - 2 * MLP_WMAX * sizeof(float))) == hipSuccess;
-    return raised ? launch_mlp<ACT, VPL> : nullptr;
+    return raised ? launch_mlp<ACT, VPL, OPROJ> : nullptr;
 }
 
+// D â‰¤ 256 always holds (each wave's W1 fragments, ceil(H/64)Â·D/16, are at
+// most 16), so the rows take one float4 a lane.
 template <int ACT>
-static step_fn mlp_launcher_act(long long D) {
-    return D <= 256 ? mlp_prepared<ACT, 1>() : D <= 512 ? mlp_prepared<ACT, 2>() : mlp_prepared<ACT, 4>();
+static step_fn mlp_launcher_act(bool oproj) {
+    return oproj ? mlp_prepared<ACT, 1, true>() : mlp_prepared<ACT, 1, false>();
 }
 
-step_fn mlp_launcher(long long D, int act) {
+step_fn mlp_launcher(long long D, int act, bool oproj) {
+    if (D > 256) return nullptr;
     switch (act) {
-        case LBR_ACT_RELU: return mlp_launcher_act<LBR_ACT_RELU>(D);
-        case LBR_ACT_GELU: return mlp_launcher_act<LBR_ACT_GELU>(D);
-        default: return mlp_launcher_act<LBR_ACT_SILU>(D);
+        case LBR_ACT_RELU: return mlp_launcher_act<LBR_ACT_RELU>(oproj);
+        case LBR_ACT_GELU: return mlp_launcher_act<LBR_ACT_GELU>(oproj);
+        default: return mlp_launcher_act<LBR_ACT_SILU>(oproj);
     }
+}
+
+bool mlp_proj_ok(long long D, long long H, long long K0, long long hd) {
+    return D <= 16 * 4 * MLP_OB && K0 % 16 == 0 && K0 / 16 <= MLP_OC && hd % 4 == 0 && K0 % hd == 0 &&
+           mlp_lds_bytes(D, H, true) + 2 * MLP_WMAX * sizeof(float) <= MLP_LDS_MAX;
 }
