@@ -441,6 +441,8 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
                     ++r;
                 }
             }
+            // a norm of this GEMM's split-K output runs in its reduce kernel
+            if (i < n_nodes && (r >= runs.size() || runs[r].first != i) && lbr_merge_reduce_norm(&s, decoded[i])) ++i;
             p->steps.push_back(s);
         } else {
             p->steps.push_back(decoded[i]);

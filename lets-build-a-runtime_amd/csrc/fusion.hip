@@ -1584,3 +1584,46 @@ bool lbr_merge_proj_mlp(Step* u, const Step& t) {
     return true;
 }
 
+// Joins the decoded RMSNORM / LAYERNORM step n right after the split-K GEMM
+// step g (one batch, float4 reduce, no head split, gated pair or activation)
+// whose output C it normalises over C's rows: g's reduce kernel then writes
+// the normalised rows too.  The reduce handles whole rows, one workgroup
+// (or wavefront) each, reading the partial sums, the bias and the residual
+// row and writing C's row and the norm's row; so the norm's output may
+// meet the residual only row for row and touch neither C, the bias nor the
+// norm's weights.
+bool lbr_merge_reduce_norm(Step* g, const Step& n) {
+    if (getenv("LBR_REDUCE_NORM") && strcmp(getenv("LBR_REDUCE_NORM"), "0") == 0) return false;
+    if (g->fuse_kind != LBR_FUSE_GEMM_RESID || !g->in[3] || g->i[10] <= 1 || g->i[3] != 1 || !g->i[12] ||
+        g->i[19] || g->i[32] || g->i[31] || g->i[16] || g->i[18] || !n.name)
+        return false;
+    const bool rms = strcmp(n.name, "rmsnorm") == 0;
+    if (!rms && strcmp(n.name, "layernorm") != 0) return false;
+    const long long M = g->i[0], N = g->i[1];
+    if (g->node_index + g->n_nodes != n.node_index || n.in[0] != g->out || n.i[0] != M || n.i[1] != N ||
+        (n.i[2] != 1 && n.i[2] != 2) || n.i[3] < 2 || n.i[3] > 4 || N % 4 || !lbr_aligned(g->out, 16) ||
+        (g->in[3] && !lbr_aligned(g->in[3], 16)))   // 2 to 4 float4 a lane: rows of 257 to 4096 columns
+        return false;
+    auto rg = [](const void* q, long long bytes) { return Rng{(uintptr_t)q, (uintptr_t)q + (uintptr_t)bytes}; };
+    const Rng y = rg(n.out, M * N * 4);
+    std::vector<Rng> fixed{rg(g->out, M * N * 4), rg(n.in[1], N * 4)};
+    if (n.in[2]) fixed.push_back(rg(n.in[2], N * 4));
+    if (g->i[6]) fixed.push_back(rg(g->in[2], N * 4));
+    if (any_overlap(y, fixed)) return false;
+    if (g->in[3]) {
+        const Rng r = rg(g->in[3], M * N * 4);
+        if (overlap(y, r) && y.lo != r.lo) return false;
+    }
+    g->i[16] = rms ? LBR_NORM_RMS : LBR_NORM_LAYER;
+    g->i[17] = n.i[2] * 16 + n.i[3];
+    g->in[4] = n.out;
+    g->in[5] = n.in[1];
+    g->in[6] = n.in[2];
+    g->f[2] = n.f[0];
+    g->n_nodes += 1;
+    const bool dma = g->i[14] != 0;
+    g->name = dma ? (rms ? "gemm_dma_f32_nt+resid+rmsnorm" : "gemm_dma_f32_nt+resid+layernorm")
+                  : (rms ? "gemm_mfma_f32+resid+rmsnorm" : "gemm_mfma_f32+resid+layernorm");
+    return true;
+}
+

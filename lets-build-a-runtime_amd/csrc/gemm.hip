@@ -75,6 +75,13 @@ struct GemmArgs {
     const float* nw;
     const float* nb;
     float neps;
+    // Norm after the split-K reduce (lbr_merge_reduce_norm): the reduce, one row
+    // at a time, also normalises C's row into nt_out (RMSNORM / LAYERNORM over
+    // the N columns, weight nt_w, LayerNorm bias nt_b)
+    float* nt_out;
+    const float* nt_w;
+    const float* nt_b;
+    float nt_eps;
 };
 
 // Final store of one C element (row m, column n of batch bz) with the fused
@@ -894,6 +901,14 @@ GemmArgs make_args(const Step& s) {
     g.nw = (const float*)(uintptr_t)s.i[38];
     g.nb = (const float*)(uintptr_t)s.i[39];
     g.neps = s.f[1];
+    // i[16] = norm after the split-K reduce (LBR_NORM_*), i[17] = its form
+    // (16·(1 wave / 2 block per row) + float4 per lane); in[4] output, in[5]
+    // weight, in[6] LayerNorm bias, f[2] eps (the head-split fields are unused
+    // then: i[19] = 0)
+    g.nt_out = s.i[16] ? (float*)s.in[4] : nullptr;
+    g.nt_w = s.i[16] ? (const float*)s.in[5] : nullptr;
+    g.nt_b = s.i[16] ? (const float*)s.in[6] : nullptr;
+    g.nt_eps = s.f[2];
     return g;
 }
 
@@ -902,6 +917,7 @@ GemmArgs make_args(const Step& s) {
 // epilogue, if any (VEC only with no head scatter).
 template <bool HAS_BIAS, bool VEC>
 __global__ void splitk_reduce(GemmArgs g, long long total) {
+#pragma clang fp contract(off)   // the same roundings as splitk_reduce_norm (no a·alpha + r fused)
     const float* __restrict__ W = g.W;
     const int N = g.N, ksplit = g.ksplit;
     if (VEC) {
@@ -942,8 +958,104 @@ __global__ void splitk_reduce(GemmArgs g, long long total) {
     }
 }
 
+// The split-K reduce of a one-batch GEMM whose output row feeds a norm: one
+// wavefront (WAVE, N ≤ 1024) or one 256-thread workgroup per row sums the K
+// ranges, adds the bias (or scales by alpha) and the residual exactly as
+// splitk_reduce does, writes C's row, and normalises it into nt_out with the
+// norm kernels' own per-lane layout and sums (lbr_norm_row_wave / _block), so
+// both outputs equal the unfused reduce + norm bit for bit.
+template <bool HAS_BIAS, bool RMS, int VPL, bool WAVE>
+__global__ __launch_bounds__(256) void splitk_reduce_norm(GemmArgs g) {
+#pragma clang fp contract(off)
+    __shared__ float red[4];
+    constexpr int STRIDE = WAVE ? 64 : 256;
+    const int N = g.N, c4 = N / 4;
+    const long long total = (long long)g.M * N;
+    const long long row = WAVE ? (long long)blockIdx.x * 4 + (threadIdx.x >> 6) : (long long)blockIdx.x;
+    if (row >= g.M) return;   // whole wavefronts (WAVE) or the whole workgroup leave
+    const int t = WAVE ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
+    const float4* __restrict__ W4 = reinterpret_cast<const float4*>(g.W);
+    const float4* __restrict__ w4 = reinterpret_cast<const float4*>(g.nt_w);
+    const float4* __restrict__ b4 = reinterpret_cast<const float4*>(g.nt_b);
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+    const long long t4 = total / 4;
+    // every load of the row's slots issues before the sums: the weight, bias and
+    // residual, then the partials CH ranges at a time (clamped indices, so no
+    // branch hides a load; values past the row or past ksplit are never added)
+    constexpr int CH = 4;
+    float4 v[VPL], wv[VPL], bv[VPL], bias[VPL], res[VPL];
+    long long i4[VPL];
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        const int idx = t + k * STRIDE;
+        const int ic = min(idx, c4 - 1);
+        i4[k] = row * c4 + ic;
+        wv[k] = w4[ic];
+        bv[k] = RMS ? zero : b4[ic];
+        bias[k] = HAS_BIAS ? reinterpret_cast<const float4*>(g.bias)[ic] : zero;
+        res[k] = g.resid ? reinterpret_cast<const float4*>(g.resid)[i4[k]] : zero;
+    }
+    for (int k0 = 0; k0 < g.ksplit; k0 += CH) {
+        float4 w[VPL][CH];
+#pragma unroll
+        for (int k = 0; k < VPL; ++k)
+#pragma unroll
+            for (int q = 0; q < CH; ++q) w[k][q] = W4[min(k0 + q, g.ksplit - 1) * t4 + i4[k]];
+#pragma unroll
+        for (int k = 0; k < VPL; ++k)
+#pragma unroll
+            for (int q = 0; q < CH; ++q) {
+                if (k0 + q >= g.ksplit) continue;
+                if (k0 + q == 0) {
+                    v[k] = w[k][q];
+                } else {
+                    v[k].x += w[k][q].x; v[k].y += w[k][q].y; v[k].z += w[k][q].z; v[k].w += w[k][q].w;
+                }
+            }
+    }
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        float4 s = v[k];
+        if (HAS_BIAS) {
+            s.x += bias[k].x; s.y += bias[k].y; s.z += bias[k].z; s.w += bias[k].w;
+        } else {
+            s.x *= g.alpha; s.y *= g.alpha; s.z *= g.alpha; s.w *= g.alpha;
+        }
+        if (g.resid) {
+            s.x = s.x + res[k].x; s.y = s.y + res[k].y; s.z = s.z + res[k].z; s.w = s.w + res[k].w;
+        }
+        const bool in = t + k * STRIDE < c4;
+        if (in) reinterpret_cast<float4*>(g.C)[i4[k]] = s;
+        v[k] = in ? s : zero;
+        if (!in) wv[k] = bv[k] = zero;
+    }
+    float4* o4 = reinterpret_cast<float4*>(g.nt_out + row * N);
+    if constexpr (WAVE) lbr_norm_row_wave<RMS, VPL>(v, wv, bv, o4, c4, N, g.nt_eps);
+    else lbr_norm_row_block<RMS, VPL>(v, wv, bv, o4, c4, N, g.nt_eps, red);
+}
+
+template <bool HAS_BIAS, bool RMS>
+void launch_splitk_reduce_norm(const Step& s, const GemmArgs& g, hipStream_t st) {
+    const int form = (int)s.i[17] >> 4, vpl = (int)s.i[17] & 15;
+    if (form == 1) {
+        const dim3 grid((unsigned)((g.M + 3) / 4));
+        // lbr_merge_reduce_norm takes rows of more than 256 columns (2 or 4 float4 a lane)
+        if (vpl == 2) hipLaunchKernelGGL((splitk_reduce_norm<HAS_BIAS, RMS, 2, true>), grid, dim3(256), 0, st, g);
+        else hipLaunchKernelGGL((splitk_reduce_norm<HAS_BIAS, RMS, 4, true>), grid, dim3(256), 0, st, g);
+    } else {
+        const dim3 grid((unsigned)g.M);   // lbr_merge_reduce_norm takes rows of at most 4096 columns
+        if (vpl == 2) hipLaunchKernelGGL((splitk_reduce_norm<HAS_BIAS, RMS, 2, false>), grid, dim3(256), 0, st, g);
+        else hipLaunchKernelGGL((splitk_reduce_norm<HAS_BIAS, RMS, 4, false>), grid, dim3(256), 0, st, g);
+    }
+}
+
 template <bool HAS_BIAS>
 void launch_splitk_reduce(const Step& s, const GemmArgs& g, hipStream_t st) {
+    if (s.i[16]) {
+        if (s.i[16] == LBR_NORM_RMS) launch_splitk_reduce_norm<HAS_BIAS, true>(s, g, st);
+        else launch_splitk_reduce_norm<HAS_BIAS, false>(s, g, st);
+        return;
+    }
     const long long total = (long long)g.M * g.N * s.i[3];
     const bool v4 = s.i[12] != 0 && g.n_split == 0 && (!g.resid || lbr_aligned(g.resid, 16));
     const unsigned blocks = lbr_grid(v4 ? total / 4 : total, 256, 4096);

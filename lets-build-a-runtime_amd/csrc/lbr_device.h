@@ -192,6 +192,88 @@ __device__ __forceinline__ float block_max(float v, float* red) {
     return t;
 }
 
+// Row norms, shared by the norm kernels and the split-K reduce that ends in a
+// norm (so the two give the same bits).  The row is held as float4s, lane /
+// thread t holding float4 idx = t + stride·k for k < VPL (0 past the row's
+// c4 = cols/4 float4s); wv / bv are the weight (γ) and LayerNorm bias (β) at
+// the same positions.  RMSNorm follows csrc/ops/norm.c:100-107 (x · 1/√(Σx²/n
+// + eps) · w), LayerNorm norm.c:47-64 (two passes, centred variance).
+// Wave form: one wavefront per row (stride 64, wave_sum).
+template <bool RMS, int VPL>
+__device__ __forceinline__ void lbr_norm_row_wave(float4 (&v)[VPL], const float4 (&wv)[VPL],
+                                                  const float4 (&bv)[VPL], float4* __restrict__ o4, int c4,
+                                                  int cols, float eps) {
+    const int lane = threadIdx.x & 63;
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) s += RMS ? lbr_sumsq4(v[k]) : lbr_sum4(v[k]);
+    s = wave_sum(s);
+    if (RMS) {
+        const float scale = 1.0f / sqrtf(s / cols + eps);
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) {
+            const int idx = lane + k * 64;
+            if (idx < c4) o4[idx] = lbr_norm_scale(v[k], scale, wv[k]);
+        }
+        return;
+    }
+    const float mean = s / cols;
+    float var = 0.f;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        const int idx = lane + k * 64;
+        if (idx < c4) {
+            v[k].x -= mean; v[k].y -= mean; v[k].z -= mean; v[k].w -= mean;
+            var += lbr_sumsq4(v[k]);
+        }
+    }
+    var = wave_sum(var);
+    const float inv_std = 1.0f / sqrtf(var / cols + eps);
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        const int idx = lane + k * 64;
+        if (idx < c4) o4[idx] = lbr_norm_affine(v[k], inv_std, wv[k], bv[k]);
+    }
+}
+
+// Block form: one 256-thread workgroup per row (stride 256, block_sum through
+// red[4]).
+template <bool RMS, int VPL>
+__device__ __forceinline__ void lbr_norm_row_block(float4 (&v)[VPL], const float4 (&wv)[VPL],
+                                                   const float4 (&bv)[VPL], float4* __restrict__ o4, int c4,
+                                                   int cols, float eps, float* red) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) s += RMS ? lbr_sumsq4(v[k]) : lbr_sum4(v[k]);
+    s = block_sum(s, red);
+    if (RMS) {
+        const float scale = 1.0f / sqrtf(s / cols + eps);
+#pragma unroll
+        for (int k = 0; k < VPL; ++k) {
+            const int idx = threadIdx.x + k * 256;
+            if (idx < c4) o4[idx] = lbr_norm_scale(v[k], scale, wv[k]);
+        }
+        return;
+    }
+    const float mean = s / cols;
+    float var = 0.f;
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        const int idx = threadIdx.x + k * 256;
+        if (idx < c4) {
+            v[k].x -= mean; v[k].y -= mean; v[k].z -= mean; v[k].w -= mean;
+            var += lbr_sumsq4(v[k]);
+        }
+    }
+    var = block_sum(var, red);
+    const float inv_std = 1.0f / sqrtf(var / cols + eps);
+#pragma unroll
+    for (int k = 0; k < VPL; ++k) {
+        const int idx = threadIdx.x + k * 256;
+        if (idx < c4) o4[idx] = lbr_norm_affine(v[k], inv_std, wv[k], bv[k]);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Decoded launch record
 // ---------------------------------------------------------------------------

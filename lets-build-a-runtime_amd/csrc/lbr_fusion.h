@@ -77,6 +77,11 @@ bool lbr_merge_head_steps(Step* a, const Step& b);
 // (and still writes it); false leaves u unchanged.
 bool lbr_merge_proj_mlp(Step* u, const Step& t);
 
+// Joins the decoded RMSNORM / LAYERNORM step n right after the split-K
+// residual GEMM step g that produces its input: g's reduce kernel then also
+// writes the normalised rows; false leaves g unchanged.
+bool lbr_merge_reduce_norm(Step* g, const Step& n);
+
 // Byte range [*lo, *hi) input k of node nd reads (per op, from its shape and
 // extras); *hi = UINTPTR_MAX when the node does not fix it.
 void lbr_input_extent(const OpNode* nd, int k, unsigned long long* lo, unsigned long long* hi);

@@ -36,46 +36,16 @@ __global__ __launch_bounds__(NB) void norm_wave_rows(const float* __restrict__ x
     const float4* g4 = reinterpret_cast<const float4*>(g);
     const float4* b4 = reinterpret_cast<const float4*>(b);
     // row, weight and (LayerNorm) bias loads all issue before the reduction
-    float4 v[VPL], wv[VPL], bv[RMS ? 1 : VPL];
+    float4 v[VPL], wv[VPL], bv[VPL];
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
         const int idx = lane + k * 64;
         const bool in = idx < c4;
         v[k] = in ? xr[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
         wv[k] = in ? g4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (!RMS) bv[k] = in ? b4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+        bv[k] = in && !RMS ? b4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    float s = 0.f;
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) s += RMS ? lbr_sumsq4(v[k]) : lbr_sum4(v[k]);
-    s = wave_sum(s);
-    float4* o4 = reinterpret_cast<float4*>(out + row * cols);
-    if (RMS) {
-        const float scale = 1.0f / sqrtf(s / cols + eps);
-#pragma unroll
-        for (int k = 0; k < VPL; ++k) {
-            const int idx = lane + k * 64;
-            if (idx < c4) o4[idx] = lbr_norm_scale(v[k], scale, wv[k]);
-        }
-    } else {
-        const float mean = s / cols;
-        float var = 0.f;
-#pragma unroll
-        for (int k = 0; k < VPL; ++k) {
-            const int idx = lane + k * 64;
-            if (idx < c4) {
-                v[k].x -= mean; v[k].y -= mean; v[k].z -= mean; v[k].w -= mean;
-                var += lbr_sumsq4(v[k]);
-            }
-        }
-        var = wave_sum(var);
-        const float inv_std = 1.0f / sqrtf(var / cols + eps);
-#pragma unroll
-        for (int k = 0; k < VPL; ++k) {
-            const int idx = lane + k * 64;
-            if (idx < c4) o4[idx] = lbr_norm_affine(v[k], inv_std, wv[k], bv[k]);
-        }
-    }
+    lbr_norm_row_wave<RMS, VPL>(v, wv, bv, reinterpret_cast<float4*>(out + row * cols), c4, cols, eps);
 }
 
 // One block per row, float4 path, cols <= NB * 4 * VPL.
@@ -91,65 +61,16 @@ __global__ __launch_bounds__(NB) void norm_block_rows(const float* __restrict__ 
     const float4* b4 = reinterpret_cast<const float4*>(b);
     // the row, the weight and (LayerNorm) the bias are all loaded before the
     // first reduction, so their latencies overlap
-    float4 v[VPL], wv[VPL], bv[RMS ? 1 : VPL];
+    float4 v[VPL], wv[VPL], bv[VPL];
 #pragma unroll
     for (int k = 0; k < VPL; ++k) {
         const int idx = threadIdx.x + k * NB;
         const bool in = idx < c4;
         v[k] = in ? xr[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
         wv[k] = in ? g4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (!RMS) bv[k] = in ? b4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+        bv[k] = in && !RMS ? b4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    float s = 0.f;
-#pragma unroll
-    for (int k = 0; k < VPL; ++k) {
-        if (!RMS) s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
-        else s += (v[k].x * v[k].x + v[k].y * v[k].y) + (v[k].z * v[k].z + v[k].w * v[k].w);
-    }
-    s = block_sum(s, red);
-    float4* o4 = reinterpret_cast<float4*>(out + row * cols);
-    if (RMS) {
-        const float scale = 1.0f / sqrtf(s / cols + eps);
-#pragma unroll
-        for (int k = 0; k < VPL; ++k) {
-            const int idx = threadIdx.x + k * NB;
-            if (idx < c4) {
-                const float4 w = wv[k];
-                float4 r;
-                r.x = v[k].x * scale * w.x;
-                r.y = v[k].y * scale * w.y;
-                r.z = v[k].z * scale * w.z;
-                r.w = v[k].w * scale * w.w;
-                o4[idx] = r;
-            }
-        }
-    } else {
-        const float mean = s / cols;
-        float var = 0.f;
-#pragma unroll
-        for (int k = 0; k < VPL; ++k) {
-            const int idx = threadIdx.x + k * NB;
-            if (idx < c4) {
-                v[k].x -= mean; v[k].y -= mean; v[k].z -= mean; v[k].w -= mean;
-                var += (v[k].x * v[k].x + v[k].y * v[k].y) + (v[k].z * v[k].z + v[k].w * v[k].w);
-            }
-        }
-        var = block_sum(var, red);
-        const float inv_std = 1.0f / sqrtf(var / cols + eps);
-#pragma unroll
-        for (int k = 0; k < VPL; ++k) {
-            const int idx = threadIdx.x + k * NB;
-            if (idx < c4) {
-                const float4 w = wv[k], bb = bv[k];
-                float4 r;
-                r.x = v[k].x * inv_std * w.x + bb.x;
-                r.y = v[k].y * inv_std * w.y + bb.y;
-                r.z = v[k].z * inv_std * w.z + bb.z;
-                r.w = v[k].w * inv_std * w.w + bb.w;
-                o4[idx] = r;
-            }
-        }
-    }
+    lbr_norm_row_block<RMS, VPL>(v, wv, bv, reinterpret_cast<float4*>(out + row * cols), c4, cols, eps, red);
 }
 
 // Generic: one block per row, scalar loads, any cols / alignment.  The row is

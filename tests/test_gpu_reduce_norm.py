@@ -1,0 +1,104 @@
+"""Split-K GEMM + residual ADD → RMSNORM / LAYERNORM with the norm inside the
+split-K reduce kernel (one row per wavefront up to 1024 columns, one row per
+workgroup above): the reduce writes the residual sum C and the normalised rows.
+It uses the norm kernels' own per-lane layout and sums, so both outputs equal
+the plan with the norm kernel apart bit for bit; against the CPU oracle and a
+float64 closed form, 1e-4 normwise.
+"""
+
+import numpy as np
+import pytest
+
+from conftest import normwise_rel
+from helpers import cf_layernorm, cf_rmsnorm, randn, rng, run_oracle
+from runtime.ir import Graph, OpType
+
+pytestmark = pytest.mark.gpu
+
+
+def _graph(r, M, N, K, norm, bias):
+    g = Graph()
+    a, x = randn(r, 1, M, K), randn(r, 1, M, N)
+    for name, arr in (("a", a), ("x", x)):
+        g.add_tensor(name, arr.shape)
+        g.inputs.append(name)
+
+    def const(name, arr):
+        g.add_tensor(name, arr.shape).buffer = arr
+        g.constants.append(name)
+
+    w = randn(r, N, K, scale=0.05)
+    const("w", w)
+    c = a.astype(np.float64) @ w.T.astype(np.float64)
+    g.add_tensor("c", (1, M, N))
+    if bias:
+        b = randn(r, N)
+        const("b", b)
+        g.add_node(OpType.MATMUL_ADD, ["a", "w", "b"], "c", {"transpose_b": True})
+        c = c + b
+    else:
+        g.add_node(OpType.MATMUL, ["a", "w"], "c", {"transpose_b": True})
+    g.add_tensor("h", (1, M, N))
+    g.add_node(OpType.ADD, ["x", "c"], "h", {})
+    h = c + x
+    gam = (1.0 + 0.5 * randn(r, N)).astype(np.float32)
+    const("gam", gam)
+    g.add_tensor("n", (1, M, N))
+    if norm == "rms":
+        g.add_node(OpType.RMSNORM, ["h", "gam"], "n", {"eps": 1e-6})
+        n = cf_rmsnorm(h, gam, 1e-6)
+    else:
+        bet = randn(r, N)
+        const("bet", bet)
+        g.add_node(OpType.LAYERNORM, ["h", "gam", "bet"], "n", {"eps": 1e-5})
+        n = cf_layernorm(h, gam, bet, 1e-5)
+    g.outputs += ["h", "n"]
+    return g, {"a": a, "x": x}, h, n
+
+
+def _run(graph, inputs):
+    from runtime.executor.compiled import CompiledExecutor
+    from runtime.planner import plan
+    ex = CompiledExecutor(fuse=True)
+    ex.compile(plan(graph))
+    try:
+        out = ex.run(inputs)
+        return out["h"], out["n"], [p["name"] for p in ex.step_params()]
+    finally:
+        ex.close()
+
+
+@pytest.mark.parametrize("norm", ["rms", "layer"])
+@pytest.mark.parametrize("bias", [False, True])
+@pytest.mark.parametrize("M,N,K", [(64, 768, 1536), (40, 1000, 1024), (96, 2560, 2048), (33, 4096, 1024),
+                                   (16, 2000, 768)])
+def test_reduce_norm(monkeypatch, norm, bias, M, N, K):
+    monkeypatch.setenv("LBR_GEMM_KSPLIT", "3")
+    g, ins, h64, n64 = _graph(rng(M + N + K), M, N, K, norm, bias)
+    h, n, names = _run(g, ins)
+    monkeypatch.setenv("LBR_REDUCE_NORM", "0")
+    h2, n2, names2 = _run(g, ins)
+    print(names, names2)
+    assert any(nm.endswith("+rmsnorm" if norm == "rms" else "+layernorm") for nm in names), names
+    assert not any(nm in ("rmsnorm", "layernorm") for nm in names), names
+    assert any(nm in ("rmsnorm", "layernorm") for nm in names2), names2
+    np.testing.assert_array_equal(h, h2)
+    np.testing.assert_array_equal(n, n2)
+    from oracle.host_exec import OracleRun
+    from runtime.planner import plan
+    o = OracleRun(plan(g)).run(ins)
+    for got, ref, name in ((h, h64, "h"), (n, n64, "n")):
+        assert normwise_rel(got, ref) <= 1e-4, name
+        assert normwise_rel(o[name], ref) <= 1e-4, name
+        assert normwise_rel(got, o[name]) <= 1e-4, name
+
+
+@pytest.mark.parametrize("N", [6000, 256])
+def test_reduce_norm_other_widths_stay_apart(monkeypatch, N):
+    """Rows above 4096 or of at most 256 columns keep the norm kernel."""
+    monkeypatch.setenv("LBR_GEMM_KSPLIT", "3")
+    g, ins, h64, n64 = _graph(rng(9), 16, N, 768, "rms", False)
+    h, n, names = _run(g, ins)
+    assert "rmsnorm" in names, names
+    assert normwise_rel(h, h64) <= 1e-4 and normwise_rel(n, n64) <= 1e-4
+
