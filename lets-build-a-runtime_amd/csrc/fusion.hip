@@ -1594,8 +1594,15 @@ bool lbr_merge_proj_mlp(Step* u, const Step& t) {
 // norm's weights.
 bool lbr_merge_reduce_norm(Step* g, const Step& n) {
     if (getenv("LBR_REDUCE_NORM") && strcmp(getenv("LBR_REDUCE_NORM"), "0") == 0) return false;
-    if (g->fuse_kind != LBR_FUSE_GEMM_RESID || !g->in[3] || g->i[10] <= 1 || g->i[3] != 1 || !g->i[12] ||
-        g->i[19] || g->i[32] || g->i[31] || g->i[16] || g->i[18] || !n.name)
+    // an unsplit GEMM of at most 2^32 flops takes two K ranges to carry the norm
+    // (GPT-2's attention projection + LayerNorm: 21.4 + 7.4 → 23.9 µs); the K sum
+    // is then split in two, other roundings than the unsplit GEMM's.
+    // LBR_REDUCE_NORM_SPLIT=0 keeps such GEMMs unsplit and their norms apart.
+    const char* sp = getenv("LBR_REDUCE_NORM_SPLIT");
+    const bool split2 = !(sp && strcmp(sp, "0") == 0) && g->i[10] <= 1 &&
+                        2.0 * g->i[0] * g->i[1] * g->i[2] <= 4294967296.0;
+    if (g->fuse_kind != LBR_FUSE_GEMM_RESID || !g->in[3] || (g->i[10] <= 1 && !split2) || g->i[3] != 1 ||
+        !g->i[12] || g->i[19] || g->i[32] || g->i[31] || g->i[16] || g->i[18] || !n.name)
         return false;
     const bool rms = strcmp(n.name, "rmsnorm") == 0;
     if (!rms && strcmp(n.name, "layernorm") != 0) return false;
@@ -1614,8 +1621,10 @@ bool lbr_merge_reduce_norm(Step* g, const Step& n) {
         const Rng r = rg(g->in[3], M * N * 4);
         if (overlap(y, r) && y.lo != r.lo) return false;
     }
+    const bool forced = g->i[10] <= 1;
+    if (forced && !gemm_dma_split2(g)) return false;
     g->i[16] = rms ? LBR_NORM_RMS : LBR_NORM_LAYER;
-    g->i[17] = n.i[2] * 16 + n.i[3];
+    g->i[17] = n.i[2] * 16 + n.i[3] + (forced ? 256 : 0);   // 256: the split was made for the norm
     g->in[4] = n.out;
     g->in[5] = n.in[1];
     g->in[6] = n.in[2];

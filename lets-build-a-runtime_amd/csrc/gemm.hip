@@ -902,7 +902,8 @@ GemmArgs make_args(const Step& s) {
     g.nb = (const float*)(uintptr_t)s.i[39];
     g.neps = s.f[1];
     // i[16] = norm after the split-K reduce (LBR_NORM_*), i[17] = its form
-    // (16·(1 wave / 2 block per row) + float4 per lane); in[4] output, in[5]
+    // (16·(1 wave / 2 block per row) + float4 per lane, + 256 when the K split
+    // was made for the norm); in[4] output, in[5]
     // weight, in[6] LayerNorm bias, f[2] eps (the head-split fields are unused
     // then: i[19] = 0)
     g.nt_out = s.i[16] ? (float*)s.in[4] : nullptr;
@@ -1036,7 +1037,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_norm(GemmArgs g) {
 
 template <bool HAS_BIAS, bool RMS>
 void launch_splitk_reduce_norm(const Step& s, const GemmArgs& g, hipStream_t st) {
-    const int form = (int)s.i[17] >> 4, vpl = (int)s.i[17] & 15;
+    const int form = ((int)s.i[17] >> 4) & 15, vpl = (int)s.i[17] & 15;
     if (form == 1) {
         const dim3 grid((unsigned)((g.M + 3) / 4));
         // lbr_merge_reduce_norm takes rows of more than 256 columns (2 or 4 float4 a lane)
@@ -1273,6 +1274,21 @@ static step_fn dma_family_launcher(const Step& s, int tile) {
     if (s.i[15]) return gemm_dma_norm_launcher(tile, bias, (int)s.i[15]);
     if (s.i[35]) return gemm_dma_heads_launcher(tile, bias);
     return bias ? dma_launcher<true>(tile) : dma_launcher<false>(tile);
+}
+
+// Two K ranges for an unsplit one-batch DMA GEMM step (K ≥ 512, ranges a
+// multiple of the 32-wide K step): its reduce kernel can then take a norm of
+// its output.  False leaves the step unchanged.
+bool gemm_dma_split2(Step* s) {
+    const long long M = s->i[0], N = s->i[1], K = s->i[2];
+    if (!s->i[14] || s->i[10] > 1 || s->i[3] != 1 || K < 512 || s->i[19] || s->i[32] || s->i[15] || s->i[18])
+        return false;
+    const long long chunk = (K / 2 + DBK - 1) / DBK * DBK;
+    if ((K + chunk - 1) / chunk != 2) return false;
+    s->i[10] = 2;
+    s->i[11] = chunk;
+    s->ws_bytes = (size_t)2 * M * N * sizeof(float);
+    return true;
 }
 
 bool gemm_dma_tile_pairs(int tile) {

@@ -365,6 +365,9 @@ step_fn gemm_dma_norm_launcher(int tile, bool has_bias, int norm);
 int gemm_dma_tune_candidates(const Step& s, int* tiles, int cap);
 // Whether a DMA tile (Step::i[14] − 1) holds gated pairs (GEMM_GATED fusion).
 bool gemm_dma_tile_pairs(int tile);
+// Two K ranges for an unsplit one-batch DMA GEMM (its reduce can then take a
+// norm); false leaves the step unchanged.
+bool gemm_dma_split2(Step* s);
 bool gemm_dma_retile(Step* s, int tile);
 int gemm_dma_written(const Step& s, void** ptr, size_t* bytes, int cap);
 int decode_attention(const OpNode* n, Step* s);

@@ -266,7 +266,8 @@ class CompiledExecutor(Executor):
         """Every kernel step of the compiled plan: its kernel (and full step name, with the
         fused parts), the nodes it covers, and the schedule its launch arguments encode
         (attention: causal fold, key-range split workgroups, deferred output; GEMM: DMA tile
-        index, K ranges, norm prologue; head prologue: float4 kernel or one wavefront per row, and
+        index, K ranges, norm prologue, norm in the split-K reduce and whether the split was
+        made for it; head prologue: float4 kernel or one wavefront per row, and
         how many Q/K parts one launch covers)."""
         lib, h = self._lib, self._plan_handle
         first, count, kind = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
@@ -282,7 +283,8 @@ class CompiledExecutor(Executor):
             if d["kernel"].startswith("attn_fwd_mfma16"):
                 d.update(fold=bool(ints[6]), split_wg=int(ints[7]), defer=bool(ints[14]))
             elif d["kernel"].startswith("gemm_"):
-                d.update(ksplit=max(1, int(ints[10])), dma_tile=int(ints[14]) - 1, norm=int(ints[15]))
+                d.update(ksplit=max(1, int(ints[10])), dma_tile=int(ints[14]) - 1, norm=int(ints[15]),
+                         reduce_norm=int(ints[16]), split_for_norm=bool(int(ints[17]) & 256))
             elif d["kind"] == "head_prologue":
                 d.update(vec=bool(ints[13]), parts=int(ints[14]) if ints[13] else 1)
             out.append(d)

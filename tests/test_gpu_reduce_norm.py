@@ -102,3 +102,31 @@ def test_reduce_norm_other_widths_stay_apart(monkeypatch, N):
     assert "rmsnorm" in names, names
     assert normwise_rel(h, h64) <= 1e-4 and normwise_rel(n, n64) <= 1e-4
 
+
+
+def _params(graph, inputs):
+    from runtime.executor.compiled import CompiledExecutor
+    from runtime.planner import plan
+    ex = CompiledExecutor(fuse=True)
+    ex.compile(plan(graph))
+    try:
+        out = ex.run(inputs)
+        return out["h"], out["n"], ex.step_params()
+    finally:
+        ex.close()
+
+
+@pytest.mark.parametrize("norm", ["rms", "layer"])
+def test_unsplit_gemm_takes_two_ranges_for_the_norm(monkeypatch, norm):
+    """A small unsplit residual GEMM (GPT-2's attention projection shape) takes two K
+    ranges so its reduce carries the norm: the K sum then rounds otherwise than the
+    unsplit GEMM (within 1e-5 of the plan that keeps them apart)."""
+    g, ins, h64, n64 = _graph(rng(21), 1024, 768, 768, norm, True)
+    h, n, steps = _params(g, ins)
+    monkeypatch.setenv("LBR_REDUCE_NORM_SPLIT", "0")
+    h2, n2, steps2 = _params(g, ins)
+    joined = [p for p in steps if p.get("split_for_norm")]
+    assert len(joined) == 1 and joined[0]["ksplit"] == 2 and joined[0]["reduce_norm"], steps
+    assert not any(p.get("split_for_norm") or p.get("reduce_norm") for p in steps2), steps2
+    assert normwise_rel(h, h2) <= 1e-5 and normwise_rel(n, n2) <= 1e-5
+    assert normwise_rel(h, h64) <= 1e-4 and normwise_rel(n, n64) <= 1e-4
