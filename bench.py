@@ -237,8 +237,13 @@ def host_facts() -> dict:
 
 # ---------------------------------------------------------------- one workload
 
-def measure(key: str, args, graph_stem: str | None = None) -> dict:
-    """Export (or load) one workload, compile it through Session, and measure it."""
+def measure(key: str, args, graph_stem: str | None = None, min_timed_ms: float = 0.0) -> dict:
+    """Export (or load) one workload, compile it through Session, and measure it.
+
+    min_timed_ms > 0 (the non-headline configs): time at least --steps steps and
+    enough more that the timed region covers that many milliseconds, so that
+    host-side jitter does not dominate a step of a few µs; the headline times
+    exactly --steps."""
     from runtime.session import Session
     from workloads import WORKLOADS, export_workload
 
@@ -266,14 +271,18 @@ def measure(key: str, args, graph_stem: str | None = None) -> dict:
     for _ in range(args.warmup):
         ex.launch()
     ex.synchronize()
+    steps = args.steps
+    if min_timed_ms > 0:
+        est = ex.time_launches(max(1, args.warmup)) / max(1, args.warmup)
+        steps = max(steps, int(np.ceil(min_timed_ms / max(est, 1e-3))))
     t_start = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         ex.launch()
     ex.synchronize()
-    wall_ms = (time.perf_counter() - t_start) * 1e3 / args.steps
-    event_ms = ex.time_launches(args.steps) / args.steps
+    wall_ms = (time.perf_counter() - t_start) * 1e3 / steps
+    event_ms = ex.time_launches(steps) / steps
     tokens = x.shape[0] * x.shape[1]
-    log(f"[bench] {args.steps} steps: {wall_ms:.3f} ms/step wall, {event_ms:.3f} ms/step hipEvent")
+    log(f"[bench] {steps} steps: {wall_ms:.3f} ms/step wall, {event_ms:.3f} ms/step hipEvent")
     # median of single replays (hipEvent pair around each graph launch), and the end-to-end
     # Session.run wall time with the input H2D and output D2H copies included
     replays = max(20, args.steps)
@@ -339,7 +348,7 @@ def measure(key: str, args, graph_stem: str | None = None) -> dict:
     result = {
         "workload": key, "title": title, "batch": int(x.shape[0]), "seq_len": int(x.shape[1]),
         "d_model": d_model, "tokens_per_s": round(tokens / (ms_per_step / 1e3), 2),
-        "ms_per_step": round(ms_per_step, 4), "event_ms_per_step": round(event_ms, 4),
+        "ms_per_step": round(ms_per_step, 4), "event_ms_per_step": round(event_ms, 4), "steps": steps,
         "latency": {"replay_median_ms": round(replay_ms, 4), "replays": replays,
                     "session_run_median_ms": round(session_run_ms, 4), "session_runs": len(run_wall) - 1,
                     "session_run_io_bytes": int(io_bytes),
@@ -409,7 +418,7 @@ def main() -> int:
         others = [] if args.config else [k for k in CONFIG_ORDER if k != head_key]
     per_shape = []
     for k in others:
-        per_shape.append(measure(k, args))
+        per_shape.append(measure(k, args, min_timed_ms=30.0))
     if per_shape:
         by_key = {r["workload"]: r for r in per_shape}
         by_key[head["workload"]] = dict(head, headline=True)
