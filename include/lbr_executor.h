@@ -226,9 +226,14 @@ int lbr_plan_node_kernel(const lbr_plan* plan, int index, char* name_out,
                                      at the norm)                                               */
 #define LBR_FUSE_MLP           11 /* [RMSNORM | LAYERNORM →] MATMUL[_ADD] → RELU | GELU | SILU →
                                      MATMUL[_ADD] [→ ADD(y, R)], small: one kernel per 16 rows
-                                     with the hidden activations in LDS (D ≤ 1024, D, H and
-                                     the output width multiples of 16, (D + H + 8)·64 B ≤ 64
-                                     KiB, 2·M·(H·D + D2·H) ≤ 2^25 flops)                        */
+                                     with both weights staged in LDS (each ≤ 64 KiB) and the
+                                     hidden activations in LDS (D, H and the output width
+                                     multiples of 16, each wavefront's share of a weight ≤ 16
+                                     float4 a lane, 2·M·(H·D + D2·H) ≤ 2^25 flops)              */
+#define LBR_FUSE_ADD_NORM      12 /* ADD (same shape, or a [P, N] row block broadcast over the
+                                      leading dims) → RMSNORM | LAYERNORM: the norm kernel adds,
+                                      writes the sum and normalises it (a plan step join; not
+                                      reported by lbr_fusion_windows)                      */
 #define LBR_FUSE_TINY           9 /* opt-in (LBR_TINY=1): the whole node array as one workgroup
                                      of 1024 threads, the intermediates held in LDS (outputs
                                      spanning at most the CU's LDS less the node records, small

@@ -445,6 +445,17 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
             if (i < n_nodes && (r >= runs.size() || runs[r].first != i) && lbr_merge_reduce_norm(&s, decoded[i])) ++i;
             p->steps.push_back(s);
         } else {
+            // an ADD whose sum only a norm right after it reads first (a position
+            // table, say): the norm kernel adds
+            Step nstep;
+            if (fuse && !tiny && i + 1 < n_nodes && (r >= runs.size() || runs[r].first != i + 1)) {
+                nstep = decoded[i + 1];
+                if (lbr_merge_add_norm(&nstep, decoded[i], &nodes[i])) {
+                    p->steps.push_back(nstep);
+                    i += 2;
+                    continue;
+                }
+            }
             p->steps.push_back(decoded[i]);
             ++i;
         }

@@ -1636,3 +1636,80 @@ bool lbr_merge_reduce_norm(Step* g, const Step& n) {
     return true;
 }
 
+// Joins the decoded ADD step a (node add) into the decoded RMSNORM /
+// LAYERNORM step n right after it whose input is the sum: n's kernel then
+// adds, writes the sum (the ADD's output) and normalises it.  The ADD must be
+// one contiguous [M, N] operand plus either one of the same shape or a [P, N]
+// block broadcast over the leading dims (row r adds row r mod P): a position
+// table.  Each wavefront / workgroup owns whole rows: the sum may overlap the
+// full operand only row for row (the same base), and nothing else either
+// output touches may be read.
+bool lbr_merge_add_norm(Step* n, const Step& a, const OpNode* add) {
+    if (getenv("LBR_ADD_NORM") && strcmp(getenv("LBR_ADD_NORM"), "0") == 0) return false;
+    if (!a.name || !n->name || add->op != OP_ADD || add->n_inputs < 2 || !is_f32(add)) return false;
+    const bool rms = strcmp(n->name, "rmsnorm") == 0;
+    if ((!rms && strcmp(n->name, "layernorm") != 0) || (n->i[2] != 1 && n->i[2] != 2) || n->in[3]) return false;
+    if (a.node_index + a.n_nodes != n->node_index || n->in[0] != a.out) return false;
+    const long long M = n->i[0], N = n->i[1];
+    if (M <= 0 || N <= 0 || N % 4 || node_total(add) != M * N) return false;
+    const void* full = nullptr;
+    const void* part = nullptr;
+    long long P = 0;
+    if (add->extra[0] == 1) {   // same shape
+        full = add->inputs[0];
+        part = add->inputs[1];
+        P = M;
+    } else if (add->extra[0] == 3) {   // broadcast: [3, nd, a strides, b strides, out shape]
+        const int nd = (int)add->extra[1];
+        if (nd < 2 || 1 + 3 * nd > MAX_DIMS - 1) return false;
+        const int* as = &add->extra[2];
+        const int* bs = &add->extra[2 + nd];
+        const int* sh = &add->extra[2 + 2 * nd];
+        if (sh[nd - 1] != N) return false;
+        auto contiguous = [&](const int* st) {
+            long long want = 1;
+            for (int d = nd - 1; d >= 0; --d) {
+                if (sh[d] > 1 && st[d] != want) return false;
+                want *= sh[d];
+            }
+            return true;
+        };
+        auto rows_of = [&](const int* st) {   // (row mod P)·N + col, P = sh[nd − 2]
+            if (st[nd - 1] != 1 || (sh[nd - 2] > 1 && st[nd - 2] != N)) return false;
+            for (int d = 0; d < nd - 2; ++d)
+                if (sh[d] > 1 && st[d] != 0) return false;
+            return true;
+        };
+        if (contiguous(as) && rows_of(bs)) {
+            full = add->inputs[0];
+            part = add->inputs[1];
+        } else if (contiguous(bs) && rows_of(as)) {
+            full = add->inputs[1];
+            part = add->inputs[0];
+        } else {
+            return false;
+        }
+        P = sh[nd - 2];
+    } else {
+        return false;
+    }
+    if (P <= 0 || M % P || P > (1LL << 30) || !lbr_aligned(full, 16) || !lbr_aligned(part, 16) ||
+        !lbr_aligned(a.out, 16))
+        return false;
+    auto rg = [](const void* q, long long bytes) { return Rng{(uintptr_t)q, (uintptr_t)q + (uintptr_t)bytes}; };
+    const Rng h = rg(a.out, M * N * 4), y = rg(n->out, M * N * 4), f = rg(full, M * N * 4);
+    std::vector<Rng> fixed{rg(part, P * N * 4), rg(n->in[1], N * 4)};
+    if (n->in[2]) fixed.push_back(rg(n->in[2], N * 4));
+    if (any_overlap(h, fixed) || any_overlap(y, fixed) || overlap(h, y)) return false;
+    if ((overlap(h, f) && h.lo != f.lo) || (overlap(y, f) && y.lo != f.lo)) return false;
+    n->in[0] = full;
+    n->in[3] = part;
+    n->i[4] = P;
+    n->in[4] = a.out;
+    n->node_index = a.node_index;
+    n->n_nodes += a.n_nodes;
+    n->fuse_kind = LBR_FUSE_ADD_NORM;
+    n->name = rms ? "rmsnorm+add" : "layernorm+add";
+    return true;
+}
+

@@ -82,6 +82,12 @@ bool lbr_merge_proj_mlp(Step* u, const Step& t);
 // writes the normalised rows; false leaves g unchanged.
 bool lbr_merge_reduce_norm(Step* g, const Step& n);
 
+// Joins the decoded ADD step a (node add) into the decoded RMSNORM /
+// LAYERNORM step n right after it that normalises the sum (same-shape or
+// row-block broadcast ADD): n's kernel then adds, writes the sum and
+// normalises it; false leaves n unchanged.
+bool lbr_merge_add_norm(Step* n, const Step& a, const OpNode* add);
+
 // Byte range [*lo, *hi) input k of node nd reads (per op, from its shape and
 // extras); *hi = UINTPTR_MAX when the node does not fix it.
 void lbr_input_extent(const OpNode* nd, int k, unsigned long long* lo, unsigned long long* hi);

@@ -24,10 +24,24 @@ constexpr int NB = 256;  // block size for row kernels
 // ----------------------------- LayerNorm / RMSNorm -------------------------
 
 // One wave per row, cols <= 64 * 4 * VPL, float4 path (cols % 4 == 0).
+// With a pre-add (lbr_merge_add_norm): the normalised row is x + p, p = row
+// (row mod period) of addb, and that sum is also written to hout (the ADD's
+// output) — the same single addition the ADD kernel makes.
+__device__ __forceinline__ void norm_pre_add(float4& v, const float* __restrict__ addb, long long row, int period,
+                                             int cols, int idx, float* __restrict__ hout) {
+    const float4 p = reinterpret_cast<const float4*>(addb + (row % period) * cols)[idx];
+    v.x = v.x + p.x;
+    v.y = v.y + p.y;
+    v.z = v.z + p.z;
+    v.w = v.w + p.w;
+    reinterpret_cast<float4*>(hout + row * cols)[idx] = v;
+}
+
 template <bool RMS, int VPL>
 __global__ __launch_bounds__(NB) void norm_wave_rows(const float* __restrict__ x, const float* __restrict__ g,
                                                      const float* __restrict__ b, float* __restrict__ out,
-                                                     long long rows, int cols, float eps) {
+                                                     long long rows, int cols, float eps, const float* __restrict__ addb,
+                                                     int period, float* __restrict__ hout) {
     const int lane = threadIdx.x & 63;
     const long long row = (long long)blockIdx.x * (NB / 64) + threadIdx.x / 64;
     if (row >= rows) return;
@@ -45,6 +59,11 @@ __global__ __launch_bounds__(NB) void norm_wave_rows(const float* __restrict__ x
         wv[k] = in ? g4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
         bv[k] = in && !RMS ? b4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    if (addb) {
+#pragma unroll
+        for (int k = 0; k < VPL; ++k)
+            if (lane + k * 64 < c4) norm_pre_add(v[k], addb, row, period, cols, lane + k * 64, hout);
+    }
     lbr_norm_row_wave<RMS, VPL>(v, wv, bv, reinterpret_cast<float4*>(out + row * cols), c4, cols, eps);
 }
 
@@ -52,7 +71,9 @@ __global__ __launch_bounds__(NB) void norm_wave_rows(const float* __restrict__ x
 template <bool RMS, int VPL>
 __global__ __launch_bounds__(NB) void norm_block_rows(const float* __restrict__ x, const float* __restrict__ g,
                                                       const float* __restrict__ b, float* __restrict__ out,
-                                                      long long rows, int cols, float eps) {
+                                                      long long rows, int cols, float eps,
+                                                      const float* __restrict__ addb, int period,
+                                                      float* __restrict__ hout) {
     __shared__ float red[NB / 64];
     const long long row = blockIdx.x;
     const int c4 = cols / 4;
@@ -69,6 +90,11 @@ __global__ __launch_bounds__(NB) void norm_block_rows(const float* __restrict__ 
         v[k] = in ? xr[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
         wv[k] = in ? g4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
         bv[k] = in && !RMS ? b4[idx] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (addb) {
+#pragma unroll
+        for (int k = 0; k < VPL; ++k)
+            if ((int)threadIdx.x + k * NB < c4) norm_pre_add(v[k], addb, row, period, cols, threadIdx.x + k * NB, hout);
     }
     lbr_norm_row_block<RMS, VPL>(v, wv, bv, reinterpret_cast<float4*>(out + row * cols), c4, cols, eps, red);
 }
@@ -113,23 +139,28 @@ void launch_norm(const Step& s, hipStream_t st) {
     const float* g = (const float*)s.in[1];
     const float* b = RMS ? nullptr : (const float*)s.in[2];
     float* out = (float*)s.out;
+    // pre-add (lbr_merge_add_norm): in[3] the broadcast operand, i[4] its period
+    // in rows, in[4] the sum's output
+    const float* addb = (const float*)s.in[3];
+    const int period = s.in[3] ? (int)s.i[4] : 1;
+    float* hout = (float*)s.in[4];
     if (rows <= 0) return;
     switch (s.i[2]) {
         case 1: {
             const unsigned grid = (unsigned)((rows + (NB / 64) - 1) / (NB / 64));
             switch (s.i[3]) {
-                case 1: hipLaunchKernelGGL((norm_wave_rows<RMS, 1>), dim3(grid), dim3(NB), 0, st, x, g, b, out, rows, cols, eps); break;
-                case 2: hipLaunchKernelGGL((norm_wave_rows<RMS, 2>), dim3(grid), dim3(NB), 0, st, x, g, b, out, rows, cols, eps); break;
-                default: hipLaunchKernelGGL((norm_wave_rows<RMS, 4>), dim3(grid), dim3(NB), 0, st, x, g, b, out, rows, cols, eps); break;
+                case 1: hipLaunchKernelGGL((norm_wave_rows<RMS, 1>), dim3(grid), dim3(NB), 0, st, x, g, b, out, rows, cols, eps, addb, period, hout); break;
+                case 2: hipLaunchKernelGGL((norm_wave_rows<RMS, 2>), dim3(grid), dim3(NB), 0, st, x, g, b, out, rows, cols, eps, addb, period, hout); break;
+                default: hipLaunchKernelGGL((norm_wave_rows<RMS, 4>), dim3(grid), dim3(NB), 0, st, x, g, b, out, rows, cols, eps, addb, period, hout); break;
             }
             break;
         }
         case 2:
             switch (s.i[3]) {
-                case 2: hipLaunchKernelGGL((norm_block_rows<RMS, 2>), dim3((unsigned)rows), dim3(NB), 0, st, x, g, b, out, rows, cols, eps); break;
-                case 4: hipLaunchKernelGGL((norm_block_rows<RMS, 4>), dim3((unsigned)rows), dim3(NB), 0, st, x, g, b, out, rows, cols, eps); break;
-                case 8: hipLaunchKernelGGL((norm_block_rows<RMS, 8>), dim3((unsigned)rows), dim3(NB), 0, st, x, g, b, out, rows, cols, eps); break;
-                default: hipLaunchKernelGGL((norm_block_rows<RMS, 16>), dim3((unsigned)rows), dim3(NB), 0, st, x, g, b, out, rows, cols, eps); break;
+                case 2: hipLaunchKernelGGL((norm_block_rows<RMS, 2>), dim3((unsigned)rows), dim3(NB), 0, st, x, g, b, out, rows, cols, eps, addb, period, hout); break;
+                case 4: hipLaunchKernelGGL((norm_block_rows<RMS, 4>), dim3((unsigned)rows), dim3(NB), 0, st, x, g, b, out, rows, cols, eps, addb, period, hout); break;
+                case 8: hipLaunchKernelGGL((norm_block_rows<RMS, 8>), dim3((unsigned)rows), dim3(NB), 0, st, x, g, b, out, rows, cols, eps, addb, period, hout); break;
+                default: hipLaunchKernelGGL((norm_block_rows<RMS, 16>), dim3((unsigned)rows), dim3(NB), 0, st, x, g, b, out, rows, cols, eps, addb, period, hout); break;
             }
             break;
         default:

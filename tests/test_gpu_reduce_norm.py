@@ -130,3 +130,65 @@ def test_unsplit_gemm_takes_two_ranges_for_the_norm(monkeypatch, norm):
     assert not any(p.get("split_for_norm") or p.get("reduce_norm") for p in steps2), steps2
     assert normwise_rel(h, h2) <= 1e-5 and normwise_rel(n, n2) <= 1e-5
     assert normwise_rel(h, h64) <= 1e-4 and normwise_rel(n, n64) <= 1e-4
+
+
+def _add_norm_graph(r, B, S, N, norm, same_shape):
+    """x [B, S, N] + p ([B, S, N], or a [S, N] table broadcast over the batch) →
+    norm; outputs the sum and the norm."""
+    g = Graph()
+    x = randn(r, B, S, N)
+    g.add_tensor("x", x.shape)
+    g.inputs.append("x")
+    if same_shape:
+        p = randn(r, B, S, N)
+        g.add_tensor("p", p.shape)
+        g.inputs.append("p")
+    else:
+        p = randn(r, S, N)
+        g.add_tensor("p", p.shape).buffer = p
+        g.constants.append("p")
+    g.add_tensor("h", (B, S, N))
+    g.add_node(OpType.ADD, ["x", "p"], "h", {})
+    h = x.astype(np.float64) + p
+    gam = (1.0 + 0.5 * randn(r, N)).astype(np.float32)
+    g.add_tensor("gam", (N,)).buffer = gam
+    g.constants.append("gam")
+    g.add_tensor("n", (B, S, N))
+    if norm == "rms":
+        g.add_node(OpType.RMSNORM, ["h", "gam"], "n", {"eps": 1e-6})
+        n = cf_rmsnorm(h, gam, 1e-6)
+    else:
+        bet = randn(r, N)
+        g.add_tensor("bet", (N,)).buffer = bet
+        g.constants.append("bet")
+        g.add_node(OpType.LAYERNORM, ["h", "gam", "bet"], "n", {"eps": 1e-5})
+        n = cf_layernorm(h, gam, bet, 1e-5)
+    g.outputs += ["h", "n"]
+    ins = {"x": x, "p": p} if same_shape else {"x": x}
+    return g, ins, h, n
+
+
+@pytest.mark.parametrize("norm", ["rms", "layer"])
+@pytest.mark.parametrize("same_shape", [False, True])
+@pytest.mark.parametrize("B,S,N", [(1, 1024, 768), (2, 100, 2560), (3, 7, 64)])
+def test_add_norm(monkeypatch, norm, same_shape, B, S, N):
+    """ADD → norm as one norm kernel that adds (the position table of GPT-2's input):
+    bit-equal to the two kernels apart; 1e-4 of float64 and the oracle."""
+    g, ins, h64, n64 = _add_norm_graph(rng(B + S + N), B, S, N, norm, same_shape)
+    h, n, names = _run(g, ins)
+    monkeypatch.setenv("LBR_ADD_NORM", "0")
+    h2, n2, names2 = _run(g, ins)
+    print(names, names2)
+    assert names == [("rmsnorm" if norm == "rms" else "layernorm") + "+add"], names
+    assert len(names2) == 2, names2
+    np.testing.assert_array_equal(h, h2)
+    np.testing.assert_array_equal(n, n2)
+    o = run_oracle_all(g, ins)
+    for got, ref, name in ((h, h64, "h"), (n, n64, "n")):
+        assert normwise_rel(got, ref) <= 1e-4 and normwise_rel(o[name], ref) <= 1e-4, name
+
+
+def run_oracle_all(graph, inputs):
+    from oracle.host_exec import OracleRun
+    from runtime.planner import plan
+    return OracleRun(plan(graph)).run(inputs)
