@@ -268,7 +268,46 @@ struct lbr_plan {
     hipGraphExec_t exec = nullptr;
     void* ws = nullptr;          // shared step workspace (split-K partial sums)
     void* tiny_buf = nullptr;    // device node copy of a single-workgroup plan
+    void* relay = nullptr;       // attention outputs moved off their inputs (lbr_relay_ok)
 };
+
+static void free_plan(lbr_plan* p) {
+    if (p->exec) (void)hipGraphExecDestroy(p->exec);
+    if (p->graph) (void)hipGraphDestroy(p->graph);
+    if (p->ws) (void)hipFree(p->ws);
+    if (p->tiny_buf) (void)hipFree(p->tiny_buf);
+    if (p->relay) (void)hipFree(p->relay);
+    delete p;
+}
+
+// Deferred split attentions whose output only the next GEMM reads write
+// into one plan-owned buffer instead (the steps run in order, and each
+// GEMM consumes the buffer before the next attention writes it); their
+// cut blocks alone then go through the merge kernel.
+static int relay_attention_outputs(lbr_plan* p, const OpNode* nodes, int n_nodes, const void* const* live_ptr,
+                                   const size_t* live_bytes, int n_live) {
+    std::vector<size_t> picks;
+    size_t need = 0;
+    for (size_t i = 0; i + 1 < p->steps.size(); ++i)
+        if (lbr_relay_ok(nodes, n_nodes, p->steps[i], p->steps[i + 1], live_ptr, live_bytes, n_live)) {
+            picks.push_back(i);
+            const Step& a = p->steps[i];
+            need = std::max(need, (size_t)(a.i[0] * a.i[1] * a.i[2]) * sizeof(float));
+        }
+    if (picks.empty()) return LBR_OK;
+    HIP_TRY(hipMalloc(&p->relay, need));
+    for (size_t i : picks) {
+        p->steps[i].out = p->relay;
+        p->steps[i].i[14] = 0;
+        // the deferred names are "attn_fwd_mfma16_f32[+v][+transpose]+defer"
+        const char* nm = p->steps[i].name;
+        const bool v = strstr(nm, "+v") != nullptr, t = strstr(nm, "+transpose") != nullptr;
+        p->steps[i].name = v ? (t ? "attn_fwd_mfma16_f32+v+transpose+relay" : "attn_fwd_mfma16_f32+v+relay")
+                             : (t ? "attn_fwd_mfma16_f32+transpose+relay" : "attn_fwd_mfma16_f32+relay");
+        p->steps[i + 1].in[0] = p->relay;
+    }
+    return LBR_OK;
+}
 
 static void run_steps(const std::vector<Step>& steps, hipStream_t st) {
     for (const Step& s : steps) s.run(s, st);
@@ -460,12 +499,11 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
             ++i;
         }
     }
-    int rc = assign_workspace(p->steps, &p->ws);
+    int rc = tiny || !fuse ? LBR_OK : relay_attention_outputs(p, nodes, n_nodes, live_ptr, live_bytes, n_live);
+    if (!rc) rc = assign_workspace(p->steps, &p->ws);
     if (!rc) rc = autotune_gemms(p->steps);
     if (rc) {
-        if (p->ws) (void)hipFree(p->ws);
-        if (p->tiny_buf) (void)hipFree(p->tiny_buf);
-        delete p;
+        free_plan(p);
         return rc;
     }
     if (use_graph && !p->steps.empty()) {
@@ -477,10 +515,7 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
         if (e == hipSuccess) e = hipGraphInstantiate(&p->exec, p->graph, nullptr, nullptr, 0);
         if (e != hipSuccess) {
             lbr_set_error("lbr_plan_create: graph capture failed: %s", hipGetErrorString(e));
-            if (p->graph) (void)hipGraphDestroy(p->graph);
-            if (p->ws) (void)hipFree(p->ws);
-            if (p->tiny_buf) (void)hipFree(p->tiny_buf);
-            delete p;
+            free_plan(p);
             return LBR_ERR_HIP;
         }
     }
@@ -814,11 +849,7 @@ int lbr_plan_step_args(const lbr_plan* p, int step, long long* ints_out, int cap
 
 int lbr_plan_destroy(lbr_plan* p) {
     if (!p) return LBR_OK;
-    if (p->exec) (void)hipGraphExecDestroy(p->exec);
-    if (p->graph) (void)hipGraphDestroy(p->graph);
-    if (p->ws) (void)hipFree(p->ws);
-    if (p->tiny_buf) (void)hipFree(p->tiny_buf);
-    delete p;
+    free_plan(p);
     return LBR_OK;
 }
 

@@ -928,6 +928,42 @@ void lbr_input_extent(const OpNode* nd, int k, unsigned long long* lo, unsigned 
     *hi = r.hi;
 }
 
+// A split attention step whose output lies over its inputs stores every
+// row through the merge kernel (deferred output).  When the step right
+// after it is a one-batch DMA GEMM whose A operand is exactly that output,
+// and no other read sees the output's bytes before they are overwritten or
+// at the end (live-out), the plan can give the attention a buffer of its
+// own and point the GEMM's A there: the store is then no longer deferred.
+bool lbr_relay_ok(const OpNode* nodes, int n, const Step& at, const Step& gm, const void* const* live_ptr,
+                  const size_t* live_bytes, int n_live) {
+    const char* e = getenv("LBR_ATTN_RELAY");
+    if (e && atoi(e) == 0) return false;
+    if (!at.name || strncmp(at.name, "attn_fwd_mfma16_f32", 19) != 0 || !at.i[7] || !at.i[14]) return false;
+    if (!gm.name || strncmp(gm.name, "gemm_dma_f32_nt", 15) != 0 || gm.in[0] != at.out || gm.i[3] != 1 || gm.i[35])
+        return false;
+    const long long yb = at.i[0] * at.i[1] * at.i[2] * 4;
+    if (gm.i[0] * gm.i[2] * 4 != yb) return false;
+    const int g0 = gm.node_index;
+    const int end = at.node_index + at.n_nodes;
+    if (g0 < end || g0 >= n) return false;
+    std::vector<Rng> inter{rng(at.out, yb)};
+    for (int j = end; j < n && !inter.empty(); ++j) {
+        const OpNode* nd = &nodes[j];
+        const int reads = nd->op == OP_ATTENTION ? 3 + (nd->extra[3] != 0) : nd->n_inputs;
+        for (int k = 0; k < reads && k < nd->n_inputs && k < MAX_INPUTS; ++k) {
+            if (j == g0 && k == 0) continue;   // the GEMM's A: the read that moves to the buffer
+            const Rng in = input_rng(nd, k);
+            for (const Rng& r : inter)
+                if (overlap(r, in)) return false;
+        }
+        subtract(&inter, out_rng(nd));
+    }
+    for (const Rng& r : inter)
+        for (int k = 0; k < n_live; ++k)
+            if (overlap(r, rng(live_ptr[k], (long long)live_bytes[k]))) return false;
+    return true;
+}
+
 // Find the fusable runs of `nodes` (in order, non-overlapping).
 int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, const size_t* live_bytes, int n_live,
                      std::vector<FusedRun>* out) {

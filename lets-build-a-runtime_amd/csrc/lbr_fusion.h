@@ -88,6 +88,12 @@ bool lbr_merge_reduce_norm(Step* g, const Step& n);
 // normalises it; false leaves n unchanged.
 bool lbr_merge_add_norm(Step* n, const Step& a, const OpNode* add);
 
+// Whether the deferred split attention step `at` can write into a buffer of
+// the plan's own that the DMA GEMM step `gm` right after it reads as A (its
+// only reader): the attention's store is then not deferred.
+bool lbr_relay_ok(const OpNode* nodes, int n, const Step& at, const Step& gm, const void* const* live_ptr,
+                  const size_t* live_bytes, int n_live);
+
 // Byte range [*lo, *hi) input k of node nd reads (per op, from its shape and
 // extras); *hi = UINTPTR_MAX when the node does not fix it.
 void lbr_input_extent(const OpNode* nd, int k, unsigned long long* lo, unsigned long long* hi);

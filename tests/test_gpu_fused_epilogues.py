@@ -297,3 +297,53 @@ def test_attention_transpose_over_v(H, S, hd, causal):
         ex.close()
     ref = np.swapaxes(cf_attention(q, k, np.maximum(x, 0.0), causal=causal), 1, 2)
     _check(g, {"q": q, "k": k, "x": x}, ref, "attn_transpose")
+
+
+@pytest.mark.parametrize("H,S,hd,causal", [(12, 1024, 64, True), (8, 640, 128, True), (4, 700, 64, False)])
+def test_attention_output_relay(monkeypatch, H, S, hd, causal):
+    """The output TRANSPOSE over V, as above, read only by the projection GEMM after it: the plan
+    gives the attention a buffer of its own and points the GEMM's A there, so the store is not
+    deferred (only cut blocks go through the merge kernel).  Bit-equal to the deferred plan
+    (LBR_ATTN_RELAY=0), and to the closed form within the fused tolerance."""
+    from helpers import cf_attention
+    from runtime.executor.compiled import CompiledExecutor
+    from runtime.planner import plan
+    r = rng(H * S + hd + 2)
+    W, N = H * hd, 96
+    q, k, x = randn(r, 1, H, S, hd), randn(r, 1, H, S, hd), randn(r, 1, H, S, hd)
+    w = randn(r, N, W, scale=0.05)
+    g = Graph()
+    for name in ("q", "k", "x"):
+        g.add_tensor(name, (1, H, S, hd))
+        g.inputs.append(name)
+    g.add_tensor("w", (N, W)).buffer = w
+    g.constants.append("w")
+    g.add_tensor("v", (1, H, S, hd))
+    g.add_node(OpType.RELU, ["x"], "v", {})
+    g.add_tensor("att", (1, H, S, hd))
+    g.add_node(OpType.ATTENTION, ["q", "k", "v"], "att", {"causal": True} if causal else {})
+    g.add_tensor("out", (1, S, H, hd))
+    g.add_node(OpType.TRANSPOSE, ["att"], "out", {"dim0": 1, "dim1": 2})
+    g.add_tensor("o2", (1, S, W))
+    g.add_node(OpType.RESHAPE, ["out"], "o2", {"shape": (1, S, W)})
+    g.add_tensor("c", (1, S, N))
+    g.add_node(OpType.MATMUL, ["o2", "w"], "c", {"transpose_b": True})
+    g.outputs.append("c")
+    ins = {"q": q, "k": k, "x": x}
+    ys = {}
+    for relay in ("1", "0"):
+        monkeypatch.setenv("LBR_ATTN_RELAY", relay)
+        ex = CompiledExecutor(fuse=True)
+        ex.compile(plan(g))
+        try:
+            names = ex.kernel_names()
+            print(relay, names)
+            assert any(n.endswith("+transpose+relay" if relay == "1" else "+transpose+defer") for n in names)
+            ys[relay] = [ex.run(ins)["c"] for _ in range(3)]
+        finally:
+            ex.close()
+    for y in ys["1"] + ys["0"][1:]:
+        assert np.array_equal(y, ys["0"][0])
+    att = np.swapaxes(cf_attention(q, k, np.maximum(x, 0.0), causal=causal), 1, 2).reshape(1, S, W)
+    ref = att.astype(np.float64) @ w.T.astype(np.float64)
+    assert normwise_rel(ys["1"][0], ref) <= 1e-4
