@@ -328,7 +328,7 @@ __device__ __forceinline__ int attn16_tiles(const AttnArgs& g, int qblk, bool ca
 // through Ks/Vs.  slot < 0: the range is the whole row, write O.  slot >= 0:
 // write the unnormalised partial (Σ p·V, running max m, Σ p) of this key
 // range to the split workspace for attn_split_merge.
-template <int DP, bool CAUSAL, bool HAS_MASK, bool SPLIT>
+template <int DP, bool CAUSAL, bool HAS_MASK, bool SPLIT, bool DB = SPLIT>
 __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qblk, int t0_, int t1, long long slot,
                                               float (*Ks)[DP + 4], float (*Vs)[DP + 4]) {
     constexpr int NCH = DP / 16;     // 16-wide d chunks (S reduction) and d blocks (O)
@@ -409,21 +409,26 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
             }
         }
     };
-    auto store = [&]() {
+    // DB (the split kernel): Ks and Vs hold two tiles, the one being read and
+    // the next one being stored, so a tile ends with one barrier, not two
+    int cur = 0;
+    auto store = [&](int buf) {
+        float (*Kd)[DP + 4] = Ks + buf * A16_KB;
+        float (*Vd)[DP + 4] = Vs + buf * A16_KB;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int idx = tid + i * A16_NT;
             if (idx < TILE4) {
                 const int r = idx / (DP / 4), d = (idx % (DP / 4)) * 4;
-                *reinterpret_cast<float4*>(&Ks[r][d]) = kr[i];
-                *reinterpret_cast<float4*>(&Vs[r][d]) = vr[i];
+                *reinterpret_cast<float4*>(&Kd[r][d]) = kr[i];
+                *reinterpret_cast<float4*>(&Vd[r][d]) = vr[i];
             }
         }
     };
 
     if (t0 < t_fast) load(t0 * A16_KB, BoolTag<false>());
     else load(t0 * A16_KB, BoolTag<true>());
-    store();
+    store(0);
     __syncthreads();
 
     // One key tile.  The scores are exponentiated against m_run, which moves only
@@ -437,6 +442,8 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
         constexpr bool MASKED = decltype(masked_tag)::value;
         const int k0 = kt * A16_KB;
         if (kt + 1 < t1) load(k0 + A16_KB, pcheck_tag);
+        const float (*Kc)[DP + 4] = Ks + cur * A16_KB;
+        const float (*Vc)[DP + 4] = Vs + cur * A16_KB;
 
         if (!MASKED || !CAUSAL || k0 <= q_wave0 + 15) {
             // Sᵀ for two 16-key blocks; register r of block b = key k0 + 16b + 4g + r
@@ -446,7 +453,7 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
                 sacc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int c = 0; c < NCH; ++c) {
-                    const floatx4 kf = *reinterpret_cast<const floatx4*>(&Ks[16 * b + lr][16 * c + 4 * lg]);
+                    const floatx4 kf = *reinterpret_cast<const floatx4*>(&Kc[16 * b + lr][16 * c + 4 * lg]);
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
                         sacc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[i], qf[c][i], sacc[b], 0, 0, 0);
@@ -500,7 +507,7 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
                     const int kvl = 16 * b + 4 * lg + r;
 #pragma unroll
                     for (int h = 0; h < NCH / W; ++h) {
-                        const VW vv = *reinterpret_cast<const VW*>(&Vs[kvl][16 * W * h + W * lr]);
+                        const VW vv = *reinterpret_cast<const VW*>(&Vc[kvl][16 * W * h + W * lr]);
 #pragma unroll
                         for (int w = 0; w < W; ++w)
                             oacc[W * h + w] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[w], sacc[b][r], oacc[W * h + w],
@@ -508,10 +515,16 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
                     }
                 }
         }
-        __syncthreads();
-        if (kt + 1 < t1) {
-            store();
+        if (DB) {
+            if (kt + 1 < t1) store(cur ^ 1);
+            __syncthreads();   // the next tile is stored, and no wave still reads this one
+            cur ^= 1;
+        } else {
             __syncthreads();
+            if (kt + 1 < t1) {
+                store(0);
+                __syncthreads();
+            }
         }
     };
     int kt = t0;
@@ -599,8 +612,8 @@ __global__ __launch_bounds__(A16_NT, 4) void attn_fwd_mfma16(AttnArgs g) {
 
 template <int DP, bool CAUSAL, bool HAS_MASK>
 __global__ __launch_bounds__(A16_NT, 4) void attn_fwd_mfma16_split(AttnArgs g) {
-    __shared__ float Ks[A16_KB][DP + 4];
-    __shared__ float Vs[A16_KB][DP + 4];
+    __shared__ float Ks[2 * A16_KB][DP + 4];
+    __shared__ float Vs[2 * A16_KB][DP + 4];
     const int w = blockIdx.x;
     const int end = sk_bound(g, w + 1);
     int G = sk_bound(g, w);
