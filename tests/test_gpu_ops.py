@@ -201,6 +201,8 @@ def test_attention(B, H, S, hd, causal, group):
     (1, 8, 512, 64, True, 2),       # 4 query blocks: pairs (3, 0), (2, 1)
     (2, 2, 1000, 32, True, 1),
     (1, 2, 130, 128, False, 1),     # non-causal ignores the fold flag
+    (1, 3, 300, 40, True, 1),       # hd/4 = 10 threads a row: merge rows straddle workgroups
+    (1, 2, 520, 96, True, 2),       # hd/4 = 24
 ])
 def test_attention_schedules(monkeypatch, env, B, H, S, hd, causal, group):
     for k, v in env.items():
