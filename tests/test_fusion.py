@@ -288,11 +288,12 @@ def test_not_rotate_half_is_not_rope():
     assert _windows(nodes) == [(0, 3, "head_prologue")]
 
 
-def _attn_transpose(out_off, v_off=20 * MB, B=1, H=4, S=128, hd=64):
-    q, k, v = ARENA + 16 * MB, ARENA + 18 * MB, ARENA + v_off
-    att = _node(OpType.ATTENTION, [q, k, v, ARENA + 30 * MB], ARENA + 24 * MB, (B, H, S, hd), (S, hd, 1, 0, 1))
+def _attn_transpose(out_off, v_off=20 * MB, B=1, H=4, S=128, hd=64, q_off=16 * MB, k_off=18 * MB,
+                    att_off=24 * MB):
+    q, k, v = ARENA + q_off, ARENA + k_off, ARENA + v_off
+    att = _node(OpType.ATTENTION, [q, k, v, ARENA + 30 * MB], ARENA + att_off, (B, H, S, hd), (S, hd, 1, 0, 1))
     att.n_inputs = 4          # Q, K, V + the planner's scratch slot
-    tr = _node(OpType.TRANSPOSE, [ARENA + 24 * MB], ARENA + out_off, (B, S, H, hd), (B, H, 1, S, hd))
+    tr = _node(OpType.TRANSPOSE, [ARENA + att_off], ARENA + out_off, (B, S, H, hd), (B, H, 1, S, hd))
     return [att, tr]
 
 
@@ -311,9 +312,29 @@ def test_attention_transpose_refuses_misaligned_output():
     assert _windows(_sliced_v(0, 24 * MB, 26 * MB + 8)) == [(0, 2, "attn_sliced_v")]
 
 
-def test_attention_transpose_refuses_output_over_v():
-    # the planner may reuse V's memory once attention is done; one fused kernel still reads V
+def _no_deferred_store(monkeypatch):
+    """Attention schedules without a deferred store: no key-range split."""
+    monkeypatch.setenv("LBR_ATTN_SPLIT", "0")
+
+
+def test_attention_transpose_output_over_v(monkeypatch):
+    # 4 heads × S 128 take the key-range split, whose merge kernel stores every output row after
+    # the attention kernel has read V: the output may lie over V (deferred store)
+    assert _windows(_attn_transpose(20 * MB)) == [(0, 2, "attn_transpose")]
+    # the same grid without the split: the planner may reuse V's memory once attention is done,
+    # but one fused kernel still reads V
+    _no_deferred_store(monkeypatch)
     assert _windows(_attn_transpose(20 * MB)) == []
+    assert _windows(_attn_transpose(26 * MB)) == [(0, 2, "attn_transpose")]
+
+
+def test_attention_transpose_refuses_output_over_v_on_a_full_grid():
+    # 32 heads × S 4096 × hd 128 fill the CUs with folded query blocks: no split, no deferred
+    # store, so an output over V is refused while one elsewhere fuses
+    big = dict(H=32, S=4096, hd=128, q_off=0, k_off=64 * MB, v_off=128 * MB, att_off=192 * MB)
+    assert _windows(_attn_transpose(256 * MB, **big)) == [(0, 2, "attn_transpose")]
+    assert _windows(_attn_transpose(128 * MB, **big)) == []
+    assert _windows(_attn_transpose(160 * MB, **big)) == []
 
 
 def _split_attn_transpose(out_off, H=12, S=1024, hd=64, later=()):
@@ -367,14 +388,21 @@ def test_attention_sliced_v_fuses():
     assert _windows(_sliced_v(0, 24 * MB, 26 * MB, sliced=True)) == [(0, 4, "attn_sliced_v")]
 
 
-def test_attention_sliced_v_refusals():
+def test_attention_sliced_v_refusals(monkeypatch):
     # the attention output over the rows V is read from is fine while the output transpose
-    # joins the run (the fused kernel never writes it) ...
+    # joins the run (the fused kernel never writes it)
     assert _windows(_sliced_v(24 * MB, 24 * MB, 26 * MB)) == [(0, 3, "attn_sliced_v")]
-    # ... but not when the final output lands there: the plain output transpose fusion only
+    # 8 heads × S 128 take the key-range split (deferred store): the final output may land over
+    # V's source rows, and so may the output transpose
+    assert _windows(_sliced_v(24 * MB, 24 * MB, 24 * MB)) == [(0, 3, "attn_sliced_v")]
+    assert _windows(_sliced_v(26 * MB, 24 * MB, 26 * MB)) == [(0, 3, "attn_sliced_v")]
+    # without the split: the final output over V's source leaves the plain output transpose
+    # fusion only, and the output transpose over V's source stays out of the run
+    _no_deferred_store(monkeypatch)
+    assert _windows(_sliced_v(24 * MB, 24 * MB, 26 * MB)) == [(0, 3, "attn_sliced_v")]
     assert _windows(_sliced_v(24 * MB, 24 * MB, 24 * MB)) == [(1, 2, "attn_transpose")]
-    # the output transpose over V's source: the attention joins, its output transpose does not
     assert _windows(_sliced_v(26 * MB, 24 * MB, 26 * MB)) == [(0, 2, "attn_sliced_v")]
+    monkeypatch.delenv("LBR_ATTN_SPLIT")
     # the transposed V read again later: it must be written
     reader = _node(OpType.RELU, [ARENA + 44 * MB], ARENA + 50 * MB, (1, 2, 128, 64))
     assert _windows(_sliced_v(0, 24 * MB, 26 * MB, later=[reader])) == [(1, 2, "attn_transpose")]
