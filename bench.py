@@ -108,7 +108,15 @@ def step_units(names, order, graph, ms, runs):
     A fused run's work: the flops of its GEMM/attention nodes; bytes = what it
     reads from outside the run (for a SLICE of an outside tensor, only the
     sliced part) plus the outputs that leave the run (read by a later node or
-    graph outputs)."""
+    graph outputs).  Views (RESHAPE, dim-0 SLICE: never dispatched, they alias
+    their input, runtime/ops.py:411-415) are resolved to the tensor that owns
+    the memory, so a view of a tensor made inside the run is not an outside
+    read, and a later read through a view still takes the run's output."""
+    from runtime.planner import _resolve_alias
+
+    def nbytes(t):
+        return float(np.prod(graph.tensors[t].shape)) * np.dtype(graph.tensors[t].dtype).itemsize
+
     start = {f: c for f, c, _ in runs}
     units, i = [], 0
     while i < len(order):
@@ -117,23 +125,27 @@ def step_units(names, order, graph, ms, runs):
         if c == 1:
             f, b = node_work(nodes[0], graph)
         else:
-            inside = {n.output for n in nodes}
-            later = {t for n in order[i + c:] for t in n.inputs} | set(graph.outputs)
+            inside = {_resolve_alias(n.output, graph) for n in nodes}
+            later = {_resolve_alias(t, graph) for n in order[i + c:] for t in n.inputs}
+            later |= {_resolve_alias(t, graph) for t in graph.outputs}
             f, b = 0.0, 0.0
             seen = set()
             for n in nodes:
                 nf, _ = node_work(n, graph)
                 f += nf
                 for t in n.inputs:
-                    if t in inside or t in seen:
+                    root = _resolve_alias(t, graph)
+                    if root in inside:
                         continue
-                    seen.add(t)
-                    t_node = n if n.op.name == "SLICE" else None
-                    src = t_node.output if t_node is not None else t
-                    b += np.prod(graph.tensors[src].shape) * np.dtype(graph.tensors[src].dtype).itemsize
-            for t in inside:
-                if t in later:
-                    b += np.prod(graph.tensors[t].shape) * np.dtype(graph.tensors[t].dtype).itemsize
+                    # a view as large as its root reads the same bytes as the root
+                    key = root if nbytes(t) == nbytes(root) else t
+                    if key in seen:
+                        continue
+                    seen.add(key)
+                    b += nbytes(n.output) if n.op.name == "SLICE" else nbytes(t)
+            for n in nodes:
+                if _resolve_alias(n.output, graph) in later:
+                    b += nbytes(n.output)
         units.append({"name": names[i], "nodes": nodes, "ms": ms[i], "flops": f, "bytes": float(b)})
         i += c
     return units
