@@ -268,10 +268,19 @@ int lbr_plan_step_info(const lbr_plan* plan, int step, int* first_node,
  * does (x < 2^31, d >= 1): test support, no counterpart in the reference. */
 unsigned lbr_tiny_fast_div(unsigned x, unsigned d);
 
+/* The (head, 16-row query block) each workgroup of the key-quartered
+ * attention kernel runs, for `bh` heads of `seq` rows (causal or not) on
+ * `cus` CUs: workgroup w gets heads_out[w], blocks_out[w] (w < cap).  The
+ * same assignment and index arithmetic as the launch, run on the host: test
+ * support, no counterpart in the reference.  Returns the grid size. */
+int lbr_attn_kq_grid(long long bh, int seq, int causal, int cus,
+                     int* heads_out, int* blocks_out, int cap);
+
 /* The decoded integer launch arguments of step `step` (up to `cap` of them,
  * 40 at most), for tests and reports.  Their meaning is the kernel's: for
  * the attention kernel [6] = causal blocks folded in pairs, [7] = key-range
- * split workgroups (0: no split), [14] = deferred output; for the GEMM
+ * split workgroups (0: no split), [14] = deferred output, [15] = the
+ * key-quartered 16-row kernel; for the GEMM
  * kernels [10] = K ranges, [14] = DMA tile index + 1 (0: register-staged
  * kernel). */
 int lbr_plan_step_args(const lbr_plan* plan, int step, long long* ints_out,

@@ -41,6 +41,16 @@
 #include <math.h>
 
 #include <algorithm>
+#include <array>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+// attn_fwd_kq's workgroup assignment (defined with the host code below) and how
+// many of its workgroups one CU holds at once.
+const std::vector<unsigned short>& kq_plan(long long bh, int S, bool causal, int C, int per_cu);
+int kq_per_cu(int dp);
 
 namespace {
 
@@ -80,6 +90,8 @@ struct AttnArgs {
     // v_ld = 0: V is [kv heads, S, D] like K.
     long long v_ld;
     int v_heads;
+    // 16-row key-quartered kernel (attn_fwd_kq): query blocks of 16 rows, kq_nq per head
+    int kq_nq, kq_bh;
 };
 
 // Row q of head bh in the output: [bh][S][D], or [B][S][H][D] when the
@@ -636,6 +648,302 @@ __global__ __launch_bounds__(A16_NT, 4) void attn_fwd_mfma16_split(AttnArgs g) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Small grids: 16 query rows per workgroup, the key tiles dealt four ways.
+//
+// With one 16-row wavefront per query block, the last rows of a causal head
+// are a serial chain of S/32 key tiles on one SIMD (S = 1024, hd = 64: 32
+// tiles × 64 MFMAs × 32 cycles ≈ 30 µs) however the grid is cut.  Here the
+// four wavefronts of a workgroup hold the same 16 query rows and take every
+// fourth key tile (tile t → wavefront t mod 4, which also spreads the causal
+// diagonal), each with its own running max, sum and O.  At the end the four
+// partial rows meet in LDS and are combined in wavefront order:
+//   O = Σ_w 2^(m_w − M)·O_w / Σ_w 2^(m_w − M)·l_w,   M = max_w m_w.
+// No partial leaves the workgroup and no merge kernel runs.  Nothing is
+// shared between the wavefronts, so K and V go from global memory (L2)
+// straight into registers, in the MFMA operand layouts of attn16_qblock; the
+// next tile's K is requested as soon as the current scores are formed and its
+// V as soon as P·V has been issued.  Rows past S read as zero through the
+// buffer views' range check (their scores are masked and their p is 0).
+// Head dims 32, 64 and 128 only (D == DP: no padded columns).
+//
+// Grid: one workgroup per (head, 16-row block), all resident at once (a few
+// per CU).  The hardware hands workgroup w to CU w mod C (C CUs; XCD w mod 8),
+// so workgroups w, w + C, w + 2C ... share a CU and its SIMDs, and a CU's time
+// is the sum of its blocks' key tiles.  The host assigns the blocks (kq_plan):
+// heaviest first, each to the least-loaded CU of the XCD that holds its head
+// (whole heads, or alternate blocks of them, per XCD, so that the K/V rows a
+// workgroup streams stay in that XCD's L2), and passes the assignment in the
+// kernel arguments.  Without one (more blocks than fit at once) workgroup w
+// runs block levels from the heaviest down.
+constexpr int KQ_WAVES = 4;
+constexpr int KQ_NT = 64 * KQ_WAVES;
+constexpr int KQ_QB = 16;        // query rows per workgroup
+constexpr int KQ_MAP_MAX = 1536; // blocks a kernel-argument assignment holds (3 KiB)
+
+struct KqArgs {
+    AttnArgs g;
+    int n_map;                           // 0: no assignment (heaviest block level first)
+    unsigned short map[KQ_MAP_MAX];      // workgroup → block index head·kq_nq + block
+};
+
+__host__ __device__ __forceinline__ void kq_item(const KqArgs& k, int w, int* bh, int* qblk) {
+    const int nq = k.g.kq_nq;
+    int it;
+    if (k.n_map) {
+        it = k.map[w];
+    } else {
+        const int level = w / k.g.kq_bh;
+        it = (w - level * k.g.kq_bh) * nq + (nq - 1 - level);
+    }
+    *bh = it / nq;
+    *qblk = it - *bh * nq;
+}
+
+template <int DP, bool CAUSAL, bool HAS_MASK>
+__global__ __launch_bounds__(KQ_NT, 2) void attn_fwd_kq(KqArgs k) {
+    const AttnArgs& g = k.g;
+    constexpr int NCH = DP / 16;     // 16-wide d chunks (S reduction) and d blocks (O)
+    constexpr int W = NCH < 4 ? NCH : 4;
+    constexpr int NH = NCH / W;
+    typedef float VW __attribute__((ext_vector_type(W)));
+    __shared__ float o_sh[KQ_WAVES][KQ_QB][DP + 4];
+    __shared__ float m_sh[KQ_WAVES][KQ_QB];
+    __shared__ float l_sh[KQ_WAVES][KQ_QB];
+
+    // the wavefront index as a scalar: the key tiles, their offsets and the loop are uniform
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 15, lg = lane >> 4;
+    int bhi, qblk;
+    kq_item(k, blockIdx.x, &bhi, &qblk);
+    const long long bh = bhi, kvh = bh / g.group_size;
+    const int S = g.S, D = g.D;
+    const float* Qb = g.Q + bh * (long long)S * DP;
+    const float* Kb = g.K + kvh * (long long)S * DP;
+    const float* Vb = g.V + kvh * (long long)S * DP;
+    unsigned vst = DP;                                           // V row stride (floats)
+    if (g.v_ld) {
+        const long long b = kvh / g.v_heads;
+        Vb = g.V + b * S * g.v_ld + (kvh - b * g.v_heads) * DP;
+        vst = (unsigned)g.v_ld;
+    }
+    // Buffer views of this head's Q, K and V rows (byte offsets < 2^32, checked by the
+    // host): every load below is a fixed per-lane offset plus a uniform one, and rows past
+    // S fall outside the view and read as zero.
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)Qb, (short)0, S * DP * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)Kb, (short)0, S * DP * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)Vb, (short)0, (int)(((S - 1) * vst + DP) * 4u), 0x00020000);
+    const int q0 = qblk * KQ_QB, q = q0 + lr;
+
+    // Q rows, pre-scaled (rows past S read zero; their lanes are never stored, and a lane's
+    // scores, max and sum never mix with another row's): all loads, then one wait
+    floatx4 qf[NCH];
+    {
+        const unsigned qo = (unsigned)(q * DP + 4 * lg) * 4u;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+            qf[c] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rq, qo + 64 * c, 0, 0));
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) qf[c] *= g.scale_log2;
+    }
+
+    const int nt = (S + A16_KB - 1) / A16_KB;
+    const int T = CAUSAL ? min(nt, min(S - 1, q0 + KQ_QB - 1) / A16_KB + 1) : nt;
+    // tiles [0, t_fast) lie wholly inside S and (causal) at or below the block's first row:
+    // no per-score test; with 16-row blocks only the last tile can need one
+    int t_fast = HAS_MASK ? 0 : S / A16_KB;
+    if (CAUSAL) t_fast = min(t_fast, (q0 + 1) / A16_KB);
+
+    floatx4 kf[2][NCH];
+    VW vf[2][4][NH];
+    // K rows 32t + 16b + lr, d 16c + 4lg .. +3 (A operand of Sᵀ = K·Qᵀ)
+    const unsigned ko = (unsigned)(lr * DP + 4 * lg) * 4u;
+    auto load_k = [&](int t) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const unsigned so = (unsigned)((t * A16_KB + 16 * b) * DP) * 4u;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c)
+                kf[b][c] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 64 * c, so, 0));
+        }
+    };
+    // V rows 32t + 16b + 4lg + rr, d 16W·h + W·lr .. +W−1 (A operand of Oᵀ = Vᵀ·Pᵀ)
+    const unsigned vo = (4 * lg * vst + W * lr) * 4u;
+    auto load_v = [&](int t) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const unsigned so = (unsigned)(t * A16_KB + 16 * b + rr) * vst * 4u;
+#pragma unroll
+                for (int h = 0; h < NH; ++h) {
+                    if constexpr (W == 4)
+                        vf[b][rr][h] = __builtin_bit_cast(
+                            VW, __builtin_amdgcn_raw_buffer_load_b128(rv, vo + 64 * W * h, so, 0));
+                    else
+                        vf[b][rr][h] = __builtin_bit_cast(
+                            VW, __builtin_amdgcn_raw_buffer_load_b64(rv, vo + 64 * W * h, so, 0));
+                }
+            }
+    };
+
+    floatx4 oacc[NCH];
+#pragma unroll
+    for (int b = 0; b < NCH; ++b) oacc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // m_run: reference max of this lane's row (the same in the row's 4 lanes); l_part: Σ p
+    // over the keys this lane holds — the row sum is the total over the 4 lanes
+    float m_run = -FLT_MAX, l_part = 0.f;
+
+    // This wavefront's tiles t = wave, wave + 4, ...: K of the next tile is fetched once the
+    // current scores are formed, V once the current P·V is issued.  (Issuing the next
+    // tile's scores before the current P·V, to run the softmax under the P·V MFMAs,
+    // measured slower: GPT-2 S1024 25.3 → 27.5 µs.)
+    int t = wave;
+    if (t < T) {
+        load_k(t);
+        load_v(t);
+    }
+    for (; t < T; t += KQ_WAVES) {
+        const int k0 = t * A16_KB;
+        // the prefetched tile; the last iteration loads its own tile again, so that every
+        // path has the same loads in flight and each wait counts exactly
+        const int tn = t + KQ_WAVES < T ? t + KQ_WAVES : t;
+        // Sᵀ for two 16-key blocks; register r of block b = key k0 + 16b + 4g + r
+        floatx4 sacc[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            sacc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < NCH; ++c)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    sacc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[b][c][i], qf[c][i], sacc[b], 0, 0, 0);
+        }
+        load_k(tn);
+
+        // p = 2^(s − m_run); m_run moves only when some lane's tile max exceeds it by more
+        // than ATTN_LAZY (log2 units): then the row max is taken across the row's 4 lanes
+        // and O and l_part are rescaled.  Tiles from t_fast apply the bounds, causal and
+        // additive-mask terms per score.
+        float tmax = -INFINITY;
+        if (t >= t_fast) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int kv = k0 + 16 * b + 4 * lg + r;
+                    float sv = sacc[b][r];
+                    if (HAS_MASK && kv < S && q < S) sv += g.mask[(bh * S + q) * (long long)S + kv] * LOG2E;
+                    if (kv >= S || (CAUSAL && kv > q)) sv = -INFINITY;
+                    sacc[b][r] = sv;
+                    tmax = fmaxf(tmax, sv);
+                }
+        } else {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sacc[b][r]);
+        }
+        if (__any(tmax > m_run + ATTN_LAZY)) {
+            const float m_new = fmaxf(m_run, rows4_max(tmax));
+            const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
+#pragma unroll
+            for (int db = 0; db < NCH; ++db) oacc[db] *= corr;
+            l_part *= corr;
+            m_run = m_new;
+        }
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = __builtin_amdgcn_exp2f(sacc[b][r] - m_run);
+                sacc[b][r] = p;
+                l_part += p;
+            }
+        // Oᵀ[d][q] += Σ_kv V[kv][d]·P[q][kv]; MFMA (b, r) takes key 16b + 4g + r from group g
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int h = 0; h < NH; ++h)
+#pragma unroll
+                    for (int w = 0; w < W; ++w)
+                        oacc[W * h + w] =
+                            __builtin_amdgcn_mfma_f32_16x16x4f32(vf[b][r][h][w], sacc[b][r], oacc[W * h + w], 0, 0, 0);
+        load_v(tn);
+        // keeps the V prefetch at the end of this iteration: otherwise the compiler merges it
+        // with the load before the loop into one load at the top of the next iteration, after
+        // which P·V waits for it
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const float l_row = rows4_sum(l_part);
+
+    // this wavefront's rows, relative to its own m_run, into LDS: register r of d block
+    // W·h + w holds d = 16W·h + W·(4g + r) + w
+    if (lg == 0) {
+        m_sh[wave][lr] = m_run;
+        l_sh[wave][lr] = l_row;
+    }
+#pragma unroll
+    for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            VW o;
+#pragma unroll
+            for (int w = 0; w < W; ++w) o[w] = oacc[W * h + w][r];
+            *reinterpret_cast<VW*>(&o_sh[wave][lr][16 * W * h + W * (4 * lg + r)]) = o;
+        }
+    __syncthreads();
+
+    // combine: thread → (row, 4 columns); the four partials in wavefront order
+    constexpr int TPR = DP / 4;
+#pragma unroll
+    for (int e0 = 0; e0 < KQ_QB * TPR; e0 += KQ_NT) {
+        const int e = e0 + tid;
+        const int row = e / TPR, d = (e % TPR) * 4;
+        const int qq = q0 + row;
+        if ((KQ_QB * TPR) % KQ_NT != 0 && e >= KQ_QB * TPR) break;
+        if (qq >= S || d >= D) continue;
+        float M = m_sh[0][row];
+#pragma unroll
+        for (int w = 1; w < KQ_WAVES; ++w) M = fmaxf(M, m_sh[w][row]);
+        float L = 0.f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int w = 0; w < KQ_WAVES; ++w) {
+            const float s = __builtin_amdgcn_exp2f(m_sh[w][row] - M);
+            L += s * l_sh[w][row];
+            const float4 p = *reinterpret_cast<const float4*>(&o_sh[w][row][d]);
+            acc.x += s * p.x;
+            acc.y += s * p.y;
+            acc.z += s * p.z;
+            acc.w += s * p.w;
+        }
+        const float inv_l = 1.0f / L;
+        acc.x *= inv_l;
+        acc.y *= inv_l;
+        acc.z *= inv_l;
+        acc.w *= inv_l;
+        float* dst = g.sk_defer ? g.part + (bh * S + qq) * (long long)D : attn_out_row(g, bh, qq);
+        *reinterpret_cast<float4*>(dst + d) = acc;
+    }
+}
+
+// Deferred output of attn_fwd_kq: rows staged in [bh, S, D] are stored to O
+// (or its fused [B, S, H, D] transpose) once every read of Q, K and V is done.
+__global__ __launch_bounds__(256) void attn_kq_flush(AttnArgs g) {
+    const int tpr = g.D / 4;
+    const long long t = blockIdx.x * 256LL + threadIdx.x;
+    const long long row = t / tpr;
+    const int d = (int)(t - row * tpr) * 4;
+    const long long bh = blockIdx.y;
+    if (row >= g.S) return;
+    *reinterpret_cast<float4*>(attn_out_row(g, bh, row) + d) =
+        *reinterpret_cast<const float4*>(g.part + (bh * g.S + row) * (long long)g.D + d);
+}
+
 // Combine the key-range partials of every query row whose block was split:
 // O = Σ_c 2^(m_c − M)·acc_c / Σ_c 2^(m_c − M)·l_c, M = max_c m_c, segments
 // summed in key order.  Rows of unsplit blocks return, unless g.sk_defer:
@@ -751,7 +1059,8 @@ __global__ __launch_bounds__(256) void attn_fwd_rows(AttnArgs g, int causal) {
 //          [9]=heads of a fused output transpose (0 = none) [10]=16x16 kernel (transpose fusable)
 //          [11]=key tiles per head (split) [12]=V row stride when V is read from the columns
 //          of a row-major tensor (0 = contiguous) [13]=K/V heads of that layout
-//          [14]=deferred output (split only: the merge kernel writes every row of O)
+//          [14]=deferred output (the merge kernel, or attn_kq_flush, writes every row of O)
+//          [15]=key-quartered kernel (attn_fwd_kq)
 AttnArgs make_args(const Step& s) {
     AttnArgs g;
     g.Q = (const float*)s.in[0];
@@ -822,6 +1131,36 @@ void launch_attn16(const Step& s, hipStream_t st) {
     hipLaunchKernelGGL((attn_fwd_mfma16<DP, CAUSAL, HAS_MASK>), dim3(gx, (unsigned)s.i[0]), dim3(A16_NT), 0, st, g);
 }
 
+// kq_plan's cache: one assignment per (heads, S, causal, CUs, workgroups per CU).
+std::mutex g_kq_mu;
+std::map<std::array<long long, 5>, std::vector<unsigned short>> g_kq_plans;
+
+template <int DP, bool CAUSAL, bool HAS_MASK>
+void launch_attn_kq(const Step& s, hipStream_t st) {
+    AttnArgs g = make_args(s);
+    if (g.S <= 0 || s.i[0] <= 0) return;
+    const int bh = (int)s.i[0];
+    g.o_heads = (int)s.i[9];
+    if (s.i[12]) {
+        g.v_ld = s.i[12];
+        g.v_heads = (int)s.i[13];
+    }
+    g.kq_nq = (g.S + KQ_QB - 1) / KQ_QB;
+    g.kq_bh = bh;
+    g.sk_defer = s.i[14] != 0;
+    g.part = g.sk_defer ? (float*)s.ws : nullptr;
+    g.ml = nullptr;
+    KqArgs k;
+    k.g = g;
+    const std::vector<unsigned short>& map = kq_plan(bh, g.S, CAUSAL, lbr_device_cus(), kq_per_cu(DP));
+    k.n_map = (int)map.size();
+    std::copy(map.begin(), map.end(), k.map);
+    hipLaunchKernelGGL((attn_fwd_kq<DP, CAUSAL, HAS_MASK>), dim3((unsigned)(g.kq_nq * bh)), dim3(KQ_NT), 0, st, k);
+    if (g.sk_defer)
+        hipLaunchKernelGGL(attn_kq_flush, dim3((unsigned)(((long long)g.S * (g.D / 4) + 255) / 256), (unsigned)bh),
+                           dim3(256), 0, st, g);
+}
+
 // Key tiles of query block q (host mirror of attn16_tiles).
 int attn16_block_tiles(int S, bool causal, int q) {
     const int nt = (S + A16_KB - 1) / A16_KB;
@@ -866,7 +1205,108 @@ step_fn pick16(bool causal, bool mask) {
     return mask ? launch_attn16<DP, false, true> : launch_attn16<DP, false, false>;
 }
 
+template <int DP>
+step_fn pick_kq(bool causal, bool mask) {
+    if (causal) return mask ? launch_attn_kq<DP, true, true> : launch_attn_kq<DP, true, false>;
+    return mask ? launch_attn_kq<DP, false, true> : launch_attn_kq<DP, false, false>;
+}
+
 }  // namespace
+
+const char* lbr_attn_step_name(const Step& s, bool v, bool t, int store) {
+    static const std::vector<std::string> table = [] {
+        std::vector<std::string> n;
+        for (int k = 0; k < 2; ++k)
+            for (int a = 0; a < 2; ++a)
+                for (int b = 0; b < 2; ++b)
+                    for (int c = 0; c < 3; ++c)
+                        n.push_back(std::string(k ? "attn_fwd_kq_f32" : "attn_fwd_mfma16_f32") + (a ? "+v" : "") +
+                                    (b ? "+transpose" : "") + (c == 1 ? "+defer" : c == 2 ? "+relay" : ""));
+        return n;
+    }();
+    const int kq = s.i[15] == 1;
+    return table[(((kq * 2 + (v ? 1 : 0)) * 2 + (t ? 1 : 0)) * 3) + (store < 0 || store > 2 ? 0 : store)].c_str();
+}
+
+// Whole heads, or alternate blocks of them, per XCD: the smallest P in
+// {1, 2, 4, 8} that divides the 16-row blocks and makes bh·P units (head h,
+// blocks b ≡ p mod P) a multiple of the 8 XCDs; *upx = units per XCD, 0 when
+// no P fits.
+void attn_kq_layout(long long bh, int S, int* P, int* upx) {
+    const int nq = (S + KQ_QB - 1) / KQ_QB;
+    *P = 1;
+    *upx = 0;
+    for (int p = 1; p <= 8; p *= 2)
+        if (p <= nq && nq % p == 0 && (bh * p) % 8 == 0) {
+            *P = p;
+            *upx = (int)(bh * p / 8);
+            return;
+        }
+}
+
+// Workgroups of attn_fwd_kq one CU holds at once (4 wavefronts each): the
+// register budget of 128 (hd ≤ 64) or 256 (hd 128) VGPRs leaves 4 or 2
+// wavefronts per SIMD.
+int kq_per_cu(int dp) { return dp <= 64 ? 4 : 2; }
+
+// The block each workgroup runs (LPT: longest processing time first).  With C
+// CUs, workgroup w = r·C + g is the r-th on CU g (XCD g mod 8).  Blocks are
+// taken heaviest first (causal: most key tiles) and each goes to the CU of its
+// head's XCD with the least load so far, ties to the CU with fewer slots left
+// (so the heaviest blocks get CUs of their own when some CUs hold fewer
+// workgroups), then the lowest index.  Empty (the kernel's own order) when the
+// grid does not fit on the CUs at once, or C is not a multiple of 8, or the
+// grid exceeds the kernel-argument table.
+const std::vector<unsigned short>& kq_plan(long long bh, int S, bool causal, int C, int per_cu) {
+    std::lock_guard<std::mutex> lock(g_kq_mu);
+    std::vector<unsigned short>& map = g_kq_plans[{bh, S, causal ? 1 : 0, C, per_cu}];
+    const int nq = (S + KQ_QB - 1) / KQ_QB;
+    const long long n = bh * nq;
+    if (!map.empty() || C <= 0 || C % 8 || n > (long long)per_cu * C || n > KQ_MAP_MAX) return map;
+    const int nt = (S + A16_KB - 1) / A16_KB;
+    auto weight = [&](int b) { return causal ? std::min(nt, std::min(S - 1, b * KQ_QB + KQ_QB - 1) / A16_KB + 1) : nt; };
+    int P, upx;
+    attn_kq_layout(bh, S, &P, &upx);
+    std::vector<int> items((size_t)n);
+    for (int i = 0; i < (int)n; ++i) items[i] = i;
+    std::stable_sort(items.begin(), items.end(), [&](int a, int b) { return weight(a % nq) > weight(b % nq); });
+    std::vector<long long> load(C, 0);
+    std::vector<int> used(C, 0), cap(C, 0);
+    for (int g = 0; g < C; ++g) cap[g] = g < n ? (int)((n - g + C - 1) / C) : 0;
+    std::vector<unsigned short> out((size_t)n);
+    for (int it : items) {
+        const int h = it / nq, b = it % nq;
+        const int x = upx > 0 ? (h * P + b % P) / upx : -1;
+        int best = -1;
+        for (int g = x < 0 ? 0 : x; g < C; g += x < 0 ? 1 : 8) {
+            if (used[g] >= cap[g]) continue;
+            if (best < 0 || load[g] < load[best] ||
+                (load[g] == load[best] && cap[g] - used[g] < cap[best] - used[best]))
+                best = g;
+        }
+        if (best < 0) return map;   // capacities do not match the XCD layout: keep the kernel's order
+        out[(size_t)used[best] * C + best] = (unsigned short)it;
+        ++used[best];
+        load[best] += weight(b);
+    }
+    map = out;
+    return map;
+}
+
+extern "C" int lbr_attn_kq_grid(long long bh, int seq, int causal, int cus, int* heads_out, int* blocks_out,
+                                int cap) {
+    if (bh <= 0 || seq <= 0) return 0;
+    KqArgs k;
+    k.g = AttnArgs();
+    k.g.kq_nq = (seq + KQ_QB - 1) / KQ_QB;
+    k.g.kq_bh = (int)bh;
+    const std::vector<unsigned short>& map = kq_plan(bh, seq, causal != 0, cus, kq_per_cu(64));
+    k.n_map = (int)map.size();
+    std::copy(map.begin(), map.end(), k.map);
+    const long long n = k.g.kq_nq * bh;
+    for (long long w = 0; w < n && w < cap; ++w) kq_item(k, (int)w, &heads_out[w], &blocks_out[w]);
+    return (int)n;
+}
 
 int decode_attention(const OpNode* n, Step* s) {
     const int seq = n->extra[0], hd = n->extra[1], causal = n->extra[2] != 0, has_mask = n->extra[3] != 0;
@@ -929,6 +1369,34 @@ int decode_attention(const OpNode* n, Step* s) {
             // one workgroup per minimum share.  No split when that gives no more
             // workgroups than the plain grid.  LBR_ATTN_SPLIT=<n> forces shares
             // of n tiles (0: no split), LBR_ATTN_SPLIT_WG=<n> n workgroups.
+            // Grids that leave CUs idle (fewer than two 8-wavefront workgroups per CU,
+            // not folded), head dim 32 or 64 (no padded columns): 16-row workgroups
+            // with the key tiles dealt over four wavefronts (attn_fwd_kq), no merge.
+            // GPT-2 S=1024: 33.1 µs + a 5.3 µs merge with the key-range split.
+            // LBR_ATTN_KQ=1 forces it for any unpadded head dim ≤ 128, 0 turns it off;
+            // a forced schedule (LBR_ATTN_FOLD / _TILE / _SPLIT / _SPLIT_WG) keeps it off.
+            {
+                const bool forced = getenv("LBR_ATTN_FOLD") || getenv("LBR_ATTN_SPLIT") || getenv("LBR_ATTN_SPLIT_WG");
+                bool kq = hd == dp && hd <= 64 && !s->i[6] && nq * bh < 2LL * cus && !forced;
+                const char* kqe = getenv("LBR_ATTN_KQ");
+                if (kqe) kq = atoi(kqe) != 0 && hd == dp;
+                const long long n16 = (seq + KQ_QB - 1) / KQ_QB;
+                // the kernel's buffer views address one head's rows with 32-bit byte offsets
+                if (kq && n16 * bh < (1LL << 31) && (long long)seq * hd * 4 < (1LL << 31)) {
+                    s->i[6] = 0;
+                    s->i[15] = 1;
+                    // staging rows of a deferred store (attn_kq_flush)
+                    s->ws_bytes = (size_t)bh * (size_t)seq * (size_t)hd * sizeof(float) + 256;
+                    switch (dp) {
+                        case 32: s->run = pick_kq<32>(causal, has_mask); break;
+                        case 64: s->run = pick_kq<64>(causal, has_mask); break;
+                        default: s->run = pick_kq<128>(causal, has_mask); break;
+                    }
+                    s->name = "attn_fwd_kq_f32";
+                    s->i[10] = 1;   // can write O as [B, S, H, D] and read a strided V, like the 16x16 kernel
+                    return LBR_OK;
+                }
+            }
             long long head_tiles = 0;
             for (int q = 0; q < nq; ++q) head_tiles += attn16_block_tiles(seq, causal != 0, q);
             const long long total = head_tiles * bh;

@@ -280,10 +280,11 @@ static void free_plan(lbr_plan* p) {
     delete p;
 }
 
-// Deferred split attentions whose output only the next GEMM reads write
-// into one plan-owned buffer instead (the steps run in order, and each
-// GEMM consumes the buffer before the next attention writes it); their
-// cut blocks alone then go through the merge kernel.
+// Deferred attentions whose output only the next GEMM reads write into one
+// plan-owned buffer instead (the steps run in order, and each GEMM consumes
+// the buffer before the next attention writes it): a split attention's cut
+// blocks alone then go through the merge kernel, a key-quartered one stores
+// its rows directly.
 static int relay_attention_outputs(lbr_plan* p, const OpNode* nodes, int n_nodes, const void* const* live_ptr,
                                    const size_t* live_bytes, int n_live) {
     std::vector<size_t> picks;
@@ -299,11 +300,10 @@ static int relay_attention_outputs(lbr_plan* p, const OpNode* nodes, int n_nodes
     for (size_t i : picks) {
         p->steps[i].out = p->relay;
         p->steps[i].i[14] = 0;
-        // the deferred names are "attn_fwd_mfma16_f32[+v][+transpose]+defer"
+        // the deferred names are "<kernel>[+v][+transpose]+defer"
         const char* nm = p->steps[i].name;
         const bool v = strstr(nm, "+v") != nullptr, t = strstr(nm, "+transpose") != nullptr;
-        p->steps[i].name = v ? (t ? "attn_fwd_mfma16_f32+v+transpose+relay" : "attn_fwd_mfma16_f32+v+relay")
-                             : (t ? "attn_fwd_mfma16_f32+transpose+relay" : "attn_fwd_mfma16_f32+relay");
+        p->steps[i].name = lbr_attn_step_name(p->steps[i], v, t, 2);
         p->steps[i + 1].in[0] = p->relay;
     }
     return LBR_OK;

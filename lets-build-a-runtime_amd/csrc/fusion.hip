@@ -675,12 +675,15 @@ bool match_attn_sliced_v(const OpNode* nodes, int n, int first, int at_i, const 
     }
     const int Hq = at->out_shape[1], group = at->extra[4] > 0 ? at->extra[4] : 1;
     if (as.i[10] != 1 || Hq != H * group) return false;   // the 16x16 kernel reads a strided V
+    // the key-quartered kernel addresses one head's V rows with 32-bit byte offsets
+    if (as.i[15] == 1 && ((long long)(S - 1) * ld + hd) * 4 >= (1LL << 31)) return false;
     const long long q_bytes = (long long)B * Hq * S * hd * 4;
     std::vector<Rng> reads{rng(at->inputs[0], q_bytes), rng(at->inputs[1], q_bytes / group),
                            rng(src, (long long)B * S * ld * 4)};
     if (at->extra[3] != 0) reads.push_back(rng(at->inputs[3], (long long)B * Hq * S * S * 4));
-    // under the key-range split the output may lie over what the kernel reads (deferred store)
-    const bool split = as.i[7] > 0;
+    // a schedule with a deferred store (key-range split, key-quartered kernel) lets the output
+    // lie over what the kernel reads
+    const bool split = lbr_attn_can_defer(as);
     const OpNode* tr = at_i + 1 < n ? &nodes[at_i + 1] : nullptr;
     int end = at_i + 1;
     Rng y = out_rng(at);
@@ -928,8 +931,9 @@ void lbr_input_extent(const OpNode* nd, int k, unsigned long long* lo, unsigned 
     *hi = r.hi;
 }
 
-// A split attention step whose output lies over its inputs stores every
-// row through the merge kernel (deferred output).  When the step right
+// An attention step whose output lies over its inputs stores every row
+// through a second kernel (deferred output: the key-range split's merge, or
+// attn_kq_flush).  When the step right
 // after it is a one-batch DMA GEMM whose A operand is exactly that output,
 // and no other read sees the output's bytes before they are overwritten or
 // at the end (live-out), the plan can give the attention a buffer of its
@@ -938,7 +942,7 @@ bool lbr_relay_ok(const OpNode* nodes, int n, const Step& at, const Step& gm, co
                   const size_t* live_bytes, int n_live) {
     const char* e = getenv("LBR_ATTN_RELAY");
     if (e && atoi(e) == 0) return false;
-    if (!at.name || strncmp(at.name, "attn_fwd_mfma16_f32", 19) != 0 || !at.i[7] || !at.i[14]) return false;
+    if (!at.name || strncmp(at.name, "attn_fwd_", 9) != 0 || !lbr_attn_can_defer(at) || !at.i[14]) return false;
     if (!gm.name || strncmp(gm.name, "gemm_dma_f32_nt", 15) != 0 || gm.in[0] != at.out || gm.i[3] != 1 || gm.i[35])
         return false;
     const long long yb = at.i[0] * at.i[1] * at.i[2] * 4;
@@ -1157,12 +1161,13 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
                 std::vector<Rng> reads{rng(nd->inputs[0], qkv), rng(nd->inputs[1], qkv / group),
                                        rng(nd->inputs[2], qkv / group)};
                 if (mask) reads.push_back(rng(nd->inputs[3], (long long)B * H * S * S * 4));
-                // under the key-range split the output may lie over them (deferred store),
-                // unless the transpose can go into the next GEMM instead, which costs nothing
+                // with a deferred store (key-range split, key-quartered kernel) the output may
+                // lie over them, unless the transpose can go into the next GEMM instead, which
+                // costs nothing
                 const Rng y = out_rng(tr);
                 const bool over = any_overlap(y, reads);
                 FusedRun tg;
-                const bool ok = !over || (as.i[7] > 0 && !match_transpose_gemm(nodes, n, i + 1, live, &tg));
+                const bool ok = !over || (lbr_attn_can_defer(as) && !match_transpose_gemm(nodes, n, i + 1, live, &tg));
                 if (ok && dead_after(nodes, n, i + 2, {out_rng(nd)}, {y}, live)) {
                     FusedRun f;
                     f.first = i;
@@ -1309,14 +1314,14 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
         }
         s->out = (void*)f.out;
         s->i[9] = f.Hs[0];
-        s->name = "attn_fwd_mfma16_f32+transpose";
+        s->name = lbr_attn_step_name(*s, false, true, 0);
         if (f.defer) {
-            if (s->i[7] <= 0) {
-                lbr_set_error("fusion: attention node %d writes over its inputs without the split", f.first);
+            if (!lbr_attn_can_defer(*s)) {
+                lbr_set_error("fusion: attention node %d writes over its inputs without a deferred store", f.first);
                 return LBR_ERR_INVALID;
             }
             s->i[14] = 1;
-            s->name = "attn_fwd_mfma16_f32+transpose+defer";
+            s->name = lbr_attn_step_name(*s, false, true, 1);
         }
     } else if (f.kind == LBR_FUSE_ATTN_SLICED_V) {
         const int at = f.first + f.attn_at;
@@ -1332,14 +1337,14 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
         s->out = (void*)f.out;
         const bool tout = f.count == f.attn_at + 2;   // the output TRANSPOSE(H,S) joined the run
         if (tout) s->i[9] = f.Hs[0];
-        s->name = tout ? "attn_fwd_mfma16_f32+v+transpose" : "attn_fwd_mfma16_f32+v";
+        s->name = lbr_attn_step_name(*s, true, tout, 0);
         if (f.defer) {
-            if (s->i[7] <= 0) {
-                lbr_set_error("fusion: attention node %d writes over its inputs without the split", at);
+            if (!lbr_attn_can_defer(*s)) {
+                lbr_set_error("fusion: attention node %d writes over its inputs without a deferred store", at);
                 return LBR_ERR_INVALID;
             }
             s->i[14] = 1;
-            s->name = tout ? "attn_fwd_mfma16_f32+v+transpose+defer" : "attn_fwd_mfma16_f32+v+defer";
+            s->name = lbr_attn_step_name(*s, true, tout, 1);
         }
     } else if (f.kind == LBR_FUSE_TRANSPOSE_GEMM) {
         int rc = decode_matmul(&nodes[f.first + 1], s);

@@ -371,6 +371,15 @@ bool gemm_dma_split2(Step* s);
 bool gemm_dma_retile(Step* s, int tile);
 int gemm_dma_written(const Step& s, void** ptr, size_t* bytes, int cap);
 int decode_attention(const OpNode* n, Step* s);
+// Whether a decoded attention step can defer its store (its rows staged, then
+// written by a second kernel after every read of Q, K and V, so that O may lie
+// over them): the key-range split (merge kernel) and the key-quartered kernel
+// (attn_kq_flush).
+inline bool lbr_attn_can_defer(const Step& s) { return s.i[7] > 0 || s.i[15] == 1; }
+// Step name of an attention: its kernel, then "+v" (V read from a row-major
+// source), "+transpose" (O stored as [B, S, H, D]) and, for store 1 / 2,
+// "+defer" / "+relay".
+const char* lbr_attn_step_name(const Step& s, bool v, bool t, int store);
 // Fused MLP (mlp.hip): whether rows of width D, hidden H and output D2 fit
 // the one-kernel form; its launcher (Step layout in mlp.hip).
 bool mlp_shape_ok(long long M, long long D, long long H, long long D2);

@@ -265,7 +265,8 @@ class CompiledExecutor(Executor):
     def step_params(self) -> list[dict]:
         """Every kernel step of the compiled plan: its kernel (and full step name, with the
         fused parts), the nodes it covers, and the schedule its launch arguments encode
-        (attention: causal fold, key-range split workgroups, deferred output; GEMM: DMA tile
+        (attention: causal fold, key-range split workgroups, deferred output, key-quartered
+        16-row kernel; GEMM: DMA tile
         index, K ranges, norm prologue, norm in the split-K reduce and whether the split was
         made for it; head prologue: float4 kernel or one wavefront per row, and
         how many Q/K parts one launch covers)."""
@@ -280,8 +281,8 @@ class CompiledExecutor(Executor):
             lib.check(lib.lbr_plan_step_args(h, st, ints, 40), "lbr_plan_step_args")
             d = {"kernel": names[first.value].split("+")[0], "name": names[first.value], "first": first.value,
                  "count": count.value, "kind": FUSE_KINDS.get(kind.value, "?")}
-            if d["kernel"].startswith("attn_fwd_mfma16"):
-                d.update(fold=bool(ints[6]), split_wg=int(ints[7]), defer=bool(ints[14]))
+            if d["kernel"].startswith(("attn_fwd_mfma16", "attn_fwd_kq")):
+                d.update(fold=bool(ints[6]), split_wg=int(ints[7]), defer=bool(ints[14]), kq=bool(ints[15]))
             elif d["kernel"].startswith("gemm_"):
                 d.update(ksplit=max(1, int(ints[10])), dma_tile=int(ints[14]) - 1, norm=int(ints[15]),
                          reduce_norm=int(ints[16]), split_for_norm=bool(int(ints[17]) & 256))

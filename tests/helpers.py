@@ -30,11 +30,16 @@ def one_node_graph(op: OpType, inputs: dict[str, np.ndarray], out_shape, attrs=N
     return g
 
 
-def run_gpu(graph: Graph, inputs: dict[str, np.ndarray], use_graph: bool = True) -> np.ndarray:
+def run_gpu(graph: Graph, inputs: dict[str, np.ndarray], use_graph: bool = True,
+            kernels: list | None = None) -> np.ndarray:
+    """The graph's first output through the compiled executor; `kernels` (a list) receives
+    the plan's step names."""
     from runtime.executor.compiled import CompiledExecutor
     ex = CompiledExecutor(use_graph=use_graph)
     ex.compile(plan(graph))
     try:
+        if kernels is not None:
+            kernels.extend(ex.kernel_names())
         return ex.run(inputs)[graph.outputs[0]]
     finally:
         ex.close()

@@ -16,8 +16,8 @@ from conftest import normwise_rel
 pytestmark = pytest.mark.gpu
 
 
-def _check(graph, inputs, ref, tol):
-    y = run_gpu(graph, inputs)
+def _check(graph, inputs, ref, tol, kernels=None):
+    y = run_gpu(graph, inputs, kernels=kernels)
     o = run_oracle(graph, inputs)
     assert y.shape == ref.shape
     e_gpu, e_orc, e_go = normwise_rel(y, ref), normwise_rel(o, ref), normwise_rel(y, o)
@@ -163,7 +163,7 @@ ATTN_CASES = [
 ]
 
 
-def _attention_case(B, H, S, hd, causal, group):
+def _attention_case(B, H, S, hd, causal, group, kernel=None):
     r = rng(S * 3 + hd + H)
     q = randn(r, B, H, S, hd)
     k = randn(r, B, H // group, S, hd)
@@ -173,7 +173,10 @@ def _attention_case(B, H, S, hd, causal, group):
         attrs["group_size"] = group
     g = one_node_graph(OpType.ATTENTION, {"q": q, "k": k, "v": v}, (B, H, S, hd), attrs)
     ref = cf_attention(q, k, v, causal=causal, group=group)
-    _check(g, {"q": q, "k": k, "v": v}, ref, 1e-4)
+    names = []
+    _check(g, {"q": q, "k": k, "v": v}, ref, 1e-4, kernels=names)
+    if kernel is not None:
+        assert names == [kernel], names
 
 
 @pytest.mark.parametrize("B,H,S,hd,causal,group", ATTN_CASES)
@@ -210,10 +213,50 @@ def test_attention_schedules(monkeypatch, env, B, H, S, hd, causal, group):
     _attention_case(B, H, S, hd, causal, group)
 
 
+# The key-quartered kernel: 16 query rows per workgroup, the key tiles dealt over its four
+# wavefronts, partial rows combined in LDS.  It takes small grids of head dim 32 or 64 by
+# default (GPT-2 and GPT-2-width); LBR_ATTN_KQ=1 forces it for head dims 32, 64 and 128.
+# Cases: blocks with fewer tiles than wavefronts (S ≤ 96), S not a multiple of 16 or 32
+# (clamped rows past S), GQA, batches, the XCD layout with alternate blocks (12 heads) and
+# without (5 and 3 heads), head dim 128.
+KQ_CASES = [
+    (1, 4, 32, 32, True, 1),
+    (1, 4, 32, 32, False, 1),
+    (2, 3, 7, 64, True, 1),
+    (1, 2, 1, 64, True, 1),
+    (1, 2, 100, 64, False, 1),
+    (1, 12, 512, 64, True, 1),
+    (1, 12, 1024, 64, True, 1),
+    (1, 5, 1000, 32, True, 1),
+    (2, 8, 200, 64, True, 4),
+    (1, 4, 257, 128, True, 1),
+    (1, 8, 300, 128, False, 4),
+    (1, 32, 256, 128, True, 4),
+    (1, 16, 333, 64, False, 2),
+]
+
+
+@pytest.mark.parametrize("B,H,S,hd,causal,group", KQ_CASES)
+def test_attention_kq(monkeypatch, B, H, S, hd, causal, group):
+    monkeypatch.setenv("LBR_ATTN_KQ", "1")
+    _attention_case(B, H, S, hd, causal, group, kernel="attn_fwd_kq_f32")
+
+
+@pytest.mark.parametrize("B,H,S,hd", [(1, 12, 512, 64), (1, 12, 1024, 64), (1, 4, 32, 16)])
+def test_attention_small_grid_default(B, H, S, hd):
+    # the schedule small grids take by default: the key-quartered kernel for head dim 32 / 64,
+    # the 16x16 kernel (here with the padded head dim 16) otherwise
+    kernel = "attn_fwd_kq_f32" if hd in (32, 64) else "attn_fwd_mfma16_f32"
+    _attention_case(B, H, S, hd, True, 1, kernel=kernel)
+
+
 @pytest.mark.parametrize("S", [16, 300])
-@pytest.mark.parametrize("split", ["0", "2"])
+@pytest.mark.parametrize("split", ["0", "2", "kq"])
 def test_attention_mask(monkeypatch, S, split):
-    monkeypatch.setenv("LBR_ATTN_SPLIT", split)
+    if split == "kq":
+        monkeypatch.setenv("LBR_ATTN_KQ", "1")
+    else:
+        monkeypatch.setenv("LBR_ATTN_SPLIT", split)
     r = rng(S)
     B, H, hd = 1, 2, 64
     q, k, v = randn(r, B, H, S, hd), randn(r, B, H, S, hd), randn(r, B, H, S, hd)

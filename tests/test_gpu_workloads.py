@@ -55,7 +55,7 @@ def test_workload_parity(key, seq):
 # case reaches.
 @pytest.mark.parametrize("key,seq,kernels", [
     ("7b4k", None, {"attn_fwd_mfma16_f32", "gemm_dma_f32_nt"}),
-    ("gpt2_lm", None, {"attn_fwd_mfma16_f32", "gemm_dma_f32_nt"}),
+    ("gpt2_lm", None, {"attn_fwd_kq_f32", "gemm_dma_f32_nt"}),
     ("qwen3_4b_lm", None, {"attn_fwd_mfma16_f32", "gemm_dma_f32_nt"}),
 ])
 def test_workload_parity_full_size(key, seq, kernels):

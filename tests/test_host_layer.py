@@ -305,3 +305,42 @@ def test_dynamic_seq_resolve():
             ref = m(torch.from_numpy(x)).numpy()
         y = OracleRun(p).run({r.inputs[0]: x})[r.outputs[0]]
         np.testing.assert_allclose(y, ref, atol=1e-4)
+
+
+@pytest.mark.parametrize("bh,seq,causal", [(12, 1024, 1), (12, 512, 1), (4, 32, 1), (32, 1024, 1), (5, 1000, 1),
+                                           (3, 7, 1), (1, 1, 1), (2, 130, 0), (8, 300, 1), (6, 48, 0), (16, 17, 1),
+                                           (24, 1024, 1), (96, 1024, 1)])
+def test_attn_kq_grid_covers_every_block_once(bh, seq, causal):
+    """The key-quartered attention grid (host mirror of the launch's assignment and the kernel's
+    index arithmetic): every (head, 16-row block) exactly once.  When the grid fits on the 256
+    CUs at once (4 workgroups a CU), workgroups w, w + 256, ... share CU w mod 256 (XCD w mod 8):
+    the busiest CU carries at most the heaviest block more than the average load, and each XCD
+    holds whole heads or alternate blocks of them.  Otherwise block levels run heaviest first."""
+    import ctypes
+    from runtime.executor.hip_lib import open_library
+    lib = open_library()
+    nq, C = (seq + 15) // 16, 256
+    n = bh * nq
+    heads, blocks = (ctypes.c_int * n)(), (ctypes.c_int * n)()
+    assert lib.lbr_attn_kq_grid(bh, seq, causal, C, heads, blocks, n) == n
+    pairs = sorted(zip(heads[:n], blocks[:n]))
+    assert pairs == [(h, b) for h in range(bh) for b in range(nq)]
+    nt = (seq + 31) // 32
+
+    def tiles(b):
+        return min(nt, min(seq - 1, 16 * b + 15) // 32 + 1) if causal else nt
+
+    P = next((p for p in (1, 2, 4, 8) if p <= nq and nq % p == 0 and bh * p % 8 == 0), None)
+    if n > 4 * C or P is None and n > 4 * C:
+        # the kernel's own order: block levels from the last (heaviest under causal masking) down
+        assert [blocks[w] for w in range(n)] == sorted(blocks[:n], reverse=True)
+        return
+    load = [0] * C
+    for w in range(n):
+        load[w % C] += tiles(blocks[w])
+    heaviest = max(tiles(b) for b in range(nq))
+    assert max(load) <= sum(load) / min(n, C) + heaviest, (max(load), sum(load) / min(n, C))
+    if P is not None:
+        for x in range(8):
+            mine = {(heads[w], blocks[w] % P) for w in range(x, n, 8)}
+            assert len(mine) == bh * P // 8
