@@ -225,6 +225,53 @@ def calibrate_copy(mib: int) -> int:
     return 0 if ok else 1
 
 
+def memory_floor(rows: int = 1024, cols: int = 2560, reps: int = 20) -> int:
+    """The memory-bound floor beside the norms, in one process: the library's float4
+    copy (a RESHAPE of an external buffer) of rows·cols floats, then RMSNORM and
+    LAYERNORM over the same [rows, cols] (Qwen3-4B's hidden rows at S=1024), each
+    launched `reps` times through lbr_execute.  Under ``rocprofv3 --kernel-trace``
+    the three kernels' mean durations compare the norms' one read + one write of
+    the rows with a plain copy of the same bytes."""
+    import struct
+    from runtime.executor.common import COpNode
+    from runtime.executor.hip_lib import load_library
+    lib = load_library(0)
+    n = rows * cols * 4
+    r = np.random.default_rng(0)
+    x_h = r.standard_normal(rows * cols).astype(np.float32)
+    w_h = r.standard_normal(cols).astype(np.float32)
+    x, y, w, b = lib.alloc(n), lib.alloc(n), lib.alloc(cols * 4), lib.alloc(cols * 4)
+    lib.h2d(x, x_h.ctypes.data, n)
+    lib.h2d(w, w_h.ctypes.data, cols * 4)
+    lib.h2d(b, w_h.ctypes.data, cols * 4)
+
+    def node(op, inputs, eps=None):
+        nd = (COpNode * 1)()
+        nd[0].op = op
+        nd[0].n_inputs = len(inputs)
+        for k, p_ in enumerate(inputs):
+            nd[0].inputs[k] = p_
+        nd[0].output = y
+        if op == 500:   # RESHAPE: a flat copy
+            nd[0].n_dims, nd[0].out_shape[0] = 1, rows * cols
+        else:
+            nd[0].n_dims, nd[0].out_shape[0], nd[0].out_shape[1] = 2, rows, cols
+            nd[0].extra[0] = struct.unpack("<i", struct.pack("<f", eps))[0]
+        nd[0].elem_size = 4
+        return nd
+
+    out = {"memory_floor": {"rows": rows, "cols": cols, "reps": reps, "bytes_read": n, "bytes_written": n}}
+    for name, nd in (("copy", node(500, [x])), ("rmsnorm", node(601, [x, w], 1e-6)),
+                     ("layernorm", node(600, [x, w, b], 1e-5))):
+        for _ in range(reps):
+            lib.check(lib.lbr_execute(nd, 1), f"lbr_execute({name})")
+        out["memory_floor"][name] = "ok"
+    for p_ in (x, y, w, b):
+        lib.free(p_)
+    print(json.dumps(out))
+    return 0
+
+
 # ---------------------------------------------------------------- host facts
 
 def host_facts() -> dict:
@@ -399,6 +446,9 @@ def main() -> int:
     ap.add_argument("--nodes", action="store_true", help="log every node's device time and roofline fraction")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run the library's copy kernel over MIB MiB, 5 times (reference for HBM counters)")
+    ap.add_argument("--memory-floor", action="store_true",
+                    help="only run the copy kernel, RMSNORM and LAYERNORM over the same 1024x2560 rows, 20 times "
+                         "each (the memory-bound floor beside the norms, for rocprofv3 --kernel-trace)")
     ap.add_argument("--save-graph", metavar="STEM",
                     help="only export the --config workload and write STEM.json + STEM.weights")
     ap.add_argument("--graph", metavar="STEM",
@@ -406,6 +456,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.calibrate_copy:
         return calibrate_copy(args.calibrate_copy)
+    if args.memory_floor:
+        return memory_floor()
     if args.save_graph:
         from workloads import export_workload
         _, _, graph = export_workload(args.config or HEADLINE)
