@@ -12,9 +12,12 @@ library stream is reported beside it).  value = tokens/s = batch·seq /
 
 With no --config the headline is the 7B-shaped block at S=4096 (BASELINE
 configs[3]) and `configs` carries the same measurement for every BASELINE
-shape in order (toy, gpt2w, gpt2, 7b4k, qwen3_4b), each with its own
-latency, roofline, kernel table, parity and CPU baseline; --config KEY
-measures one workload only.
+shape in order (toy, gpt2w, gpt2, 7b4k, qwen3_4b), then the two full language
+models the reference publishes latencies for (gpt2_lm: GPT-2 with embeddings
+and LM head, qwen3_4b_lm: the Qwen3-4B-shaped body with embeddings and LM
+head, both at S=1024), each with its own latency, roofline, kernel table,
+schedule (GEMM tiles and K ranges, attention kernel), parity and CPU
+baseline; --config KEY measures one workload only.
 
 Also reported, on the same JSON line:
   roofline      dominant kernel (largest share of device time): algorithmic
@@ -397,8 +400,11 @@ def measure(key: str, args, graph_stem: str | None = None, min_timed_ms: float =
             cpu = {"value": round(tokens / cpu_s, 2), "unit": "tokens/s", "cores": num_threads(),
                    "kind": "port", "ms_per_step": round(cpu_s * 1e3, 2), "runs": len(times) - 1,
                    "statistic": "median of 3 forwards after 1 warm-up",
-                   "sample": f"whole forward of the same workload ({title}) on the CPU oracle (C restatement of "
-                             f"the reference compiled executor, OpenMP), same plan and input"}
+                   "sample": f"whole forward of the same workload ({title}) on the CPU oracle, same plan and "
+                             f"input: a C restatement of the reference compiled executor that differs from its "
+                             f"Linux schedule in two ways: the attention batch x head loop runs in parallel "
+                             f"(OpenMP; the reference's Linux loop is serial, csrc/ops.h:56-57) and the GEMMs use "
+                             f"the oracle's own cache-blocked OpenMP sgemm, not OpenBLAS cblas_sgemm"}
             log(f"[bench] cpu oracle: {cpu_s * 1e3:.2f} ms/forward (median of {len(times) - 1}) on "
                 f"{num_threads()} threads")
 
@@ -423,6 +429,8 @@ def measure(key: str, args, graph_stem: str | None = None, min_timed_ms: float =
                      else dom["bytes_per_launch"]},
         "kernels": [{k: r[k] for k in ("kernel", "launches", "ms_per_step", "share", "achieved", "unit", "frac",
                                        "mean_launch_us")} for r in rows],
+        "schedule": [{k: v for k, v in p.items() if k not in ("first", "count", "kernel")}
+                     for p in ex.step_params() if p["kernel"].startswith(("gemm_", "attn_"))],
         "parity": parity,
         "cpu_baseline": cpu,
     }
@@ -472,21 +480,21 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
-    from workloads import CONFIG_ORDER
+    from workloads import CONFIG_ORDER, LM_ORDER
     if args.graph:
         head = measure(Path(args.graph).name, args, graph_stem=args.graph)
         others = []
     else:
         head_key = args.config or HEADLINE
         head = measure(head_key, args)
-        others = [] if args.config else [k for k in CONFIG_ORDER if k != head_key]
+        others = [] if args.config else [k for k in CONFIG_ORDER + LM_ORDER if k != head_key]
     per_shape = []
     for k in others:
         per_shape.append(measure(k, args, min_timed_ms=30.0))
     if per_shape:
         by_key = {r["workload"]: r for r in per_shape}
         by_key[head["workload"]] = dict(head, headline=True)
-        per_shape = [by_key[k] for k in CONFIG_ORDER if k in by_key]
+        per_shape = [by_key[k] for k in CONFIG_ORDER + LM_ORDER if k in by_key]
 
     cpu = head["cpu_baseline"]
     if cpu is not None:

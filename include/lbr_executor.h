@@ -276,6 +276,11 @@ unsigned lbr_tiny_fast_div(unsigned x, unsigned d);
 int lbr_attn_kq_grid(long long bh, int seq, int causal, int cus,
                      int* heads_out, int* blocks_out, int cap);
 
+/* Name ("64x64", "32x48s4" ...) of DMA GEMM tile index `tile` (the value
+ * lbr_plan_step_args reports in [14], less one), "" for other indices: for
+ * reports, no counterpart in the reference. */
+const char* lbr_gemm_tile_name(int tile);
+
 /* The decoded integer launch arguments of step `step` (up to `cap` of them,
  * 40 at most), for tests and reports.  Their meaning is the kernel's: for
  * the attention kernel [6] = causal blocks folded in pairs, [7] = key-range

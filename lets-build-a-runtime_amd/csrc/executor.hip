@@ -317,19 +317,53 @@ static bool bad_live(const void* const* live_ptr, const size_t* live_bytes, int 
     return n_live < 0 || (n_live > 0 && (!live_ptr || !live_bytes));
 }
 
-// Measured tile choice for small one-batch, unsplit DMA GEMMs (2^24 to 2^34
-// flops: larger ones run on the big tiles, which the model ranks well; smaller
-// ones last a few µs, which launch gaps would swamp).  Every candidate tile of
-// the step's family runs once to warm up, then three timed batches of three
-// launches, the fastest batch counting; a tile at least 3% faster than the
-// model's choice replaces it.  Every tile
-// sums each output's K terms in the same order, so the choice never changes a
-// result bit.  The ranges the step writes are saved first and restored after,
-// so plan creation leaves memory as it found it.  LBR_GEMM_AUTOTUNE=0, or a
-// tile forced by LBR_GEMM_TILE, keeps the model's choice.
+// Measured tiles of the workloads' GEMM steps (MI355X): where repeated plan
+// creations with the timing below picked another tile than the model.  A listed
+// step (same step name and M, N, K) takes its tile without timing, so plans
+// come out the same run to run; the model's pick holds for every other step.
+// Every tile sums each output's K terms in the same order: the choice never
+// changes a result bit.
+struct TunedTile {
+    const char* step;
+    long long M, N, K;
+    const char* tile;
+};
+static const TunedTile kTunedTiles[] = {
+    // GPT-2-width QKV and FFN1 (512 rows): 64×64 leaves a fractional last round
+    // of 4-workgroup CUs; 24.9 µs against 31.0 and 26.8 against 31.3
+    {"gemm_dma_f32_nt+heads", 512, 2304, 768, "32x48"},
+    {"gemm_dma_f32_nt+act", 512, 3072, 768, "32x48"},
+    // GPT-2 QKV (1024 rows): 4 of 6 timings, 40.6 µs against 43.8 for 64×64
+    {"gemm_dma_f32_nt+heads", 1024, 2304, 768, "32x48s4"},
+};
+
+// Tile choice at plan creation.  A step listed in kTunedTiles takes its tile.
+// LBR_GEMM_AUTOTUNE=1 also times every other small one-batch, unsplit DMA GEMM
+// (2^24 to 2^34 flops: larger ones run on the big tiles, which the model ranks
+// well; smaller ones last a few µs, which launch gaps would swamp) over every
+// tile its launcher family has — one warm-up launch, then three timed batches
+// of three launches, the fastest batch counting — and a tile at least 3% faster
+// than the model's choice replaces it; LBR_GEMM_AUTOTUNE=2 times the listed
+// steps too (to regenerate the table); LBR_GEMM_AUTOTUNE=0, or a tile forced
+// by LBR_GEMM_TILE, keeps the model's choice everywhere.  The ranges a timed
+// step writes are saved first and restored after, so plan creation leaves
+// memory as it found it.
 static int autotune_gemms(std::vector<Step>& steps) {
     const char* env = getenv("LBR_GEMM_AUTOTUNE");
-    if ((env && atoi(env) == 0) || getenv("LBR_GEMM_TILE")) return LBR_OK;
+    const int mode = env ? atoi(env) : -1;   // -1: the table only
+    if (mode == 0 || getenv("LBR_GEMM_TILE")) return LBR_OK;
+    std::vector<char> tabled(steps.size(), 0);
+    if (mode != 2)
+        for (size_t i = 0; i < steps.size(); ++i) {
+            Step& s = steps[i];
+            if (!s.name || strncmp(s.name, "gemm_dma_f32", 12) != 0 || !s.i[14] || s.i[10] > 1 || s.i[3] != 1) continue;
+            for (const TunedTile& t : kTunedTiles)
+                if (strcmp(s.name, t.step) == 0 && s.i[0] == t.M && s.i[1] == t.N && s.i[2] == t.K) {
+                    const int tile = gemm_dma_tile_by_name(t.tile);
+                    if (tile >= 0 && gemm_dma_retile(&s, tile)) tabled[i] = 1;
+                }
+        }
+    if (mode < 1) return LBR_OK;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     void* save = nullptr;
     size_t save_cap = 0;
@@ -337,7 +371,7 @@ static int autotune_gemms(std::vector<Step>& steps) {
     if (err == hipSuccess) err = hipEventCreate(&e1);
     for (size_t i = 0; i < steps.size() && err == hipSuccess; ++i) {
         Step& s = steps[i];
-        if (!s.name || strncmp(s.name, "gemm_dma_f32", 12) != 0) continue;
+        if (!s.name || strncmp(s.name, "gemm_dma_f32", 12) != 0 || tabled[i]) continue;
         int cand[16];
         const int nc = gemm_dma_tune_candidates(s, cand, 16);
         // below 2^24 flops a launch lasts a few µs and the timing measures launch

@@ -1320,6 +1320,16 @@ int gemm_dma_tune_candidates(const Step& s, int* tiles, int cap) {
     return n;
 }
 
+extern "C" const char* lbr_gemm_tile_name(int tile) {
+    return tile >= 0 && tile < kNumDmaTiles ? kDmaTiles[tile].name : "";
+}
+
+int gemm_dma_tile_by_name(const char* name) {
+    for (int t = 0; t < kNumDmaTiles; ++t)
+        if (name && strcmp(name, kDmaTiles[t].name) == 0) return t;
+    return -1;
+}
+
 bool gemm_dma_retile(Step* s, int tile) {
     const step_fn run = dma_family_launcher(*s, tile);
     if (!run) return false;

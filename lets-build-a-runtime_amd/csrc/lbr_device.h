@@ -369,6 +369,8 @@ bool gemm_dma_tile_pairs(int tile);
 // norm); false leaves the step unchanged.
 bool gemm_dma_split2(Step* s);
 bool gemm_dma_retile(Step* s, int tile);
+// Index of the DMA tile called `name` ("32x48", "64x64" ...), or -1.
+int gemm_dma_tile_by_name(const char* name);
 int gemm_dma_written(const Step& s, void** ptr, size_t* bytes, int cap);
 int decode_attention(const OpNode* n, Step* s);
 // Whether a decoded attention step can defer its store (its rows staged, then

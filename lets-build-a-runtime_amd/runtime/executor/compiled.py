@@ -284,7 +284,9 @@ class CompiledExecutor(Executor):
             if d["kernel"].startswith(("attn_fwd_mfma16", "attn_fwd_kq")):
                 d.update(fold=bool(ints[6]), split_wg=int(ints[7]), defer=bool(ints[14]), kq=bool(ints[15]))
             elif d["kernel"].startswith("gemm_"):
-                d.update(ksplit=max(1, int(ints[10])), dma_tile=int(ints[14]) - 1, norm=int(ints[15]),
+                d.update(m=int(ints[0]), n=int(ints[1]), k=int(ints[2]),
+                         tile=lib.lbr_gemm_tile_name(int(ints[14]) - 1).decode() or "legacy",
+                         ksplit=max(1, int(ints[10])), dma_tile=int(ints[14]) - 1, norm=int(ints[15]),
                          reduce_norm=int(ints[16]), split_for_norm=bool(int(ints[17]) & 256))
             elif d["kind"] == "head_prologue":
                 d.update(vec=bool(ints[13]), parts=int(ints[14]) if ints[13] else 1)

@@ -82,6 +82,7 @@ class HipLibrary:
             "lbr_plan_step_info": ([c_vp, c_int, P(c_int), P(c_int), P(c_int)], c_int),
             "lbr_plan_step_args": ([c_vp, c_int, P(ctypes.c_longlong), c_int], c_int),
             "lbr_tiny_fast_div": ([ctypes.c_uint, ctypes.c_uint], ctypes.c_uint),
+            "lbr_gemm_tile_name": ([c_int], c_char_p),
             "lbr_attn_kq_grid": ([ctypes.c_longlong, c_int, c_int, c_int, P(c_int), P(c_int), c_int], c_int),
         }
         for name, (args, res) in sig.items():

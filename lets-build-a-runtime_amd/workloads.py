@@ -198,6 +198,9 @@ WORKLOADS: dict[str, Workload] = {
 
 # BASELINE.json configs[i] → workload key
 CONFIG_ORDER = ["toy", "gpt2w", "gpt2", "7b4k", "qwen3_4b"]
+# the full language models (embeddings + LM head) the reference quotes latencies for
+# (README.md:41-57), measured after the BASELINE shapes
+LM_ORDER = ["gpt2_lm", "qwen3_4b_lm"]
 
 
 def export_workload(key: str, seed: int = 0, seq_len: int | None = None):

@@ -1,6 +1,9 @@
-"""Measured GEMM tile choice at plan creation (LBR_GEMM_AUTOTUNE, on by
-default): small one-batch, unsplit DMA GEMMs are timed over every tile their
-launcher family has, and the fastest replaces the model's choice.
+"""GEMM tile choice at plan creation.  By default a committed table of measured
+tiles (kTunedTiles) sets the tile of the workloads' listed GEMM steps and the
+model's pick holds elsewhere, so a plan is the same run to run.
+LBR_GEMM_AUTOTUNE=1 also times the other small one-batch, unsplit DMA GEMMs
+over every tile their launcher family has, and the fastest replaces the
+model's choice; LBR_GEMM_AUTOTUNE=0 keeps the model's pick everywhere.
 
 Every DMA tile sums each output's K terms in the same order (K steps in
 order, the same 4-wide MFMA reduction inside a step), so a tuned plan and
@@ -102,3 +105,28 @@ def test_autotune_workload_bitwise(monkeypatch, key, seq):
             ex.close()
     print(f"{key} S={seq}: DMA tiles tuned {tiles['1']} model {tiles['0']}")
     np.testing.assert_array_equal(outs["1"], outs["0"])
+
+
+def test_default_plan_takes_the_table_tiles_every_time():
+    """GPT-2-width at S=512: the QKV (heads) and FFN1 (activation) GEMMs take the table's
+    32x48 tile, the other GEMMs the model's, identically in every plan creation."""
+    from runtime.executor.compiled import CompiledExecutor
+    from runtime.passes import run_pipeline
+    from runtime.planner import plan
+    from workloads import export_workload
+    _, x, graph = export_workload("gpt2w", seq_len=512)
+    run_pipeline(graph, None)
+    mp = plan(graph)
+    picks = []
+    for _ in range(3):
+        ex = CompiledExecutor()
+        ex.compile(mp)
+        try:
+            picks.append([(p["name"], p["m"], p["n"], p["k"], p["dma_tile"]) for p in ex.step_params()
+                          if p["kernel"].startswith("gemm_dma")])
+        finally:
+            ex.close()
+    assert picks[0] == picks[1] == picks[2], picks
+    by_name = {name: tile for name, m, n, k, tile in picks[0]}
+    # kDmaTiles order: 256x256, 128x128, 128x64, 64x128, 64x64, 32x48, 32x48s4, 64x96
+    assert by_name["gemm_dma_f32_nt+heads"] == 5 and by_name["gemm_dma_f32_nt+act"] == 5, picks[0]
