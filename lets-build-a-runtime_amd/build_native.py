@@ -1,10 +1,16 @@
 """Build liblbr_executor.so (the gfx950 compiled-executor library) in-tree.
 
-    python lets-build-a-runtime_amd/build_native.py
+    python lets-build-a-runtime_amd/build_native.py [--sanitize]
 
 Compiles every csrc/*.hip translation unit with hipcc for gfx950 (in
 parallel) and links them into csrc/liblbr_executor.so.  Always rebuilds.
 Packed-FP32 instruction selection is disabled for all device code.
+
+--sanitize builds the same sources with AddressSanitizer and
+UndefinedBehaviorSanitizer on the host code only (node decoders, the fusion
+matcher, plan joins, launchers; the device code is built as usual) into
+_build_san/liblbr_executor_san.so, for CPU tests of the host layer: load it
+with LBR_EXECUTOR_LIB and the shared ASan runtime preloaded (asan_runtime()).
 """
 
 from __future__ import annotations
@@ -33,9 +39,22 @@ COMMON_FLAGS = [
 ]
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+# host-only sanitizers (each -fsanitize= applies to the host compilation alone)
+SAN_FLAGS = "-Xarch_host -fsanitize=address -Xarch_host -fsanitize=undefined".split() + [
+    "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer", "-g1"]
+SAN_BUILD = HERE / "_build_san"
+SAN_LIB = SAN_BUILD / "liblbr_executor_san.so"
+
+
+def asan_runtime() -> str:
+    """Path of the shared ASan runtime the sanitized library links against."""
+    res = subprocess.run([HIPCC, "-print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+    return res.stdout.strip()
+
+
+def _compile(src: Path, sanitize: bool = False) -> Path:
+    obj = (SAN_BUILD if sanitize else BUILD) / (src.stem + ".o")
+    cmd = [HIPCC, *COMMON_FLAGS, *(SAN_FLAGS if sanitize else []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
@@ -47,25 +66,29 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = True) -> Path:
-    """Compile and link; returns the path of the shared library."""
+def build(verbose: bool = True, sanitize: bool = False) -> Path:
+    """Compile and link; returns the path of the shared library (the sanitized
+    variant with sanitize=True)."""
     if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    BUILD.mkdir(exist_ok=True)
+    out_dir, lib = (SAN_BUILD, SAN_LIB) if sanitize else (BUILD, LIB)
+    out_dir.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     workers = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(max_workers=workers) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+        objs = list(ex.map(lambda src: _compile(src, sanitize), sources))
+    tmp = lib.with_suffix(".so.tmp")
+    link_san = "-Xarch_host -fsanitize=address -Xarch_host -fsanitize=undefined -shared-libsan".split()
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *(link_san if sanitize else []), *map(str, objs),
+           "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB.relative_to(HERE.parent)} from {len(sources)} sources")
-    return LIB
+        print(f"built {lib.relative_to(HERE.parent)} from {len(sources)} sources")
+    return lib
 
 
 if __name__ == "__main__":
-    build()
+    build(sanitize="--sanitize" in sys.argv[1:])
