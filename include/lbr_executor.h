@@ -234,10 +234,6 @@ int lbr_plan_node_kernel(const lbr_plan* plan, int index, char* name_out,
                                       leading dims) → RMSNORM | LAYERNORM: the norm kernel adds,
                                       writes the sum and normalises it (a plan step join; not
                                       reported by lbr_fusion_windows)                      */
-#define LBR_FUSE_TINY           9 /* opt-in (LBR_TINY=1): the whole node array as one workgroup
-                                     of 1024 threads, the intermediates held in LDS (outputs
-                                     spanning at most the CU's LDS less the node records, small
-                                     GEMM/attention work, supported ops)                       */
 
 typedef struct {
     int first;   /* index of the run's first node */
@@ -263,10 +259,11 @@ int lbr_plan_num_steps(const lbr_plan* plan);
 int lbr_plan_step_info(const lbr_plan* plan, int step, int* first_node,
                        int* n_nodes, int* kind);
 
-/* x / d by the multiply-shift divisor the single-workgroup plan
- * (LBR_FUSE_TINY) indexes with, computed on the host exactly as the kernel
- * does (x < 2^31, d >= 1): test support, no counterpart in the reference. */
-unsigned lbr_tiny_fast_div(unsigned x, unsigned d);
+/* x / d by the multiply-shift divisor the attention key-range split and the
+ * head prologue index with (lbr_fast_divisor, lbr_fdiv), computed on the host
+ * exactly as the kernels do (x < 2^31, d >= 1): test support, no counterpart
+ * in the reference. */
+unsigned lbr_fast_div(unsigned x, unsigned d);
 
 /* The (head, 16-row query block) each workgroup of the key-quartered
  * attention kernel runs, for `bh` heads of `seq` rows (causal or not) on

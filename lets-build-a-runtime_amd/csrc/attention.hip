@@ -1213,6 +1213,13 @@ step_fn pick_kq(bool causal, bool mask) {
 
 }  // namespace
 
+void lbr_attn_defer(Step* s) {
+    s->i[14] = 1;
+    // the key-quartered kernel stages every row of O ([bh, S, D]) for attn_kq_flush; the
+    // split's workspace (its partials) already covers every block
+    if (s->i[15] == 1) s->ws_bytes = (size_t)s->i[0] * (size_t)s->i[1] * (size_t)s->i[2] * sizeof(float) + 256;
+}
+
 const char* lbr_attn_step_name(const Step& s, bool v, bool t, int store) {
     static const std::vector<std::string> table = [] {
         std::vector<std::string> n;
@@ -1291,6 +1298,13 @@ const std::vector<unsigned short>& kq_plan(long long bh, int S, bool causal, int
     }
     map = out;
     return map;
+}
+
+extern "C" unsigned lbr_fast_div(unsigned x, unsigned d) {
+    int m = 0, sh = 0;
+    lbr_fast_divisor(d, &m, &sh);
+    if (m == 0) return x;
+    return (unsigned)(((unsigned long long)x * (unsigned)m) >> 32) >> sh;
 }
 
 extern "C" int lbr_attn_kq_grid(long long bh, int seq, int causal, int cus, int* heads_out, int* blocks_out,
@@ -1384,9 +1398,7 @@ int decode_attention(const OpNode* n, Step* s) {
                 // the kernel's buffer views address one head's rows with 32-bit byte offsets
                 if (kq && n16 * bh < (1LL << 31) && (long long)seq * hd * 4 < (1LL << 31)) {
                     s->i[6] = 0;
-                    s->i[15] = 1;
-                    // staging rows of a deferred store (attn_kq_flush)
-                    s->ws_bytes = (size_t)bh * (size_t)seq * (size_t)hd * sizeof(float) + 256;
+                    s->i[15] = 1;   // a deferred store stages its rows in the workspace (lbr_attn_defer)
                     switch (dp) {
                         case 32: s->run = pick_kq<32>(causal, has_mask); break;
                         case 64: s->run = pick_kq<64>(causal, has_mask); break;

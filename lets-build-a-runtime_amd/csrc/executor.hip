@@ -267,7 +267,6 @@ struct lbr_plan {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     void* ws = nullptr;          // shared step workspace (split-K partial sums)
-    void* tiny_buf = nullptr;    // device node copy of a single-workgroup plan
     void* relay = nullptr;       // attention outputs moved off their inputs (lbr_relay_ok)
 };
 
@@ -275,7 +274,6 @@ static void free_plan(lbr_plan* p) {
     if (p->exec) (void)hipGraphExecDestroy(p->exec);
     if (p->graph) (void)hipGraphDestroy(p->graph);
     if (p->ws) (void)hipFree(p->ws);
-    if (p->tiny_buf) (void)hipFree(p->tiny_buf);
     if (p->relay) (void)hipFree(p->relay);
     delete p;
 }
@@ -448,30 +446,16 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
         }
     }
     std::vector<FusedRun> runs;
-    bool tiny = false;
     if (fuse) {
-        // a graph small enough for one workgroup becomes a single step
-        Step ts;
-        int rc = lbr_tiny_step(nodes, n_nodes, live_ptr, live_bytes, n_live, n_live > 0, &ts, &p->tiny_buf, &tiny);
+        int rc = lbr_find_fusions(nodes, n_nodes, live_ptr, live_bytes, n_live, &runs);
         if (rc) {
             delete p;
             return rc;
         }
-        if (tiny) {
-            p->node_step.assign((size_t)n_nodes, -1);
-            p->node_step[0] = 0;
-            p->steps.push_back(ts);
-        } else {
-            rc = lbr_find_fusions(nodes, n_nodes, live_ptr, live_bytes, n_live, &runs);
-            if (rc) {
-                delete p;
-                return rc;
-            }
-        }
     }
-    if (!tiny) p->node_step.assign((size_t)n_nodes, -1);
+    p->node_step.assign((size_t)n_nodes, -1);
     size_t r = 0;
-    for (int i = 0; i < n_nodes && !tiny;) {
+    for (int i = 0; i < n_nodes;) {
         p->node_step[i] = (int)p->steps.size();
         if (r < runs.size() && runs[r].first == i) {
             Step s;
@@ -521,7 +505,7 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
             // an ADD whose sum only a norm right after it reads first (a position
             // table, say): the norm kernel adds
             Step nstep;
-            if (fuse && !tiny && i + 1 < n_nodes && (r >= runs.size() || runs[r].first != i + 1)) {
+            if (fuse && i + 1 < n_nodes && (r >= runs.size() || runs[r].first != i + 1)) {
                 nstep = decoded[i + 1];
                 if (lbr_merge_add_norm(&nstep, decoded[i], &nodes[i])) {
                     p->steps.push_back(nstep);
@@ -533,7 +517,7 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
             ++i;
         }
     }
-    int rc = tiny || !fuse ? LBR_OK : relay_attention_outputs(p, nodes, n_nodes, live_ptr, live_bytes, n_live);
+    int rc = !fuse ? LBR_OK : relay_attention_outputs(p, nodes, n_nodes, live_ptr, live_bytes, n_live);
     if (!rc) rc = assign_workspace(p->steps, &p->ws);
     if (!rc) rc = autotune_gemms(p->steps);
     if (rc) {
@@ -843,12 +827,8 @@ int lbr_fusion_windows(const OpNode* nodes, int n_nodes, const void* const* live
         return LBR_ERR_INVALID;
     }
     std::vector<FusedRun> runs;
-    if (lbr_tiny_eligible(nodes, n_nodes, live_ptr, live_bytes, n_live, n_live > 0)) {
-        runs.push_back({0, n_nodes, LBR_FUSE_TINY});
-    } else {
-        int rc = lbr_find_fusions(nodes, n_nodes, live_ptr, live_bytes, n_live, &runs);
-        if (rc) return rc;
-    }
+    int rc = lbr_find_fusions(nodes, n_nodes, live_ptr, live_bytes, n_live, &runs);
+    if (rc) return rc;
     for (size_t k = 0; k < runs.size() && (int)k < cap; ++k) {
         out[k].first = runs[k].first;
         out[k].count = runs[k].count;

@@ -1320,7 +1320,7 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
                 lbr_set_error("fusion: attention node %d writes over its inputs without a deferred store", f.first);
                 return LBR_ERR_INVALID;
             }
-            s->i[14] = 1;
+            lbr_attn_defer(s);
             s->name = lbr_attn_step_name(*s, false, true, 1);
         }
     } else if (f.kind == LBR_FUSE_ATTN_SLICED_V) {
@@ -1343,7 +1343,7 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
                 lbr_set_error("fusion: attention node %d writes over its inputs without a deferred store", at);
                 return LBR_ERR_INVALID;
             }
-            s->i[14] = 1;
+            lbr_attn_defer(s);
             s->name = lbr_attn_step_name(*s, true, tout, 1);
         }
     } else if (f.kind == LBR_FUSE_TRANSPOSE_GEMM) {

@@ -378,6 +378,9 @@ int decode_attention(const OpNode* n, Step* s);
 // over them): the key-range split (merge kernel) and the key-quartered kernel
 // (attn_kq_flush).
 inline bool lbr_attn_can_defer(const Step& s) { return s.i[7] > 0 || s.i[15] == 1; }
+// Marks a decoded attention step (lbr_attn_can_defer) as deferring its store,
+// with the workspace that needs.
+void lbr_attn_defer(Step* s);
 // Step name of an attention: its kernel, then "+v" (V read from a row-major
 // source), "+transpose" (O stored as [B, S, H, D]) and, for store 1 / 2,
 // "+defer" / "+relay".

@@ -98,12 +98,4 @@ bool lbr_relay_ok(const OpNode* nodes, int n, const Step& at, const Step& gm, co
 // extras); *hi = UINTPTR_MAX when the node does not fix it.
 void lbr_input_extent(const OpNode* nd, int k, unsigned long long* lo, unsigned long long* hi);
 
-// Whether lbr_tiny_step would take the node array (host only, no device).
-bool lbr_tiny_eligible(const OpNode* nodes, int n, const void* const* live_ptr, const size_t* live_bytes,
-                       int n_live, bool have_live);
 
-// The whole node array as one single-workgroup step (tiny.hip) when it is
-// small enough; *taken says whether it was, *dev_buf is the device memory the
-// step uses (the plan frees it).
-int lbr_tiny_step(const OpNode* nodes, int n, const void* const* live_ptr, const size_t* live_bytes, int n_live,
-                  bool have_live, Step* s, void** dev_buf, bool* taken);

@@ -36,7 +36,7 @@ class LbrWindow(ctypes.Structure):
 
 
 FUSE_KINDS = {0: "none", 1: "gemm_resid", 2: "gemm_heads", 3: "head_prologue", 4: "attn_transpose",
-              5: "gemm_act", 6: "gemm_gated", 7: "transpose_gemm", 8: "attn_sliced_v", 9: "tiny", 10: "norm_gemm",
+              5: "gemm_act", 6: "gemm_gated", 7: "transpose_gemm", 8: "attn_sliced_v", 10: "norm_gemm",
               11: "mlp", 12: "add_norm"}
 
 
@@ -81,7 +81,7 @@ class HipLibrary:
             "lbr_plan_num_steps": ([c_vp], c_int),
             "lbr_plan_step_info": ([c_vp, c_int, P(c_int), P(c_int), P(c_int)], c_int),
             "lbr_plan_step_args": ([c_vp, c_int, P(ctypes.c_longlong), c_int], c_int),
-            "lbr_tiny_fast_div": ([ctypes.c_uint, ctypes.c_uint], ctypes.c_uint),
+            "lbr_fast_div": ([ctypes.c_uint, ctypes.c_uint], ctypes.c_uint),
             "lbr_gemm_tile_name": ([c_int], c_char_p),
             "lbr_attn_kq_grid": ([ctypes.c_longlong, c_int, c_int, c_int, P(c_int), P(c_int), c_int], c_int),
         }

@@ -21,14 +21,6 @@ for p in (str(PKG), str(ROOT)):
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built device library")
     config.addinivalue_line("markers", "slow: long-running CPU test")
-    config.addinivalue_line("markers", "tiny: plans may take the single-workgroup form (LBR_TINY=1)")
-
-
-@pytest.fixture(autouse=True)
-def _tiny_plans_only_where_marked(request, monkeypatch):
-    """The single-workgroup plan is opt-in (LBR_TINY=1): on for tests marked
-    `tiny`, off for every other test whatever the caller's environment says."""
-    monkeypatch.setenv("LBR_TINY", "1" if request.node.get_closest_marker("tiny") else "0")
 
 
 def normwise_rel(y, ref) -> float:

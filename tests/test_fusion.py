@@ -522,60 +522,14 @@ def test_transpose_gemm_refusals():
     assert all(k != "transpose_gemm" for _, _, k in _windows(_tgemm(0, 1 * MB, 2 * MB, 3 * MB, later=[reader])))
 
 
-# ------------------------------------------------------------ single-workgroup plan
+# ------------------------------------------------------------ index arithmetic
 
-@pytest.mark.tiny
-def test_tiny_plan_takes_the_toy_block_at_its_own_size(monkeypatch):
-    """With LBR_TINY=1 (the `tiny` mark), S = 32: every intermediate of the toy
-    block fits one CU's LDS, and the whole array is one window; at S = 128 the
-    outputs span more than the CU's 160 KiB of LDS and the peephole runs come
-    back; LBR_TINY=0 (the default) leaves the peephole runs."""
-    lib = _lib()
-    arr, order, live = _workload_nodes("toy", 32)
-    assert lib.fusion_windows(arr, len(order), live) == [(0, len(order), "tiny")]
-    assert lib.fusion_windows(arr, len(order), []) == [(0, len(order), "tiny")]
-    arr64, order64, live64 = _workload_nodes("toy", 128)
-    assert "tiny" not in {k for _, _, k in lib.fusion_windows(arr64, len(order64), live64)}
-    monkeypatch.setenv("LBR_TINY", "0")
-    assert "tiny" not in {k for _, _, k in lib.fusion_windows(arr, len(order), live)}
-
-
-def _tiny_chain(x_ptr=EXT, mid=ARENA, out=ARENA + 4096, n=256):
-    """RELU(x) → mid, NEG(mid) → out."""
-    return [_node(OpType.RELU, [x_ptr], mid, (n,)), _node(OpType.NEG, [mid], out, (n,))]
-
-
-@pytest.mark.tiny
-def test_tiny_plan_refusals():
-    assert _windows(_tiny_chain()) == [(0, 2, "tiny")]
-    # one node: its own kernel
-    assert _windows(_tiny_chain()[:1]) == []
-    # an input inside the window that no earlier node wrote (an input placed between outputs)
-    assert _windows(_tiny_chain(x_ptr=ARENA + 2048)) == []
-    # a read that straddles the window's edge
-    nodes = _tiny_chain()
-    nodes[1] = _node(OpType.NEG, [ARENA - 512], ARENA + 4096, (256,))
-    assert _windows(nodes) == []
-    # outputs spanning more than the CU's 160 KiB of LDS less the node records
-    assert _windows(_tiny_chain(out=ARENA + 159 * 1024)) == []
-    assert _windows(_tiny_chain(out=ARENA + 158 * 1024)) == [(0, 2, "tiny")]
-    # an op the interpreter does not run (SUM) anywhere in the array
-    nodes = _tiny_chain() + [_node(OpType.SUM, [ARENA + 4096], ARENA + 8192, (1,), (0, 256))]
-    assert "tiny" not in {k for _, _, k in _windows(nodes)}
-    # GEMM work beyond the single-workgroup budget (2·M·N·K > 32 Mi FLOP)
-    big = [_node(OpType.MATMUL, [A_, W_], ARENA, (64, 64), (8192, 1, 1, 0)),
-           _node(OpType.NEG, [ARENA], ARENA + 16384, (64, 64))]
-    assert _windows(big) == []
-    big[0].extra[0] = 4096
-    assert _windows(big) == [(0, 2, "tiny")]
-
-
-def test_tiny_fast_divisor_matches_integer_division():
-    """The single-workgroup kernel divides by a multiply and a shift (x < 2^31):
+def test_fast_divisor_matches_integer_division():
+    """The attention key-range split and the head prologue divide by a multiply and a shift (x < 2^31):
     the host computation of the same (m, s) against plain division on every
     divisor up to 4096 with the dividends at each multiple's edges, on divisors
     around powers of two, and on random pairs."""
-    f = _lib().lbr_tiny_fast_div
+    f = _lib().lbr_fast_div
     r = np.random.default_rng(11)
     top = (1 << 31) - 1
     divisors = list(range(1, 4097)) + [(1 << k) + e for k in range(12, 31) for e in (-1, 0, 1)] + [top]
