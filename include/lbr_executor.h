@@ -179,9 +179,11 @@ int lbr_synchronize(void);
  * on the library stream; *out_ms = total elapsed milliseconds. */
 int lbr_plan_time(lbr_plan* plan, int iters, float* out_ms);
 
-/* Per-node device time: runs the plan `iters` times eagerly with a hipEvent
- * pair around every node's launches (on the library stream) and writes the
- * mean milliseconds of node i to out_ms[i] (n_out >= number of nodes). */
+/* Per-node device time: runs each step of the plan `iters` times back to back
+ * between one hipEvent pair (on the library stream, behind a short arithmetic-only
+ * kernel that keeps the GPU busy while the host enqueues them), then one plain
+ * pass, and writes the mean milliseconds per launch of node i's step to out_ms[i]
+ * (0 for the later nodes of a fused run; n_out >= number of nodes). */
 int lbr_plan_profile(lbr_plan* plan, int iters, float* out_ms, int n_out);
 
 /* Short name of the kernel that executes node `index` (for reports); nodes

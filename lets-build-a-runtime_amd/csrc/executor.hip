@@ -53,6 +53,15 @@ void lbr_set_error(const char* fmt, ...) {
 
 // ------------------------------------------------------------------ device
 static std::mutex g_mu;
+
+// Dependent arithmetic only, `iters` steps of it: a GPU-side delay of known length
+// for lbr_plan_profile (x stays a; the store never happens for a = 0, b = 1).
+__device__ float g_busy_sink;
+__global__ void lbr_busy(int iters, float a, float b) {
+    float x = a;
+    for (int i = 0; i < iters; ++i) x = fmaf(x, b, a);
+    if (x == -1.f) g_busy_sink = x;
+}
 static int g_device = -1;
 static hipStream_t g_stream = nullptr;
 static int g_cus = 0;
@@ -923,24 +932,47 @@ int lbr_plan_profile(lbr_plan* p, int iters, float* out_ms, int n_out) {
         return LBR_ERR_INVALID;
     }
     const size_t n = p->steps.size();
-    std::vector<hipEvent_t> ev(n + 1);
-    for (auto& e : ev) HIP_TRY(hipEventCreate(&e));
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    HIP_TRY(hipEventCreate(&e0));
+    HIP_TRY(hipEventCreate(&e1));
+    // Each step runs `iters` times back to back between one event pair, so the
+    // events' own cost (a completion signal and a fresh dispatch per event) is
+    // spread over `iters` launches. Eager launches would still leave the GPU idle
+    // while the host enqueues the next one; a busy kernel queued first keeps it
+    // occupied until they are all enqueued: 40 us of GPU time per launch covers the
+    // host's enqueue cost, profilers included. Its length is calibrated once.
+    HIP_TRY(hipEventRecord(e0, g_stream));
+    hipLaunchKernelGGL(lbr_busy, dim3(1), dim3(64), 0, g_stream, 1 << 16, 0.f, 1.f);
+    HIP_TRY(hipEventRecord(e1, g_stream));
+    HIP_TRY(hipEventSynchronize(e1));
+    HIP_TRY(hipGetLastError());
+    float cal_ms = 0.f;
+    HIP_TRY(hipEventElapsedTime(&cal_ms, e0, e1));
+    const double want_ms = std::max(0.2, 0.04 * (double)iters);
+    const double busy = cal_ms > 0.f ? want_ms / cal_ms * (double)(1 << 16) : (double)(1 << 20);
+    const int busy_iters = (int)std::min(busy, (double)(1 << 28));
+    // A repeated step may read what its own previous launch wrote (an in-place
+    // epilogue, an output stored over its input): the values change, the work does
+    // not (grids, loop trips and addresses follow shapes; the only data-indexed
+    // reads, embedding rows, index graph inputs, which no step writes). One plain
+    // pass at the end leaves every buffer as a forward pass leaves it.
     std::vector<double> acc(n, 0.0);
-    for (int it = 0; it < iters; ++it) {
-        HIP_TRY(hipEventRecord(ev[0], g_stream));
-        for (size_t i = 0; i < n; ++i) {
-            p->steps[i].run(p->steps[i], g_stream);
-            HIP_TRY(hipEventRecord(ev[i + 1], g_stream));
-        }
-        HIP_TRY(hipEventSynchronize(ev[n]));
+    for (size_t i = 0; i < n; ++i) {
+        hipLaunchKernelGGL(lbr_busy, dim3(1), dim3(64), 0, g_stream, busy_iters, 0.f, 1.f);
+        HIP_TRY(hipEventRecord(e0, g_stream));
+        for (int it = 0; it < iters; ++it) p->steps[i].run(p->steps[i], g_stream);
+        HIP_TRY(hipEventRecord(e1, g_stream));
+        HIP_TRY(hipEventSynchronize(e1));
         HIP_TRY(hipGetLastError());
-        for (size_t i = 0; i < n; ++i) {
-            float ms = 0.f;
-            HIP_TRY(hipEventElapsedTime(&ms, ev[i], ev[i + 1]));
-            acc[i] += ms;
-        }
+        float ms = 0.f;
+        HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+        acc[i] = ms;
     }
-    for (auto& e : ev) (void)hipEventDestroy(e);
+    run_steps(p->steps, g_stream);
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    HIP_TRY(hipGetLastError());
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
     // a step's time goes to its first node; the other nodes of a fused run get 0
     for (int i = 0; i < p->n_nodes; ++i) out_ms[i] = 0.f;
     for (size_t i = 0; i < n; ++i) out_ms[p->steps[i].node_index] = (float)(acc[i] / iters);

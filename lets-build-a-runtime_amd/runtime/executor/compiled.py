@@ -372,7 +372,8 @@ class CompiledExecutor(Executor):
         return float(ms.value)
 
     def profile_nodes(self, iters: int = 1) -> list[float]:
-        """Mean milliseconds per dispatched node (eager launches, hipEvent pairs)."""
+        """Mean milliseconds per dispatched node: each step launched ``iters`` times back to
+        back between one hipEvent pair (eager launches on the library stream)."""
         n = len(self._order)
         buf = (ctypes.c_float * max(n, 1))()
         self._lib.check(self._lib.lbr_plan_profile(self._plan_handle, int(iters), buf, max(n, 1)),

@@ -239,3 +239,26 @@ def test_profile_run_reports_every_node():
     assert len(prof.op_timings) == 20
     assert prof.total_ns > 0
     s.close()
+
+
+def test_node_profile_adds_up_to_the_replayed_step():
+    """The per-node hipEvent times are kernel times, not host launch gaps: on GPT-2 width at
+    S=512, whose fused kernels last 5-40 us, their sum stays within 20% of the replayed step's
+    time (a replay has the GPU's own dispatch gaps, the profile an event between kernels)."""
+    from workloads import export_workload
+    from runtime.session import Session
+    _, x, graph = export_workload("gpt2w")
+    s = Session(graph)
+    s.create(use_graph=True)
+    try:
+        ex = s.executor
+        s.run({graph.inputs[0]: x})
+        ex.time_launches(5)
+        step_ms = ex.time_launches(50) / 50
+        node_ms = ex.profile_nodes(20)
+        assert all(t >= 0.0 for t in node_ms)
+        total = sum(node_ms)
+        print(f"replayed step {step_ms * 1e3:.1f} us, sum of node times {total * 1e3:.1f} us")
+        assert 0.8 * step_ms <= total <= 1.2 * step_ms
+    finally:
+        s.close()
