@@ -90,8 +90,10 @@ struct AttnArgs {
     // v_ld = 0: V is [kv heads, S, D] like K.
     long long v_ld;
     int v_heads;
-    // 16-row key-quartered kernel (attn_fwd_kq): query blocks of 16 rows, kq_nq per head
+    // 16-row key-quartered kernel (attn_fwd_kq): query blocks of 16 rows, kq_nq per head;
+    // k_frag: K is stored fragment-major (lbr_frag_offset) by the GEMM that wrote it
     int kq_nq, kq_bh;
+    int k_frag;
 };
 
 // Row q of head bh in the output: [bh][S][D], or [B][S][H][D] when the
@@ -739,14 +741,6 @@ __global__ __launch_bounds__(KQ_NT, 2) void attn_fwd_kq(KqArgs k) {
     // Q rows, pre-scaled (rows past S read zero; their lanes are never stored, and a lane's
     // scores, max and sum never mix with another row's): all loads, then one wait
     floatx4 qf[NCH];
-    {
-        const unsigned qo = (unsigned)(q * DP + 4 * lg) * 4u;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c)
-            qf[c] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rq, qo + 64 * c, 0, 0));
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) qf[c] *= g.scale_log2;
-    }
 
     const int nt = (S + A16_KB - 1) / A16_KB;
     const int T = CAUSAL ? min(nt, min(S - 1, q0 + KQ_QB - 1) / A16_KB + 1) : nt;
@@ -757,15 +751,18 @@ __global__ __launch_bounds__(KQ_NT, 2) void attn_fwd_kq(KqArgs k) {
 
     floatx4 kf[2][NCH];
     VW vf[2][4][NH];
-    // K rows 32t + 16b + lr, d 16c + 4lg .. +3 (A operand of Sᵀ = K·Qᵀ)
-    const unsigned ko = (unsigned)(lr * DP + 4 * lg) * 4u;
+    // K rows 32t + 16b + lr, d 16c + 4lg .. +3 (A operand of Sᵀ = K·Qᵀ). Row-major, one
+    // load instruction reads 64 of the 128 bytes of 16 lines; fragment-major
+    // (lbr_frag_offset), 1 KiB of 8 whole lines, which halves the L2 requests for K.
+    const unsigned ko = g.k_frag ? (unsigned)(lr * 16 + 4 * lg) * 4u : (unsigned)(lr * DP + 4 * lg) * 4u;
+    const unsigned kcs = g.k_frag ? 1024u : 64u;
     auto load_k = [&](int t) {
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             const unsigned so = (unsigned)((t * A16_KB + 16 * b) * DP) * 4u;
 #pragma unroll
             for (int c = 0; c < NCH; ++c)
-                kf[b][c] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 64 * c, so, 0));
+                kf[b][c] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rk, ko + kcs * c, so, 0));
         }
     };
     // V rows 32t + 16b + 4lg + rr, d 16W·h + W·lr .. +W−1 (A operand of Oᵀ = Vᵀ·Pᵀ)
@@ -800,9 +797,35 @@ __global__ __launch_bounds__(KQ_NT, 2) void attn_fwd_kq(KqArgs k) {
     // tile's scores before the current P·V, to run the softmax under the P·V MFMAs,
     // measured slower: GPT-2 S1024 25.3 → 27.5 µs.)
     int t = wave;
-    if (t < T) {
-        load_k(t);
-        load_v(t);
+    {
+        // Q rows, pre-scaled (rows past S read zero; their lanes are never stored, and a
+        // lane's scores, max and sum never mix with another row's). The four wavefronts
+        // share the block's rows: each fetches the 16-column chunks c = wave mod 4, issues
+        // its first K/V tile, and the chunks meet in LDS (the combine area, free until
+        // the end). One request per Q line instead of four matters at launch, when every
+        // workgroup asks the L2 for its Q and first tile at once.
+        constexpr int QPW = (NCH + KQ_WAVES - 1) / KQ_WAVES;
+        floatx4 qpart[QPW];
+        const unsigned qo = (unsigned)(q * DP + 4 * lg) * 4u;
+#pragma unroll
+        for (int c = 0; c < QPW; ++c)
+            if (wave + KQ_WAVES * c < NCH)
+                qpart[c] = __builtin_bit_cast(
+                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(rq, qo + 64 * (wave + KQ_WAVES * c), 0, 0));
+        if (t < T) {
+            load_k(t);
+            load_v(t);
+        }
+#pragma unroll
+        for (int c = 0; c < QPW; ++c)
+            if (wave + KQ_WAVES * c < NCH)
+                *reinterpret_cast<floatx4*>(&o_sh[0][lr][16 * (wave + KQ_WAVES * c) + 4 * lg]) = qpart[c];
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) qf[c] = *reinterpret_cast<const floatx4*>(&o_sh[0][lr][16 * c + 4 * lg]);
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) qf[c] *= g.scale_log2;
     }
     for (; t < T; t += KQ_WAVES) {
         const int k0 = t * A16_KB;
@@ -1060,7 +1083,8 @@ __global__ __launch_bounds__(256) void attn_fwd_rows(AttnArgs g, int causal) {
 //          [11]=key tiles per head (split) [12]=V row stride when V is read from the columns
 //          of a row-major tensor (0 = contiguous) [13]=K/V heads of that layout
 //          [14]=deferred output (the merge kernel, or attn_kq_flush, writes every row of O)
-//          [15]=key-quartered kernel (attn_fwd_kq)
+//          [15]=key-quartered kernel (attn_fwd_kq) [16]=K stored fragment-major (key-quartered
+//          kernel only; set by the plan with the QKV GEMM's head scatter, lbr_frag_keys_ok)
 AttnArgs make_args(const Step& s) {
     AttnArgs g;
     g.Q = (const float*)s.in[0];
@@ -1078,6 +1102,7 @@ AttnArgs make_args(const Step& s) {
     g.sk_defer = 0;
     g.v_ld = 0;
     g.v_heads = 1;
+    g.k_frag = 0;
     return g;
 }
 
@@ -1147,6 +1172,7 @@ void launch_attn_kq(const Step& s, hipStream_t st) {
     }
     g.kq_nq = (g.S + KQ_QB - 1) / KQ_QB;
     g.kq_bh = bh;
+    g.k_frag = s.i[16] != 0;
     g.sk_defer = s.i[14] != 0;
     g.part = g.sk_defer ? (float*)s.ws : nullptr;
     g.ml = nullptr;

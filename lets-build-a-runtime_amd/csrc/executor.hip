@@ -316,6 +316,31 @@ static int relay_attention_outputs(lbr_plan* p, const OpNode* nodes, int n_nodes
     return LBR_OK;
 }
 
+// Keys in fragment-major order (lbr_frag_keys_ok): a key-quartered attention
+// whose K only its own step reads gets it from the head-scattering GEMM that
+// writes it in the order the attention's K loads take it, whole cache lines
+// per load instead of half lines.
+static void fragment_keys(lbr_plan* p, const OpNode* nodes, int n_nodes, const void* const* live_ptr,
+                          const size_t* live_bytes, int n_live) {
+    for (size_t a = 0; a < p->steps.size(); ++a) {
+        Step& at = p->steps[a];
+        if (!at.name || strncmp(at.name, "attn_fwd_kq", 11) != 0 || at.i[15] != 1) continue;
+        for (size_t g = a; g-- > 0;) {
+            Step& gm = p->steps[g];
+            if (!gm.name || strncmp(gm.name, "gemm_", 5) != 0 || gm.i[19] <= 0) continue;
+            int k = -1;
+            for (int q = 0; q < gm.i[19] && q < 4; ++q)
+                if (gm.in[4 + q] == at.in[1]) k = q;
+            if (k < 0) continue;
+            if (lbr_frag_keys_ok(nodes, n_nodes, gm, k, at, live_ptr, live_bytes, n_live)) {
+                gm.i[5] |= 1LL << k;
+                at.i[16] = 1;
+            }
+            break;
+        }
+    }
+}
+
 static void run_steps(const std::vector<Step>& steps, hipStream_t st) {
     for (const Step& s : steps) s.run(s, st);
 }
@@ -527,6 +552,7 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
         }
     }
     int rc = !fuse ? LBR_OK : relay_attention_outputs(p, nodes, n_nodes, live_ptr, live_bytes, n_live);
+    if (!rc && fuse) fragment_keys(p, nodes, n_nodes, live_ptr, live_bytes, n_live);
     if (!rc) rc = assign_workspace(p->steps, &p->ws);
     if (!rc) rc = autotune_gemms(p->steps);
     if (rc) {

@@ -968,6 +968,50 @@ bool lbr_relay_ok(const OpNode* nodes, int n, const Step& at, const Step& gm, co
     return true;
 }
 
+// A head-scattering GEMM step can store split k fragment-major
+// (lbr_frag_offset) for the key-quartered attention step that reads it as K,
+// when the split is exactly that attention's K ([B, Hkv, S, hd] with S a
+// multiple of 16 and hd the kernel's head dim) and no other read sees its
+// bytes before they are overwritten or at the end (live-out): the Q and V
+// reads of the attention itself included, so a K that is also its Q or V
+// keeps the row-major layout.
+bool lbr_frag_keys_ok(const OpNode* nodes, int n, const Step& gm, int k, const Step& at, const void* const* live_ptr,
+                      const size_t* live_bytes, int n_live) {
+    const char* e = getenv("LBR_KQ_FRAG");
+    if (e && atoi(e) == 0) return false;
+    if (!at.name || strncmp(at.name, "attn_fwd_kq", 11) != 0 || at.i[15] != 1) return false;
+    if (!gm.name || strncmp(gm.name, "gemm_", 5) != 0 || k < 0 || k >= gm.i[19] || k >= 4 || gm.in[4 + k] != at.in[1])
+        return false;
+    const long long S = at.i[1], hd = at.i[2];
+    if (S <= 0 || S % 16 != 0 || gm.i[30] != S || gm.i[29] != hd || at.i[5] != hd || at.i[4] <= 0) return false;
+    const long long rows = gm.i[0];
+    if (gm.i[3] != 1 || rows % S != 0 || (rows / S) * gm.i[25 + k] * at.i[4] != at.i[0]) return false;
+    int an = -1;
+    for (int j = at.node_index; j < at.node_index + at.n_nodes && j < n; ++j)
+        if (nodes[j].op == OP_ATTENTION) {
+            an = j;
+            break;
+        }
+    const int end = gm.node_index + gm.n_nodes;
+    if (an < end || nodes[an].inputs[1] != at.in[1]) return false;
+    std::vector<Rng> inter{rng(at.in[1], at.i[0] / at.i[4] * S * hd * 4)};
+    for (int j = end; j < n && !inter.empty(); ++j) {
+        const OpNode* nd = &nodes[j];
+        const int reads = nd->op == OP_ATTENTION ? 3 + (nd->extra[3] != 0) : nd->n_inputs;
+        for (int q = 0; q < reads && q < nd->n_inputs && q < MAX_INPUTS; ++q) {
+            if (j == an && q == 1) continue;   // the attention's K: the read that follows the layout
+            const Rng in = input_rng(nd, q);
+            for (const Rng& r : inter)
+                if (overlap(r, in)) return false;
+        }
+        subtract(&inter, out_rng(nd));
+    }
+    for (const Rng& r : inter)
+        for (int q = 0; q < n_live; ++q)
+            if (overlap(r, rng(live_ptr[q], (long long)live_bytes[q]))) return false;
+    return true;
+}
+
 // Find the fusable runs of `nodes` (in order, non-overlapping).
 int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, const size_t* live_bytes, int n_live,
                      std::vector<FusedRun>* out) {

@@ -58,6 +58,7 @@ struct GemmArgs {
     float* dst[4];            // split k's output, laid out [B, H, S, hd]
     const float* sbias[4];    // split k's bias row (indexed by column - col_begin[k]) or null
     int Hs[4], hd, S;         // heads of each split, head dim, rows per batch (M = B·S)
+    int frag;                 // bit k: split k is stored fragment-major (lbr_frag_offset)
     int act;                  // LBR_ACT_*: a following RELU / GELU / SILU applied to C (DMA kernel)
     // Gated pair (DMA kernel): the GEMM's columns hold a gate half and an up half
     // of gF columns each; the kernel writes out[m][j] = act(gate[m][j] (+ gbias[j]))·up[m][j]
@@ -100,7 +101,8 @@ __device__ __forceinline__ void epi_store(const GemmArgs& g, long long bz, int m
     if (g.sbias[k]) v = v + g.sbias[k][c];
     const int h = c / g.hd, d = c - h * g.hd;
     const int b = m / g.S, s = m - b * g.S;
-    g.dst[k][(((long long)b * g.Hs[k] + h) * g.S + s) * g.hd + d] = v;
+    const long long head = ((long long)b * g.Hs[k] + h) * g.S * g.hd;
+    g.dst[k][head + (((g.frag >> k) & 1) ? lbr_frag_offset(s, d, g.hd) : (long long)s * g.hd + d)] = v;
 }
 
 __device__ __forceinline__ void tile_coords(const GemmArgs& g, int& tm, int& tn) {
@@ -320,7 +322,8 @@ __global__ __launch_bounds__(NT, 2) void gemm_mfma_f32(GemmArgs g) {
             const float bv = HAS_BIAS ? g.bias[n] : 0.f;
             const float sb = g.sbias[k] ? g.sbias[k][c] : 0.f;
             const bool has_sb = g.sbias[k] != nullptr;
-            float* __restrict__ col = g.dst[k] + ((long long)h * g.S) * g.hd + d;
+            const bool fr = (g.frag >> k) & 1;
+            float* __restrict__ col = g.dst[k] + ((long long)h * g.S) * g.hd + (fr ? lbr_frag_offset(0, d, g.hd) : d);
             const long long bstride = (long long)g.Hs[k] * g.S * g.hd;
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
@@ -337,7 +340,7 @@ __global__ __launch_bounds__(NT, 2) void gemm_mfma_f32(GemmArgs g) {
                     }
                     float v = HAS_BIAS ? (acc[i][j][r] + bv) : g.alpha * acc[i][j][r];
                     if (has_sb) v = v + sb;
-                    col[b * bstride + (long long)s * g.hd] = v;
+                    col[b * bstride + (fr ? lbr_frag_offset(s, 0, g.hd) : (long long)s * g.hd)] = v;
                 }
             }
         }
@@ -728,7 +731,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
             const float bv = HAS_BIAS ? g.bias[n] : 0.f;
             const bool has_sb = g.sbias[k] != nullptr;
             const float sb = has_sb ? g.sbias[k][c] : 0.f;
-            float* __restrict__ col = g.dst[k] + ((long long)h * g.S) * g.hd + d;
+            const bool fr = (g.frag >> k) & 1;
+            float* __restrict__ col = g.dst[k] + ((long long)h * g.S) * g.hd + (fr ? lbr_frag_offset(0, d, g.hd) : d);
             const long long bstride = (long long)g.Hs[k] * g.S * g.hd;
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
@@ -744,7 +748,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
                     }
                     float v = HAS_BIAS ? (acc[i][j][r] + bv) : g.alpha * acc[i][j][r];
                     if (has_sb) v = v + sb;
-                    col[b * bstride + (long long)s * g.hd] = v;
+                    col[b * bstride + (fr ? lbr_frag_offset(s, 0, g.hd) : (long long)s * g.hd)] = v;
                 }
             }
         }
@@ -876,7 +880,8 @@ GemmArgs make_args(const Step& s) {
     g.W = (float*)s.ws;
     // fused epilogue: in[3] = resid (gated pair: the GATED_ACT bias);
     // i[19] = n_split, i[20..24] = col_begin, in[4..7] = dst, in[8..11] =
-    // split biases, i[25..28] = heads per split, i[29] = hd, i[30] = S;
+    // split biases, i[25..28] = heads per split, i[29] = hd, i[30] = S,
+    // i[5] = splits stored fragment-major (bit k, set by the plan);
     // i[31] = act; i[32] = gated F, i[33] = gated act, i[34] = gate half's first column
     g.gF = (int)s.i[32];
     g.gact = (int)s.i[33];
@@ -892,6 +897,7 @@ GemmArgs make_args(const Step& s) {
     }
     g.hd = (int)s.i[29];
     g.S = (int)s.i[30];
+    g.frag = (int)s.i[5];
     g.act = (int)s.i[31];
     // i[35..37] = A in head layout [B, H, S, hd]: H, S, hd (0: row-major A)
     g.aH = (int)s.i[35];

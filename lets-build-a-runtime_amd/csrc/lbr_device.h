@@ -323,6 +323,16 @@ __device__ __forceinline__ unsigned lbr_fdiv(unsigned x, int m, int s) {
     return m == 0 ? x : __umulhi(x, (unsigned)m) >> s;
 }
 
+// Fragment-major layout of one head's [S, hd] rows (the keys the key-quartered
+// attention reads, written so by the QKV GEMM's head scatter): rows go in groups
+// of 16, and each group's 16 × hd values as hd/16 chunks of [16 rows][16 columns],
+// so that the 16-row × 16-column operand fragment one load instruction fetches is
+// 1 KiB of contiguous memory. S must be a multiple of 16. The offset of element
+// (s, d) is the sum of a row part and a column part.
+__host__ __device__ __forceinline__ long long lbr_frag_offset(int s, int d, int hd) {
+    return (long long)(s & ~15) * hd + ((d >> 4) << 8) + ((s & 15) << 4) + (d & 15);
+}
+
 static inline bool lbr_aligned(const void* p, size_t a) {
     return (reinterpret_cast<uintptr_t>(p) % a) == 0;
 }

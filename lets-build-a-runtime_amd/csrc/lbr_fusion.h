@@ -94,6 +94,11 @@ bool lbr_merge_add_norm(Step* n, const Step& a, const OpNode* add);
 bool lbr_relay_ok(const OpNode* nodes, int n, const Step& at, const Step& gm, const void* const* live_ptr,
                   const size_t* live_bytes, int n_live);
 
+// GEMM step `gm` may write head split k fragment-major for the key-quartered
+// attention step `at` that reads it as K (and nothing else reads it).
+bool lbr_frag_keys_ok(const OpNode* nodes, int n, const Step& gm, int k, const Step& at, const void* const* live_ptr,
+                      const size_t* live_bytes, int n_live);
+
 // Byte range [*lo, *hi) input k of node nd reads (per op, from its shape and
 // extras); *hi = UINTPTR_MAX when the node does not fix it.
 void lbr_input_extent(const OpNode* nd, int k, unsigned long long* lo, unsigned long long* hi);

@@ -266,9 +266,9 @@ class CompiledExecutor(Executor):
         """Every kernel step of the compiled plan: its kernel (and full step name, with the
         fused parts), the nodes it covers, and the schedule its launch arguments encode
         (attention: causal fold, key-range split workgroups, deferred output, key-quartered
-        16-row kernel; GEMM: DMA tile
+        16-row kernel and whether it reads K fragment-major; GEMM: DMA tile
         index, K ranges, norm prologue, norm in the split-K reduce and whether the split was
-        made for it; head prologue: float4 kernel or one wavefront per row, and
+        made for it, head splits it stores fragment-major (bit mask); head prologue: float4 kernel or one wavefront per row, and
         how many Q/K parts one launch covers)."""
         lib, h = self._lib, self._plan_handle
         first, count, kind = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
@@ -282,12 +282,14 @@ class CompiledExecutor(Executor):
             d = {"kernel": names[first.value].split("+")[0], "name": names[first.value], "first": first.value,
                  "count": count.value, "kind": FUSE_KINDS.get(kind.value, "?")}
             if d["kernel"].startswith(("attn_fwd_mfma16", "attn_fwd_kq")):
-                d.update(fold=bool(ints[6]), split_wg=int(ints[7]), defer=bool(ints[14]), kq=bool(ints[15]))
+                d.update(fold=bool(ints[6]), split_wg=int(ints[7]), defer=bool(ints[14]), kq=bool(ints[15]),
+                         k_frag=bool(ints[15]) and bool(ints[16]))
             elif d["kernel"].startswith("gemm_"):
                 d.update(m=int(ints[0]), n=int(ints[1]), k=int(ints[2]),
                          tile=lib.lbr_gemm_tile_name(int(ints[14]) - 1).decode() or "legacy",
                          ksplit=max(1, int(ints[10])), dma_tile=int(ints[14]) - 1, norm=int(ints[15]),
-                         reduce_norm=int(ints[16]), split_for_norm=bool(int(ints[17]) & 256))
+                         reduce_norm=int(ints[16]), split_for_norm=bool(int(ints[17]) & 256),
+                         frag_splits=int(ints[5]) if int(ints[19]) > 0 else 0)
             elif d["kind"] == "head_prologue":
                 d.update(vec=bool(ints[13]), parts=int(ints[14]) if ints[13] else 1)
             out.append(d)

@@ -347,3 +347,75 @@ def test_attention_output_relay(monkeypatch, H, S, hd, causal):
     att = np.swapaxes(cf_attention(q, k, np.maximum(x, 0.0), causal=causal), 1, 2).reshape(1, S, W)
     ref = att.astype(np.float64) @ w.T.astype(np.float64)
     assert normwise_rel(ys["1"][0], ref) <= 1e-4
+
+
+@pytest.mark.parametrize("H,Hkv,S,hd,causal,k_live", [(12, 12, 256, 64, True, False), (8, 2, 512, 64, True, False),
+                                                      (4, 4, 128, 32, False, False), (12, 12, 256, 64, True, True)])
+def test_attention_fragment_major_keys(monkeypatch, H, Hkv, S, hd, causal, k_live):
+    """x → MATMUL_ADD → q/k/v (SLICE → RESHAPE → TRANSPOSE(1, 2)) → key-quartered ATTENTION: the
+    QKV GEMM's head scatter stores K fragment-major (16-row × 16-column chunks of 1 KiB) and the
+    attention loads it so, whole cache lines per load.  Bit-equal to the row-major plan
+    (LBR_KQ_FRAG=0), within 1e-4 of the float64 closed form.  With K also a graph output the
+    plan keeps K row-major (the caller reads it), and the returned K matches the closed form."""
+    from helpers import cf_attention
+    from runtime.executor.compiled import CompiledExecutor
+    from runtime.planner import plan
+    r = rng(H * S + hd + 7)
+    D = 96
+    widths = [H * hd, Hkv * hd, Hkv * hd]
+    N = sum(widths)
+    x = randn(r, 1, S, D)
+    w = randn(r, N, D, scale=0.1)
+    b = randn(r, N, scale=0.1)
+    g = Graph()
+    g.add_tensor("x", (1, S, D))
+    g.inputs.append("x")
+    g.add_tensor("w", (N, D)).buffer = w
+    g.add_tensor("b", (N,)).buffer = b
+    g.constants += ["w", "b"]
+    g.add_tensor("c", (1, S, N))
+    g.add_node(OpType.MATMUL_ADD, ["x", "w", "b"], "c", {"transpose_b": True})
+    col = 0
+    for name, heads, wd in (("q", H, widths[0]), ("k", Hkv, widths[1]), ("v", Hkv, widths[2])):
+        g.add_tensor(name + "2", (1, S, wd))
+        g.add_node(OpType.SLICE, ["c"], name + "2", {"dim": 2, "start": col, "end": col + wd})
+        g.add_tensor(name + "4", (1, S, heads, hd))
+        g.add_node(OpType.RESHAPE, [name + "2"], name + "4", {"shape": (1, S, heads, hd)})
+        g.add_tensor(name + "t", (1, heads, S, hd))
+        g.add_node(OpType.TRANSPOSE, [name + "4"], name + "t", {"dim0": 1, "dim1": 2})
+        col += wd
+    attrs = {"group_size": H // Hkv} if Hkv != H else {}
+    if causal:
+        attrs["causal"] = True
+    g.add_tensor("att", (1, H, S, hd))
+    g.add_node(OpType.ATTENTION, ["qt", "kt", "vt"], "att", attrs)
+    g.outputs.append("att")
+    if k_live:
+        g.outputs.append("kt")
+    c64 = x.astype(np.float64) @ w.T.astype(np.float64) + b
+    heads = []
+    col = 0
+    for hh, wd in zip((H, Hkv, Hkv), widths):
+        heads.append(np.ascontiguousarray(c64[..., col:col + wd].reshape(1, S, hh, hd).transpose(0, 2, 1, 3)))
+        col += wd
+    ref = cf_attention(*heads, causal=causal, group=H // Hkv)
+    ys = {}
+    for frag in ("1", "0"):
+        monkeypatch.setenv("LBR_KQ_FRAG", frag)
+        ex = CompiledExecutor(fuse=True)
+        ex.compile(plan(g))
+        try:
+            params = ex.step_params()
+            att = [p for p in params if p["kernel"].startswith("attn_fwd_kq")]
+            gem = [p for p in params if p["kernel"].startswith("gemm_")]
+            print(frag, [p["name"] for p in params], [p.get("k_frag") for p in att], [p.get("frag_splits") for p in gem])
+            assert len(att) == 1 and len(gem) == 1
+            on = frag == "1" and not k_live
+            assert att[0]["k_frag"] == on and gem[0]["frag_splits"] == (2 if on else 0)
+            ys[frag] = ex.run({"x": x})
+        finally:
+            ex.close()
+    np.testing.assert_array_equal(ys["1"]["att"], ys["0"]["att"])
+    assert normwise_rel(ys["1"]["att"], ref) <= 1e-4
+    if k_live:
+        assert normwise_rel(ys["1"]["kt"], heads[1]) <= 1e-5

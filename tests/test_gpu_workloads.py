@@ -70,6 +70,12 @@ def test_workload_parity_full_size(key, seq, kernels):
         # the folded schedule, not the key-range split, at 32 blocks x 32 heads
         att = [s for s in sess.executor.step_params() if s["kernel"] == "attn_fwd_mfma16_f32"]
         assert att and all(s["fold"] and not s["split_wg"] for s in att), att
+    if key == "gpt2_lm":
+        # each layer's key-quartered attention reads K fragment-major, as its QKV GEMM writes it
+        params = sess.executor.step_params()
+        att = [s for s in params if s["kernel"] == "attn_fwd_kq_f32"]
+        assert len(att) == 2 and all(s["k_frag"] for s in att), att
+        assert sum(1 for s in params if s.get("frag_splits") == 2) == 2, params
     t1 = time.time()
     o = OracleRun(sess.memory_plan).run({graph.inputs[0]: x})[graph.outputs[0]]
     sess.close()
