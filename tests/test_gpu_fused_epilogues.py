@@ -349,19 +349,22 @@ def test_attention_output_relay(monkeypatch, H, S, hd, causal):
     assert normwise_rel(ys["1"][0], ref) <= 1e-4
 
 
-@pytest.mark.parametrize("H,Hkv,S,hd,causal,k_live", [(12, 12, 256, 64, True, False), (8, 2, 512, 64, True, False),
-                                                      (4, 4, 128, 32, False, False), (12, 12, 256, 64, True, True)])
-def test_attention_fragment_major_keys(monkeypatch, H, Hkv, S, hd, causal, k_live):
+@pytest.mark.parametrize("H,Hkv,S,hd,causal,k_live,D", [(12, 12, 256, 64, True, False, 96),
+                                                        (8, 2, 512, 64, True, False, 96),
+                                                        (4, 4, 128, 32, False, False, 96),
+                                                        (12, 12, 256, 64, True, True, 96),
+                                                        (4, 4, 192, 64, True, False, 100)])
+def test_attention_fragment_major_keys(monkeypatch, H, Hkv, S, hd, causal, k_live, D):
     """x → MATMUL_ADD → q/k/v (SLICE → RESHAPE → TRANSPOSE(1, 2)) → key-quartered ATTENTION: the
     QKV GEMM's head scatter stores K fragment-major (16-row × 16-column chunks of 1 KiB) and the
     attention loads it so, whole cache lines per load.  Bit-equal to the row-major plan
     (LBR_KQ_FRAG=0), within 1e-4 of the float64 closed form.  With K also a graph output the
-    plan keeps K row-major (the caller reads it), and the returned K matches the closed form."""
+    plan keeps K row-major (the caller reads it), and the returned K matches the closed form.
+    D = 100 is not a multiple of the DMA GEMM's K step: the other MFMA kernel's head scatter."""
     from helpers import cf_attention
     from runtime.executor.compiled import CompiledExecutor
     from runtime.planner import plan
     r = rng(H * S + hd + 7)
-    D = 96
     widths = [H * hd, Hkv * hd, Hkv * hd]
     N = sum(widths)
     x = randn(r, 1, S, D)
@@ -410,6 +413,7 @@ def test_attention_fragment_major_keys(monkeypatch, H, Hkv, S, hd, causal, k_liv
             gem = [p for p in params if p["kernel"].startswith("gemm_")]
             print(frag, [p["name"] for p in params], [p.get("k_frag") for p in att], [p.get("frag_splits") for p in gem])
             assert len(att) == 1 and len(gem) == 1
+            assert gem[0]["kernel"].startswith("gemm_dma" if D % 32 == 0 else "gemm_mfma")
             on = frag == "1" and not k_live
             assert att[0]["k_frag"] == on and gem[0]["frag_splits"] == (2 if on else 0)
             ys[frag] = ex.run({"x": x})
