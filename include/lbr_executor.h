@@ -236,6 +236,11 @@ int lbr_plan_node_kernel(const lbr_plan* plan, int index, char* name_out,
                                       leading dims) → RMSNORM | LAYERNORM: the norm kernel adds,
                                       writes the sum and normalises it (a plan step join; not
                                       reported by lbr_fusion_windows)                      */
+#define LBR_FUSE_GEMM_HEAD_PROLOGUE 13 /* MATMUL[_ADD] → the HEAD_PROLOGUE run(s) of its output
+                                      (the Q and K of a layer, head dim 128): the GEMM runs
+                                      64×128 tiles, one head each, and normalises, rotates
+                                      and stores each head in its epilogue (a plan step join;
+                                      not reported by lbr_fusion_windows)                  */
 
 typedef struct {
     int first;   /* index of the run's first node */

@@ -277,6 +277,7 @@ struct lbr_plan {
     hipGraphExec_t exec = nullptr;
     void* ws = nullptr;          // shared step workspace (split-K partial sums)
     void* relay = nullptr;       // attention outputs moved off their inputs (lbr_relay_ok)
+    void* head_relay = nullptr;  // Q/K head outputs moved off a GEMM's input (relay_head_outputs)
 };
 
 static void free_plan(lbr_plan* p) {
@@ -284,6 +285,7 @@ static void free_plan(lbr_plan* p) {
     if (p->graph) (void)hipGraphDestroy(p->graph);
     if (p->ws) (void)hipFree(p->ws);
     if (p->relay) (void)hipFree(p->relay);
+    if (p->head_relay) (void)hipFree(p->head_relay);
     delete p;
 }
 
@@ -312,6 +314,46 @@ static int relay_attention_outputs(lbr_plan* p, const OpNode* nodes, int n_nodes
         const bool v = strstr(nm, "+v") != nullptr, t = strstr(nm, "+transpose") != nullptr;
         p->steps[i].name = lbr_attn_step_name(p->steps[i], v, t, 2);
         p->steps[i + 1].in[0] = p->relay;
+    }
+    return LBR_OK;
+}
+
+// Q/K head outputs that a GEMM's head-prologue epilogue would write over the
+// GEMM's own input A (lbr_merge_gemm_head_prologue sets Step::i[27] to the
+// ATTENTION node that alone reads them, + 1): one buffer of the plan's own takes
+// them, and that attention's step reads Q and K there.  One buffer serves every
+// layer: the steps run in order, and each attention has read its Q and K before
+// the next such GEMM writes.
+static int relay_head_outputs(lbr_plan* p) {
+    auto bytes = [](const Step& g, int part) {
+        return part < g.i[18] ? ((size_t)(g.i[0] * g.i[22 + part] * 128) * sizeof(float) + 255) / 256 * 256 : 0;
+    };
+    std::vector<std::pair<size_t, size_t>> picks;
+    size_t need = 0;
+    for (size_t gi = 0; gi < p->steps.size(); ++gi) {
+        const Step& g = p->steps[gi];
+        if (g.i[18] <= 0 || g.i[27] <= 0) continue;
+        const int node = (int)g.i[27] - 1;
+        size_t ai = gi + 1;
+        while (ai < p->steps.size() &&
+               !(p->steps[ai].node_index <= node && node < p->steps[ai].node_index + p->steps[ai].n_nodes))
+            ++ai;
+        if (ai >= p->steps.size() || p->steps[ai].in[0] != g.in[4] ||
+            (g.i[18] == 2 && p->steps[ai].in[1] != g.in[5])) {
+            lbr_set_error("lbr_plan_create: the attention that reads head outputs of GEMM node %d is not node %d's "
+                          "step", g.node_index, node);
+            return LBR_ERR_INVALID;
+        }
+        picks.push_back({gi, ai});
+        need = std::max(need, bytes(g, 0) + bytes(g, 1));
+    }
+    if (picks.empty()) return LBR_OK;
+    HIP_TRY(hipMalloc(&p->head_relay, need));
+    for (const auto& pa : picks) {
+        Step& g = p->steps[pa.first];
+        Step& a = p->steps[pa.second];
+        g.in[4] = a.in[0] = p->head_relay;
+        if (g.i[18] == 2) g.in[5] = a.in[1] = (char*)p->head_relay + bytes(g, 0);
     }
     return LBR_OK;
 }
@@ -534,6 +576,12 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
             }
             // a norm of this GEMM's split-K output runs in its reduce kernel
             if (i < n_nodes && (r >= runs.size() || runs[r].first != i) && lbr_merge_reduce_norm(&s, decoded[i])) ++i;
+            // the Q/K head prologues of a plain GEMM's output run in its epilogue
+            if (s.fuse_kind == LBR_FUSE_HEAD_PROLOGUE && !p->steps.empty() &&
+                lbr_merge_gemm_head_prologue(&p->steps.back(), s, nodes, n_nodes, live_ptr, live_bytes, n_live)) {
+                for (int k = s.node_index; k < s.node_index + s.n_nodes; ++k) p->node_step[k] = -1;
+                continue;
+            }
             p->steps.push_back(s);
         } else {
             // an ADD whose sum only a norm right after it reads first (a position
@@ -552,6 +600,7 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
         }
     }
     int rc = !fuse ? LBR_OK : relay_attention_outputs(p, nodes, n_nodes, live_ptr, live_bytes, n_live);
+    if (!rc && fuse) rc = relay_head_outputs(p);
     if (!rc && fuse) fragment_keys(p, nodes, n_nodes, live_ptr, live_bytes, n_live);
     if (!rc) rc = assign_workspace(p->steps, &p->ws);
     if (!rc) rc = autotune_gemms(p->steps);

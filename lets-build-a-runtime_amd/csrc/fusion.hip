@@ -193,6 +193,8 @@ __global__ __launch_bounds__(256) void head_rows4(HeadArgs4 a) {
     const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
     float4 xv[R], cv[R], sv[R], wv = zero;
 #pragma unroll
+    for (int k = 0; k < R; ++k) cv[k] = sv[k] = zero;   // read only with ROPE
+#pragma unroll
     for (int k = 0; k < R; ++k) {
         const int h = h0 + k * HPS;
         xv[k] = h < H ? *reinterpret_cast<const float4*>(x + (long long)h * HD) : zero;
@@ -229,29 +231,7 @@ __global__ __launch_bounds__(256) void head_rows4(HeadArgs4 a) {
     }
 #pragma unroll
     for (int k = 0; k < R; ++k) {
-        float v[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w};
-        if (NORM) {   // norm.c:100-107 order: x · (1/sqrt(Σx²/n + eps)) · w
-            const float ss = lbr_group_sum<LPR>((v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]));
-            const float scale = 1.0f / sqrtf(ss / HD + eps);
-            v[0] = v[0] * scale * wv.x;
-            v[1] = v[1] * scale * wv.y;
-            v[2] = v[2] * scale * wv.z;
-            v[3] = v[3] * scale * wv.w;
-        }
-        float4 y;
-        if (ROPE) {   // y = x·cos + rotate_half(x)·sin, rotate_half = cat(−x[half:], x[:half])
-            const float sign = l < LPR / 2 ? -1.0f : 1.0f;
-            const float c[4] = {cv[k].x, cv[k].y, cv[k].z, cv[k].w}, sn[4] = {sv[k].x, sv[k].y, sv[k].z, sv[k].w};
-            float o[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float rot = sign * lbr_half_partner<LPR>(v[q], lane);
-                o[q] = __fadd_rn(__fmul_rn(v[q], c[q]), __fmul_rn(rot, sn[q]));
-            }
-            y = make_float4(o[0], o[1], o[2], o[3]);
-        } else {
-            y = make_float4(v[0], v[1], v[2], v[3]);
-        }
+        const float4 y = lbr_head_row<LPR, HD>(xv[k], NORM, wv, eps, ROPE, cv[k], sv[k], lane);
         const int h = h0 + k * HPS;
         if (h < H) *reinterpret_cast<float4*>(out + (((long long)b * H + h) * a.S + s) * HD + d) = y;
     }
@@ -1611,6 +1591,153 @@ bool lbr_merge_head_steps(Step* a, const Step& b) {
     a->in[7] = b.out;
     a->f[1] = b.f[0];
     a->n_nodes += b.n_nodes;
+    return true;
+}
+
+// Joins the HEAD_PROLOGUE step h (one part, or the Q and K parts of a layer
+// joined by lbr_merge_head_steps; head dim 128) into the plain one-batch DMA GEMM
+// step g right before it, whose output C is h's source: g then runs 64×128 tiles,
+// and a tile that holds a head of a part normalises, rotates and stores it in
+// its epilogue with the float4 prologue kernel's lanes and sums (the same bits).
+// C's columns of the parts are not written, so no read of C other than a SLICE
+// of columns outside them may follow the prologue, and C may not be live-out.
+// The parts' outputs are written while the GEMM still reads A: where the planner
+// put them over A (dead once the GEMM alone has run), the step gets Step::i[27] =
+// the ATTENTION node that alone reads them (as Q and K) + 1, and the plan moves
+// them to a buffer of its own (relay_head_outputs).
+bool lbr_merge_gemm_head_prologue(Step* g, const Step& h, const OpNode* nodes, int n, const void* const* live_ptr,
+                                  const size_t* live_bytes, int n_live) {
+    const char* e = getenv("LBR_QKV_EPILOGUE");
+    if (e && atoi(e) == 0) return false;
+    if (h.fuse_kind != LBR_FUSE_HEAD_PROLOGUE || !h.i[13] || h.i[5] != 128) return false;
+    if (!g->name || strcmp(g->name, "gemm_dma_f32_nt") != 0 || g->fuse_kind != LBR_FUSE_NONE || g->n_nodes != 1)
+        return false;
+    // no other epilogue, no K split, no norm prologue or reduce norm, row-major A, one batch
+    if (g->i[3] != 1 || g->i[10] > 1 || g->i[19] || g->i[31] || g->i[32] || g->in[3] || g->i[15] || g->i[16] ||
+        g->i[35] || g->i[18] || g->i[5])
+        return false;
+    const long long M = g->i[0], N = g->i[1];
+    if (h.in[0] != g->out || h.i[0] != N || h.i[2] * h.i[3] != M || g->node_index + g->n_nodes != h.node_index)
+        return false;
+    if (N % 4 != 0 || !lbr_aligned(g->out, 16) || M * N >= (1LL << 31)) return false;
+    const int parts = h.i[14] == 2 ? 2 : 1;
+    const long long col[2] = {h.i[1], h.i[16]}, H[2] = {h.i[4], parts == 2 ? h.i[15] : 0};
+    for (int p = 0; p < parts; ++p)
+        if (col[p] % 128 != 0 || H[p] <= 0 || col[p] + H[p] * 128 > N) return false;
+    const bool rope = h.in[3] != nullptr, norm = h.in[2] != nullptr;
+    bool relay = false;
+    // RoPE rows shared by the heads, the same strides for cos and sin
+    if (rope && (h.i[7] != 0 || h.i[10] != 0 || h.i[6] != h.i[9] || h.i[8] != h.i[11])) return false;
+    // the parts' outputs are written while other workgroups still read A, B, the bias, the
+    // norm weights, the RoPE rows and the parts' biases (the planner may have put a prologue
+    // output over A, dead once the GEMM alone has run), and while other tiles write C
+    {
+        const long long K = g->i[2];
+        std::vector<Rng> reads{rng(g->in[0], M * K * 4), rng(g->in[1], N * K * 4), rng(g->out, M * N * 4)};
+        if (g->in[2]) reads.push_back(rng(g->in[2], N * 4));
+        for (int p = 0; p < parts; ++p) {
+            const void* w = p ? h.in[6] : h.in[2];
+            const void* pb = p ? h.in[5] : h.in[1];
+            if (w) reads.push_back(rng(w, 128 * 4));
+            if (pb) reads.push_back(rng(pb, H[p] * 128 * 4));
+        }
+        if (rope) {
+            const long long B = h.i[2], S = h.i[3];
+            const long long ext = ((B - 1) * h.i[6] + (S - 1) * h.i[8] + 128) * 4;
+            reads.push_back(rng(h.in[3], ext));
+            reads.push_back(rng(h.in[4], ext));
+        }
+        for (int p = 0; p < parts; ++p) {
+            const Rng o = rng(p ? h.in[7] : h.out, M * H[p] * 128 * 4);
+            for (size_t k = 0; k < reads.size(); ++k)
+                if (overlap(o, reads[k])) {
+                    if (k != 0) return false;
+                    relay = true;   // over A only: the outputs can move to a buffer of the plan's own
+                }
+        }
+        if (parts == 2 && overlap(rng(h.out, M * H[0] * 128 * 4), rng(h.in[7], M * H[1] * 128 * 4))) return false;
+    }
+    // moved outputs: after the run only one ATTENTION node reads them, as its Q (part 0) and K
+    // (part 1), and they are not live-out; its step then reads the plan's buffer
+    int relay_at = -1;
+    if (relay) {
+        for (int p = 0; p < parts; ++p) {
+            const void* op = p ? h.in[7] : h.out;
+            std::vector<Rng> rest{rng(op, M * H[p] * 128 * 4)};
+            for (int j = h.node_index + h.n_nodes; j < n && !rest.empty(); ++j) {
+                const OpNode* nd = &nodes[j];
+                const int reads = nd->op == OP_ATTENTION ? 3 + (nd->extra[3] != 0) : nd->n_inputs;
+                for (int q = 0; q < reads && q < nd->n_inputs && q < MAX_INPUTS; ++q) {
+                    const Rng in = input_rng(nd, q);
+                    bool hit = false;
+                    for (const Rng& r : rest) hit = hit || overlap(r, in);
+                    if (!hit) continue;
+                    if (nd->op != OP_ATTENTION || q != p || nd->inputs[q] != op || (relay_at >= 0 && relay_at != j))
+                        return false;
+                    relay_at = j;
+                }
+                subtract(&rest, out_rng(nd));
+            }
+            for (const Rng& r : rest)
+                for (int q = 0; q < n_live; ++q)
+                    if (overlap(r, rng(live_ptr[q], (long long)live_bytes[q]))) return false;
+        }
+        if (relay_at < 0) return false;
+    }
+    // C's columns of the parts are never written: after the prologue only SLICEs of other
+    // columns may read C (the V rows an attention takes), and C may not be live-out
+    {
+        const uintptr_t c0 = (uintptr_t)g->out, c1 = c0 + (uintptr_t)(M * N * 4);
+        std::vector<Rng> rest{Rng{c0, c1}};
+        for (int j = h.node_index + h.n_nodes; j < n && !rest.empty(); ++j) {
+            const OpNode* nd = &nodes[j];
+            const int reads = nd->op == OP_ATTENTION ? 3 + (nd->extra[3] != 0) : nd->n_inputs;
+            for (int q = 0; q < reads && q < nd->n_inputs && q < MAX_INPUTS; ++q) {
+                const Rng in = input_rng(nd, q);
+                bool hit = false;
+                for (const Rng& r : rest) hit = hit || overlap(r, in);
+                if (!hit) continue;
+                // a SLICE of C over its last dim: [outer, orig_dim, start, len, inner]
+                if (nd->op != OP_SLICE || q != 0 || nd->inputs[0] != g->out || nd->extra[0] != M ||
+                    nd->extra[1] != N || nd->extra[4] != 1)
+                    return false;
+                const long long a = nd->extra[2], b = a + nd->extra[3];
+                for (int p = 0; p < parts; ++p)
+                    if (a < col[p] + H[p] * 128 && col[p] < b) return false;
+            }
+            subtract(&rest, out_rng(nd));
+        }
+        for (const Rng& r : rest)
+            for (int q = 0; q < n_live; ++q)
+                if (overlap(r, rng(live_ptr[q], (long long)live_bytes[q]))) return false;
+    }
+    Step t = *g;
+    if (!gemm_dma_retile(&t, gemm_dma_tile_by_name("64x128"))) return false;
+    t.i[18] = parts;
+    for (int p = 0; p < 2; ++p) {
+        t.i[20 + p] = col[p];
+        t.i[22 + p] = H[p];
+    }
+    t.i[24] = (norm ? 1 : 0) | (rope ? 2 : 0);
+    t.i[27] = relay ? relay_at + 1 : 0;   // lbr_plan's relay_head_outputs moves the outputs
+    t.i[25] = rope ? h.i[6] : 0;
+    t.i[26] = rope ? h.i[8] : 0;
+    t.i[30] = h.i[3];
+    t.in[4] = h.out;
+    t.in[5] = parts == 2 ? h.in[7] : nullptr;
+    t.in[6] = h.in[2];
+    t.in[7] = parts == 2 ? h.in[6] : nullptr;
+    t.in[8] = h.in[3];
+    t.in[9] = h.in[4];
+    t.in[10] = h.in[1];
+    t.in[11] = parts == 2 ? h.in[5] : nullptr;
+    t.f[2] = h.f[0];
+    t.f[3] = parts == 2 ? h.f[1] : 0.f;
+    t.n_nodes += h.n_nodes;
+    t.fuse_kind = LBR_FUSE_GEMM_HEAD_PROLOGUE;
+    t.name = rope ? (norm ? "gemm_dma_f32_nt+head_norm_rope" : "gemm_dma_f32_nt+head_rope")
+                  : (norm ? "gemm_dma_f32_nt+head_norm" : "gemm_dma_f32_nt+head_transpose");
+    *g = t;
     return true;
 }
 

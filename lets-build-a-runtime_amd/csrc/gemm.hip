@@ -59,6 +59,21 @@ struct GemmArgs {
     const float* sbias[4];    // split k's bias row (indexed by column - col_begin[k]) or null
     int Hs[4], hd, S;         // heads of each split, head dim, rows per batch (M = B·S)
     int frag;                 // bit k: split k is stored fragment-major (lbr_frag_offset)
+    // Head prologue in the epilogue (lbr_merge_gemm_head_prologue; 64×128 DMA tile, hd =
+    // 128 = TN): C columns [hp_col[p], hp_col[p] + hp_H[p]·128) of part p hold heads of
+    // 128; each tile's C values (+ bias) go round through LDS, get the part's bias,
+    // per-head RMSNorm (weight hp_w[p], eps hp_eps[p]) and rotate-half RoPE (cos/sin row
+    // of token (b, s) at b·hp_tst[0] + s·hp_tst[1]) and are stored as [B, H, S, 128] at
+    // hp_out[p] (C's columns of the parts are not written); hp_flags: 1 norm, 2 RoPE
+    int hp_parts, hp_flags, hp_S;
+    int hp_col[2], hp_H[2];
+    float* hp_out[2];
+    const float* hp_w[2];
+    const float* hp_b[2];
+    float hp_eps[2];
+    const float* hp_cos;
+    const float* hp_sin;
+    long long hp_tst[2];
     int act;                  // LBR_ACT_*: a following RELU / GELU / SILU applied to C (DMA kernel)
     // Gated pair (DMA kernel): the GEMM's columns hold a gate half and an up half
     // of gF columns each; the kernel writes out[m][j] = act(gate[m][j] (+ gbias[j]))·up[m][j]
@@ -701,6 +716,63 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
             }
         }
     }
+    if constexpr (TM == 64 && TN == 128 && WGM == 2 && WGN == 2 && !AHEADS && NORM == 0) {
+        int p = -1;
+        for (int q = 0; q < g.hp_parts; ++q)
+            if (n0 >= g.hp_col[q] && n0 < g.hp_col[q] + g.hp_H[q] * TN) p = q;
+        if (p >= 0) {
+            // one head per tile: C (+ bias) through LDS, then each wavefront takes 16 rows,
+            // two a pass, a row over 32 lanes of 4 columns each — the lanes, sums and
+            // partner swaps of head_rows4 at HD = 128, so the values are the same bits
+            constexpr int TS = TN + 4;
+            static_assert(TM * TS <= NS * STAGE, "the tile fits in the stages");
+            __syncthreads();   // every wavefront's last fragment reads are done
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int c = wn * (TN / WGN) + j * 16 + cl;
+                const float bv = HAS_BIAS ? g.bias[n0 + c] : 0.f;
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        lds[(wm * (TM / WGM) + i * 16 + rq + r) * TS + c] =
+                            HAS_BIAS ? (acc[i][j][r] + bv) : g.alpha * acc[i][j][r];
+            }
+            __syncthreads();
+            const int H = g.hp_H[p], h = (n0 - g.hp_col[p]) / TN, S = g.hp_S;
+            const int l = lane & 31, d = 4 * l;
+            const bool norm = g.hp_flags & 1, rope = g.hp_flags & 2;
+            const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 wv = norm ? *reinterpret_cast<const float4*>(g.hp_w[p] + d) : zero;
+            const float* __restrict__ pbias = g.hp_b[p];
+            const float4 pb = pbias ? *reinterpret_cast<const float4*>(pbias + h * TN + d) : zero;
+            const float eps = g.hp_eps[p];
+#pragma unroll 2
+            for (int pass = 0; pass < TM / NW / 2; ++pass) {
+                const int row = wave * (TM / NW) + 2 * pass + (lane >> 5);
+                const int m = m0 + row, mc = min(m, M - 1);
+                const int b = mc / S, s = mc - b * S;
+                const float4 x = *reinterpret_cast<const float4*>(&lds[row * TS + d]);
+                float4 v = x;
+                if (pbias) {
+                    v.x = v.x + pb.x;
+                    v.y = v.y + pb.y;
+                    v.z = v.z + pb.z;
+                    v.w = v.w + pb.w;
+                }
+                float4 c4 = zero, s4 = zero;
+                if (rope) {
+                    const long long t = b * g.hp_tst[0] + s * g.hp_tst[1] + d;
+                    c4 = *reinterpret_cast<const float4*>(g.hp_cos + t);
+                    s4 = *reinterpret_cast<const float4*>(g.hp_sin + t);
+                }
+                const float4 y = lbr_head_row<32, TN>(v, norm, wv, eps, rope, c4, s4, lane);
+                if (m < M)
+                    *reinterpret_cast<float4*>(g.hp_out[p] + (((long long)b * H + h) * S + s) * TN + d) = y;
+            }
+            return;
+        }
+    }
     if (g.ksplit > 1) {
         float* __restrict__ Wp = g.W + ((long long)ks * gridDim.z + bz) * (long long)M * N;
 #pragma unroll
@@ -855,7 +927,7 @@ __global__ __launch_bounds__(256) void gemv_n(GemmArgs g) {
     c[n] = HAS_BIAS ? acc + g.bias[n] : g.alpha * acc;
 }
 
-// Step::i: [0]=M [1]=N [2]=K [3]=batches [4]=trans_b [5]=vec [6]=has_bias
+// Step::i: [0]=M [1]=N [2]=K [3]=batches [4]=trans_b [5]=fragment-major head splits [6]=has_bias
 //          [7]=sA [8]=sB [9]=sC [10]=ksplit [11]=kchunk [12]=float4 reduce
 //          [13]=1 (takes fused epilogues) [14]=DMA tile + 1 (0: gemm_mfma_f32)
 //          [19..30] head scatter, [31] activation, [32..34] gated pair, [35..37] A in
@@ -898,6 +970,25 @@ GemmArgs make_args(const Step& s) {
     g.hd = (int)s.i[29];
     g.S = (int)s.i[30];
     g.frag = (int)s.i[5];
+    // i[18] = head prologue parts (0: none; see lbr_merge_gemm_head_prologue), i[20..23]
+    // = their first columns and heads, i[24] = flags, i[25..26] = RoPE row strides over
+    // b and s, i[30] = S; in[4..5] outputs, in[6..7] norm weights, in[8..9] cos / sin,
+    // in[10..11] biases; f[2..3] eps
+    g.hp_parts = (int)s.i[18];
+    g.hp_flags = (int)s.i[24];
+    g.hp_S = (int)s.i[30];
+    for (int p = 0; p < 2; ++p) {
+        g.hp_col[p] = (int)s.i[20 + p];
+        g.hp_H[p] = (int)s.i[22 + p];
+        g.hp_out[p] = (float*)s.in[4 + p];
+        g.hp_w[p] = (const float*)s.in[6 + p];
+        g.hp_b[p] = (const float*)s.in[10 + p];
+        g.hp_eps[p] = s.f[2 + p];
+    }
+    g.hp_cos = (const float*)s.in[8];
+    g.hp_sin = (const float*)s.in[9];
+    g.hp_tst[0] = s.i[25];
+    g.hp_tst[1] = s.i[26];
     g.act = (int)s.i[31];
     // i[35..37] = A in head layout [B, H, S, hd]: H, S, hd (0: row-major A)
     g.aH = (int)s.i[35];
@@ -1349,6 +1440,17 @@ bool gemm_dma_retile(Step* s, int tile) {
 int gemm_dma_written(const Step& s, void** ptr, size_t* bytes, int cap) {
     const long long M = s.i[0], N = s.i[1];
     int n = 0;
+    if (s.i[18] > 0) {   // head-prologue epilogue: the parts' outputs, and C's other columns
+        for (int p = 0; p < s.i[18] && p < 2 && n < cap; ++p) {
+            ptr[n] = (void*)s.in[4 + p];
+            bytes[n++] = (size_t)(M * s.i[22 + p] * 128) * sizeof(float);
+        }
+        if (n < cap) {
+            ptr[n] = s.out;
+            bytes[n++] = (size_t)(M * N) * sizeof(float);
+        }
+        return n;
+    }
     if (s.i[19] > 0) {
         for (int k = 0; k < s.i[19] && k < 4 && n < cap; ++k) {
             ptr[n] = (void*)s.in[4 + k];

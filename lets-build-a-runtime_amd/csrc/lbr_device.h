@@ -138,6 +138,42 @@ __device__ __forceinline__ float lbr_half_partner(float v, int lane) {
     }
 }
 
+template <int LPR, int HD>
+__device__ __forceinline__ float4 lbr_head_row(float4 x, bool norm, float4 w, float eps, bool rope, float4 c4, float4 s4,
+                                               int lane) {
+#pragma clang fp contract(off)
+    float v[4] = {x.x, x.y, x.z, x.w};
+    if (norm) {
+        const float ss = lbr_group_sum<LPR>((v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]));
+        const float scale = 1.0f / sqrtf(ss / HD + eps);
+        v[0] = v[0] * scale * w.x;
+        v[1] = v[1] * scale * w.y;
+        v[2] = v[2] * scale * w.z;
+        v[3] = v[3] * scale * w.w;
+    }
+    if (!rope) return make_float4(v[0], v[1], v[2], v[3]);
+    const float sign = (lane % LPR) < LPR / 2 ? -1.0f : 1.0f;
+    const float c[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
+    float o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float rot = sign * lbr_half_partner<LPR>(v[q], lane);
+        o[q] = v[q] * c[q] + rot * sn[q];
+    }
+    return make_float4(o[0], o[1], o[2], o[3]);
+}
+
+// One head row of the float4 head prologue: LPR lanes hold the row's HD values,
+// 4 consecutive a lane (x, already biased).  RMSNorm (norm.c:100-107 order:
+// x · (1/sqrt(Σx²/HD + eps)) · w) and rotate-half RoPE (y = x·cos +
+// rotate_half(x)·sin, rotate_half = cat(−x[HD/2:], x[:HD/2]); the partner is LPR/2
+// lanes away).  Shared by the prologue kernel and the QKV GEMM's head epilogue,
+// with contraction off, so both round every multiply and add on its own and give
+// the same bits.  Every lane of the wavefront must take part (cross-lane sums).
+template <int LPR, int HD>
+__device__ __forceinline__ float4 lbr_head_row(float4 x, bool norm, float4 w, float eps, bool rope, float4 c4, float4 s4,
+                                               int lane);
+
 // Max over aligned groups of G lanes, as lbr_group_sum.
 template <int G>
 __device__ __forceinline__ float lbr_group_max(float s) {

@@ -72,6 +72,12 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s);
 // reads; false leaves a unchanged.
 bool lbr_merge_head_steps(Step* a, const Step& b);
 
+// Joins the HEAD_PROLOGUE step h into the plain DMA GEMM step g right before it
+// that writes h's source (head dim 128): g's 64×128 tiles apply the prologue in
+// their epilogue; false leaves g unchanged.
+bool lbr_merge_gemm_head_prologue(Step* g, const Step& h, const OpNode* nodes, int n, const void* const* live_ptr,
+                                  const size_t* live_bytes, int n_live);
+
 // Joins the TRANSPOSE_GEMM step t (the run right before u's) into the MLP
 // step u when u's input is t's output: u's kernel then computes that input
 // (and still writes it); false leaves u unchanged.

@@ -268,7 +268,8 @@ class CompiledExecutor(Executor):
         (attention: causal fold, key-range split workgroups, deferred output, key-quartered
         16-row kernel and whether it reads K fragment-major; GEMM: DMA tile
         index, K ranges, norm prologue, norm in the split-K reduce and whether the split was
-        made for it, head splits it stores fragment-major (bit mask); head prologue: float4 kernel or one wavefront per row, and
+        made for it, head splits it stores fragment-major (bit mask), head-prologue parts
+        its epilogue applies; head prologue: float4 kernel or one wavefront per row, and
         how many Q/K parts one launch covers)."""
         lib, h = self._lib, self._plan_handle
         first, count, kind = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
@@ -289,7 +290,8 @@ class CompiledExecutor(Executor):
                          tile=lib.lbr_gemm_tile_name(int(ints[14]) - 1).decode() or "legacy",
                          ksplit=max(1, int(ints[10])), dma_tile=int(ints[14]) - 1, norm=int(ints[15]),
                          reduce_norm=int(ints[16]), split_for_norm=bool(int(ints[17]) & 256),
-                         frag_splits=int(ints[5]) if int(ints[19]) > 0 else 0)
+                         frag_splits=int(ints[5]) if int(ints[19]) > 0 else 0,
+                         head_parts=int(ints[18]))
             elif d["kind"] == "head_prologue":
                 d.update(vec=bool(ints[13]), parts=int(ints[14]) if ints[13] else 1)
             out.append(d)

@@ -37,7 +37,7 @@ class LbrWindow(ctypes.Structure):
 
 FUSE_KINDS = {0: "none", 1: "gemm_resid", 2: "gemm_heads", 3: "head_prologue", 4: "attn_transpose",
               5: "gemm_act", 6: "gemm_gated", 7: "transpose_gemm", 8: "attn_sliced_v", 10: "norm_gemm",
-              11: "mlp", 12: "add_norm"}
+              11: "mlp", 12: "add_norm", 13: "gemm_head_prologue"}
 
 
 class HipLibrary:

@@ -46,6 +46,7 @@ def test_head_prologue_forms(monkeypatch, hd, bias, kernel):
     from runtime.exporter import export_model
     from runtime.session import Session
     from workloads import init_weights, reference_forward
+    monkeypatch.setenv("LBR_QKV_EPILOGUE", "0")   # the prologue kernels themselves (hd 128 joins the GEMM)
     m = init_weights(_Layer(hd, bias), seed=hd + bias)
     if bias:   # non-zero biases, so the bias add is exercised
         with torch.no_grad():
@@ -120,6 +121,7 @@ def test_head_prologue_per_head_tables(monkeypatch, hd, H, merge):
     from runtime.exporter import export_model
     from runtime.session import Session
     from workloads import init_weights, reference_forward
+    monkeypatch.setenv("LBR_QKV_EPILOGUE", "0")
     S = 40
     m = init_weights(_PerHeadTables(H, hd, S), seed=hd)
     with torch.no_grad():   # non-trivial norm weights
@@ -146,3 +148,115 @@ def test_head_prologue_per_head_tables(monkeypatch, hd, H, merge):
     print(f"per-head tables hd={hd} H={H} merge={merge}: fused-vs-unfused {e_fz:.2e}, vs torch64 {e_ref:.2e}")
     assert e_fz <= 1e-5
     assert e_ref <= 1e-3
+
+
+class _SharedTables(torch.nn.Module):
+    """Q/K prologues with RoPE rows shared by the heads ([1, 1, S, hd], as Qwen3's rotary
+    embedding gives them), head dim 128."""
+
+    def __init__(self, H, S, bias):
+        super().__init__()
+        from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+        hd = 128
+        self.H, self.hd = H, hd
+        self.qp = torch.nn.Linear(2 * H * hd, H * hd, bias=bias)
+        self.kp = torch.nn.Linear(2 * H * hd, H * hd, bias=bias)
+        self.vp = torch.nn.Linear(2 * H * hd, H * hd, bias=bias)
+        self.qn, self.kn = Qwen3RMSNorm(hd, eps=1e-6), Qwen3RMSNorm(hd, eps=1e-5)
+        g = torch.Generator().manual_seed(H + S)
+        self.register_buffer("cos", torch.randn(1, 1, S, hd, generator=g))
+        self.register_buffer("sin", torch.randn(1, 1, S, hd, generator=g))
+
+    def forward(self, x):
+        B, S, _ = x.shape
+        H, hd = self.H, self.hd
+        q = self.qn(self.qp(x).view(B, S, H, hd)).transpose(1, 2)
+        k = self.kn(self.kp(x).view(B, S, H, hd)).transpose(1, 2)
+        v = self.vp(x).view(B, S, H, hd).transpose(1, 2)
+        q = q * self.cos + _rotate_half(q) * self.sin
+        k = k * self.cos + _rotate_half(k) * self.sin
+        return torch.cat([q, k, v], dim=1)
+
+
+@pytest.mark.parametrize("bias,merge,S", [(False, True, 64), (True, True, 40), (False, False, 64), (True, True, 100)])
+def test_head_prologue_in_qkv_epilogue(monkeypatch, bias, merge, S):
+    """At head dim 128 the Q and K prologues run in the QKV GEMM's epilogue: 64×128 tiles, one
+    head each, normalised and rotated from LDS with the float4 prologue kernel's lanes and sums,
+    so the output equals the GEMM + prologue-kernel plan (LBR_QKV_EPILOGUE=0) bit for bit.
+    Apart (LBR_HEAD_MERGE=0) only the Q prologue, right after the GEMM, joins it.  S = 40 and 100 leave partial 64-row tiles and a batch boundary inside a tile (B = 2).  The
+    join needs a GEMM without K ranges."""
+    from runtime.exporter import export_model
+    from runtime.executor.compiled import CompiledExecutor
+    from runtime.ir import OpType
+    from runtime.passes import run_pipeline
+    from runtime.planner import plan
+    from workloads import init_weights, reference_forward
+    H = 4
+    m = init_weights(_SharedTables(H, S, bias), seed=S + bias)
+    with torch.no_grad():
+        m.qn.weight.normal_(1.0, 0.3)
+        m.kn.weight.normal_(1.0, 0.3)
+        if bias:
+            for p in (m.qp.bias, m.kp.bias, m.vp.bias):
+                p.normal_(0.0, 0.5)
+    x = np.random.default_rng(S).standard_normal((2, S, 2 * H * 128)).astype(np.float32)
+    g = export_model(m, (torch.from_numpy(x),))
+    run_pipeline(g, None)
+    mm = [n for n in g.nodes.values() if n.op in (OpType.MATMUL, OpType.MATMUL_ADD)]
+    assert len(mm) == 1   # q, k and v projections merged into one GEMM
+    out = g.outputs[0]
+    if not merge:
+        monkeypatch.setenv("LBR_HEAD_MERGE", "0")
+    # at M = 2·S the model would cut K of this GEMM into ranges, and the epilogue needs one
+    # (Qwen3's M = 1024 takes one anyway); the same single range in every plan compared
+    monkeypatch.setenv("LBR_GEMM_KSPLIT", "1")
+    ys = []
+    for env in ("1", "0", "nofuse"):
+        monkeypatch.setenv("LBR_QKV_EPILOGUE", "0" if env == "0" else "1")
+        ex = CompiledExecutor(fuse=env != "nofuse")
+        ex.compile(plan(g))
+        try:
+            params = ex.step_params()
+            joined = [p for p in params if p["kind"] == "gemm_head_prologue"]
+            heads = [p for p in params if p["kind"] == "head_prologue"]
+            print(env, [(p["name"], p.get("head_parts")) for p in params])
+            if env == "1":
+                assert len(joined) == 1 and joined[0]["tile"] == "64x128", params
+                assert joined[0]["head_parts"] == (2 if merge else 1) and len(heads) == (0 if merge else 1)
+            elif env != "nofuse":
+                assert not joined and len(heads) == (1 if merge else 2)
+            ys.append(ex.run({g.inputs[0]: x})[out])
+        finally:
+            ex.close()
+    np.testing.assert_array_equal(ys[0], ys[1])
+    ref = reference_forward(m, x)
+    e_fz, e_ref = normwise_rel(ys[0], ys[2]), normwise_rel(ys[0], ref)
+    print(f"qkv epilogue bias={bias} merge={merge} S={S}: fused-vs-unfused {e_fz:.2e}, "
+          f"vs torch64 {e_ref:.2e}")
+    assert e_fz <= 1e-5
+    assert e_ref <= 1e-3
+
+
+@pytest.mark.parametrize("S", [512, 1024])
+def test_qkv_epilogue_in_qwen3_layer(monkeypatch, S):
+    """A Qwen3-4B-shaped layer (32/8 heads of 128, hidden 2560): the planner puts the Q/K
+    prologue outputs over the QKV GEMM's input, which the epilogue cannot write while other
+    workgroups still read it, so the plan moves them to a buffer of its own and points the
+    attention's Q and K there.  Bit-equal to the GEMM + prologue-kernel plan."""
+    from runtime.exporter import export_model
+    from runtime.session import Session
+    from workloads import Qwen3Body, init_weights
+    m = init_weights(Qwen3Body(n_layer=1), seed=0)
+    x = np.random.default_rng(S).standard_normal((1, S, 2560)).astype(np.float32)
+    g = export_model(m, (torch.from_numpy(x),))
+    ys = []
+    for env in ("1", "0"):
+        monkeypatch.setenv("LBR_QKV_EPILOGUE", env)
+        sess = Session(copy.deepcopy(g))
+        sess.create()
+        kinds = [p["kind"] for p in sess.executor.step_params()]
+        print(env, [p["name"] for p in sess.executor.step_params()])
+        assert ("gemm_head_prologue" in kinds) == (env == "1") and ("head_prologue" in kinds) == (env == "0")
+        ys.append(sess.run({g.inputs[0]: x})[g.outputs[0]])
+        sess.close()
+    np.testing.assert_array_equal(ys[0], ys[1])
