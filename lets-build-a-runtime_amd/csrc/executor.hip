@@ -278,6 +278,7 @@ struct lbr_plan {
     void* ws = nullptr;          // shared step workspace (split-K partial sums)
     void* relay = nullptr;       // attention outputs moved off their inputs (lbr_relay_ok)
     void* head_relay = nullptr;  // Q/K head outputs moved off a GEMM's input (relay_head_outputs)
+    void* gated_relay = nullptr; // gated-pair outputs moved off their GEMM's input (relay_gated_outputs)
 };
 
 static void free_plan(lbr_plan* p) {
@@ -286,6 +287,7 @@ static void free_plan(lbr_plan* p) {
     if (p->ws) (void)hipFree(p->ws);
     if (p->relay) (void)hipFree(p->relay);
     if (p->head_relay) (void)hipFree(p->head_relay);
+    if (p->gated_relay) (void)hipFree(p->gated_relay);
     delete p;
 }
 
@@ -354,6 +356,34 @@ static int relay_head_outputs(lbr_plan* p) {
         Step& a = p->steps[pa.second];
         g.in[4] = a.in[0] = p->head_relay;
         if (g.i[18] == 2) g.in[5] = a.in[1] = (char*)p->head_relay + bytes(g, 0);
+    }
+    return LBR_OK;
+}
+
+// Gated-pair GEMM steps whose output the planner put over the GEMM's own input
+// A (GEMM_GATED with FusedRun::relay_out, Step::i[28]): one buffer of the plan's
+// own takes the output, and the GEMM right after, its only reader, reads A there
+// (one buffer for every layer: the steps run in order).
+static int relay_gated_outputs(lbr_plan* p) {
+    std::vector<size_t> picks;
+    size_t need = 0;
+    for (size_t i = 0; i < p->steps.size(); ++i) {
+        const Step& s = p->steps[i];
+        if (s.fuse_kind != LBR_FUSE_GEMM_GATED || s.i[28] != 1) continue;
+        if (i + 1 >= p->steps.size() || p->steps[i + 1].in[0] != s.out || !p->steps[i + 1].name ||
+            strncmp(p->steps[i + 1].name, "gemm_", 5) != 0) {
+            lbr_set_error("lbr_plan_create: the gated GEMM at node %d is not followed by the GEMM reading its "
+                          "output as A", s.node_index);
+            return LBR_ERR_INVALID;
+        }
+        picks.push_back(i);
+        need = std::max(need, (size_t)(s.i[0] * s.i[32]) * sizeof(float));
+    }
+    if (picks.empty()) return LBR_OK;
+    HIP_TRY(hipMalloc(&p->gated_relay, need));
+    for (size_t i : picks) {
+        p->steps[i].out = p->gated_relay;
+        p->steps[i + 1].in[0] = p->gated_relay;
     }
     return LBR_OK;
 }
@@ -601,6 +631,7 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
     }
     int rc = !fuse ? LBR_OK : relay_attention_outputs(p, nodes, n_nodes, live_ptr, live_bytes, n_live);
     if (!rc && fuse) rc = relay_head_outputs(p);
+    if (!rc && fuse) rc = relay_gated_outputs(p);
     if (!rc && fuse) fragment_keys(p, nodes, n_nodes, live_ptr, live_bytes, n_live);
     if (!rc) rc = assign_workspace(p->steps, &p->ws);
     if (!rc) rc = autotune_gemms(p->steps);

@@ -619,6 +619,32 @@ bool match_head_chain(const OpNode* nodes, int n, int p, const void* C, long lon
 }
 
 // Extent of a GEMM's inputs (A, B, bias) for the overlap test.
+// GEMM_GATED over its own A: the gated output y (at ptr) can move to a buffer of
+// the plan's own when node `next` is a GEMM that reads it as A, no other read sees
+// y's bytes before they are overwritten, and y is not live-out.
+bool gated_relay_ok(const OpNode* nodes, int n, int next, const void* ptr, Rng y, const std::vector<Rng>& live) {
+    const char* e = getenv("LBR_GATED_RELAY");
+    if (e && atoi(e) == 0) return false;
+    if (next >= n || (nodes[next].op != OP_MATMUL && nodes[next].op != OP_MATMUL_ADD) || nodes[next].inputs[0] != ptr)
+        return false;
+    std::vector<Rng> rest{y};
+    for (int j = next; j < n && !rest.empty(); ++j) {
+        const OpNode* nd = &nodes[j];
+        const int reads = nd->op == OP_ATTENTION ? 3 + (nd->extra[3] != 0) : nd->n_inputs;
+        for (int k = 0; k < reads && k < nd->n_inputs && k < MAX_INPUTS; ++k) {
+            if (j == next && k == 0) continue;   // the read that moves to the buffer
+            const Rng in = input_rng(nd, k);
+            for (const Rng& r : rest)
+                if (overlap(r, in)) return false;
+        }
+        subtract(&rest, out_rng(nd));
+    }
+    for (const Rng& r : rest)
+        for (const Rng& l : live)
+            if (overlap(r, l)) return false;
+    return true;
+}
+
 void gemm_input_rngs(const OpNode* g, const Step& st, std::vector<Rng>* r) {
     const long long M = st.i[0], N = st.i[1], K = st.i[2], batches = st.i[3];
     const bool b2d = g->extra[2] != 0;
@@ -1092,7 +1118,11 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
                         const Rng y = out_rng(ga);
                         std::vector<Rng> reads = gin;
                         if (gb) reads.push_back(rng(gb, (long long)F * 4));
-                        bool ok = !any_overlap(y, reads);
+                        bool ok = !any_overlap(y, reads), relay = false;
+                        if (!ok && overlap(y, reads[0]) &&
+                            !any_overlap(y, std::vector<Rng>(reads.begin() + 1, reads.end())) &&
+                            gated_relay_ok(nodes, n, i + 4, ga->output, y, live))
+                            ok = relay = true;
                         if (ok) ok = dead_after(nodes, n, i + 4, {c_r, out_rng(s1), out_rng(s2)}, {y}, live);
                         if (ok) {
                             FusedRun f;
@@ -1104,6 +1134,7 @@ int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, co
                             f.gact = ga->extra[1];
                             f.gbias = gb;
                             f.out = ga->output;
+                            f.relay_out = relay;
                             out->push_back(f);
                             i += 4;
                             continue;
@@ -1446,6 +1477,7 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
             s->i[33] = f.gact;
             s->i[34] = f.gate_base;
             s->in[3] = f.gbias;
+            s->i[28] = f.relay_out ? 1 : 0;   // relay_gated_outputs moves the output
             s->name = "gemm_dma_f32_nt+gated";
         }
     } else if (f.kind == LBR_FUSE_GEMM_RESID || f.kind == LBR_FUSE_GEMM_HEADS) {

@@ -34,6 +34,10 @@ struct FusedRun {
     // GATED_ACT's act code and bias (`out` is the GATED_ACT output)
     int gF = 0, gate_base = 0, gact = 0;
     const void* gbias = nullptr;
+    // GEMM_GATED: the output lies over the GEMM's A (the planner's reuse of a dead
+    // input), and only the A of the GEMM right after reads it: the plan writes it into a
+    // buffer of its own and points that GEMM there (relay_gated_outputs)
+    bool relay_out = false;
     // TRANSPOSE_GEMM: the GEMM's A in head layout [B, H, S, hd] at `src`; `resid` /
     // `out` set when the residual ADD is fused as well (B, S, hd and Hs[0] = H)
     // ATTN_SLICED_V: the ATTENTION is node first + attn_at; V rows come from `src`

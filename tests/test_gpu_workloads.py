@@ -268,3 +268,27 @@ def test_node_profile_adds_up_to_the_replayed_step():
         assert 0.8 * step_ms <= total <= 1.2 * step_ms
     finally:
         s.close()
+
+
+def test_gated_relay_matches_unrelayed(monkeypatch):
+    """Qwen3-4B-shaped LM at S=1024: the planner puts each layer's gated-FFN output over the
+    gate/up GEMM's own input, so the fused gated GEMM would overwrite A rows other workgroups
+    still read; the plan writes that output into a buffer of its own instead and points the
+    down projection there.  Bit-equal to the plan that leaves the chain unfused
+    (LBR_GATED_RELAY=0: SLICE, SLICE, GATED_ACT kernels)."""
+    from workloads import export_workload
+    from runtime.session import Session
+    import copy
+    _, x, graph = export_workload("qwen3_4b_lm")
+    ys = []
+    for relay in ("1", "0"):
+        monkeypatch.setenv("LBR_GATED_RELAY", relay)
+        s = Session(copy.deepcopy(graph))
+        s.create()
+        names = [p["name"] for p in s.executor.step_params()]
+        gated = [n for n in names if n.endswith("+gated")]
+        print(relay, names)
+        assert len(gated) == (2 if relay == "1" else 0), names
+        ys.append(s.run({graph.inputs[0]: x})[graph.outputs[0]])
+        s.close()
+    np.testing.assert_array_equal(ys[0], ys[1])
