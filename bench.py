@@ -522,6 +522,7 @@ def main() -> int:
                    "fused_runs": head["fused_runs"]},
         "roofline": head["roofline"],
         "kernels": head["kernels"],
+        "schedule": head["schedule"],
         "parity": head["parity"],
         "cpu_baseline": cpu,
     }

@@ -421,52 +421,68 @@ static bool bad_live(const void* const* live_ptr, const size_t* live_bytes, int 
     return n_live < 0 || (n_live > 0 && (!live_ptr || !live_bytes));
 }
 
-// Measured tiles of the workloads' GEMM steps (MI355X): where repeated plan
-// creations with the timing below picked another tile than the model.  A listed
-// step (same step name and M, N, K) takes its tile without timing, so plans
+// Measured tiles of the workloads' GEMM steps (MI355X): where timing each step
+// in its plan (every tile, and K splits of 1 to 8 ranges) found a faster tile
+// than the model's.  A listed step (same step name and M, N, K) takes its
+// tile, and its number of K ranges when `ks` > 0, without timing, so plans
 // come out the same run to run; the model's pick holds for every other step.
-// Every tile sums each output's K terms in the same order: the choice never
-// changes a result bit.
+// Every tile sums each output's K terms in the same order: the tile never
+// changes a result bit; another number of K ranges sums the ranges' partial
+// sums instead (a step whose reduce carries a norm keeps its ranges).
 struct TunedTile {
     const char* step;
     long long M, N, K;
     const char* tile;
+    int ks;   // K ranges; 0: the step's own
 };
 static const TunedTile kTunedTiles[] = {
-    // GPT-2-width QKV and FFN1 (512 rows): 64×64 leaves a fractional last round
-    // of 4-workgroup CUs; 24.9 µs against 31.0 and 26.8 against 31.3
-    {"gemm_dma_f32_nt+heads", 512, 2304, 768, "32x48"},
-    {"gemm_dma_f32_nt+act", 512, 3072, 768, "32x48"},
-    // GPT-2 QKV (1024 rows): 4 of 6 timings, 40.6 µs against 43.8 for 64×64
-    {"gemm_dma_f32_nt+heads", 1024, 2304, 768, "32x48s4"},
+    // GPT-2-width block (512 rows; µs for the listed tile against the model's)
+    {"gemm_dma_f32_nt+heads", 512, 2304, 768, "32x160", 0},      // QKV: 24.6 against 26.6 (32x48)
+    {"gemm_dma_f32_nt+tin+resid", 512, 768, 768, "32x64", 1},    // O proj: 12.2 against 14.1 (64x64, 2 ranges)
+    {"gemm_dma_f32_nt+act", 512, 3072, 768, "32x64", 0},         // FFN1: 25.6 against 27.5 (32x48)
+    {"gemm_dma_f32_nt+resid", 512, 768, 3072, "32x96", 2},       // FFN2: 28.2 against 30.4 (64x64, 8 ranges)
+    // GPT-2 body and LM (1024 rows)
+    {"gemm_dma_f32_nt+heads", 1024, 2304, 768, "32x96", 0},      // QKV: 34.9 against 43.3 (32x48s4)
+    {"gemm_dma_f32_nt+resid+layernorm", 1024, 768, 768, "32x96", 0},   // O proj + LN: 19.6 against 22.2
+    {"gemm_dma_f32_nt+resid", 1024, 768, 768, "32x96", 1},       // O proj (LM): 15.0 against 18.0 (64x64)
 };
 
-// Tile choice at plan creation.  A step listed in kTunedTiles takes its tile.
-// LBR_GEMM_AUTOTUNE=1 also times every other small one-batch, unsplit DMA GEMM
+// The tiles (and K ranges) of kTunedTiles, before the plan's workspace is
+// sized; marks the steps it set.  Skipped under LBR_GEMM_AUTOTUNE=0 or 2 and
+// under a tile forced by LBR_GEMM_TILE.
+static void table_tiles(std::vector<Step>& steps, std::vector<char>* tabled) {
+    tabled->assign(steps.size(), 0);
+    const char* env = getenv("LBR_GEMM_AUTOTUNE");
+    const int mode = env ? atoi(env) : -1;
+    if (mode == 0 || mode == 2 || getenv("LBR_GEMM_TILE")) return;
+    for (size_t i = 0; i < steps.size(); ++i) {
+        Step& s = steps[i];
+        if (!s.name || strncmp(s.name, "gemm_dma_f32", 12) != 0 || !s.i[14] || s.i[3] != 1) continue;
+        for (const TunedTile& t : kTunedTiles) {
+            if (strcmp(s.name, t.step) != 0 || s.i[0] != t.M || s.i[1] != t.N || s.i[2] != t.K) continue;
+            const int tile = gemm_dma_tile_by_name(t.tile);
+            Step u = s;
+            if (tile < 0 || !gemm_dma_retile(&u, tile) || (t.ks > 0 && !gemm_dma_set_ksplit(&u, t.ks))) continue;
+            s = u;
+            (*tabled)[i] = 1;
+        }
+    }
+}
+
+// Tile timing at plan creation (after table_tiles).  LBR_GEMM_AUTOTUNE=1 times
+// every small one-batch, unsplit DMA GEMM step the table did not set
 // (2^24 to 2^34 flops: larger ones run on the big tiles, which the model ranks
 // well; smaller ones last a few µs, which launch gaps would swamp) over every
 // tile its launcher family has — one warm-up launch, then three timed batches
 // of three launches, the fastest batch counting — and a tile at least 3% faster
-// than the model's choice replaces it; LBR_GEMM_AUTOTUNE=2 times the listed
-// steps too (to regenerate the table); LBR_GEMM_AUTOTUNE=0, or a tile forced
-// by LBR_GEMM_TILE, keeps the model's choice everywhere.  The ranges a timed
-// step writes are saved first and restored after, so plan creation leaves
-// memory as it found it.
-static int autotune_gemms(std::vector<Step>& steps) {
+// than the model's choice replaces it; LBR_GEMM_AUTOTUNE=2 ignores the table
+// (to regenerate it); unset or 0, or a tile forced by LBR_GEMM_TILE, times
+// nothing.  The ranges a timed step writes are saved first and restored after,
+// so plan creation leaves memory as it found it.
+static int autotune_gemms(std::vector<Step>& steps, const std::vector<char>& tabled) {
     const char* env = getenv("LBR_GEMM_AUTOTUNE");
-    const int mode = env ? atoi(env) : -1;   // -1: the table only
-    if (mode == 0 || getenv("LBR_GEMM_TILE")) return LBR_OK;
-    std::vector<char> tabled(steps.size(), 0);
-    if (mode != 2)
-        for (size_t i = 0; i < steps.size(); ++i) {
-            Step& s = steps[i];
-            if (!s.name || strncmp(s.name, "gemm_dma_f32", 12) != 0 || !s.i[14] || s.i[10] > 1 || s.i[3] != 1) continue;
-            for (const TunedTile& t : kTunedTiles)
-                if (strcmp(s.name, t.step) == 0 && s.i[0] == t.M && s.i[1] == t.N && s.i[2] == t.K) {
-                    const int tile = gemm_dma_tile_by_name(t.tile);
-                    if (tile >= 0 && gemm_dma_retile(&s, tile)) tabled[i] = 1;
-                }
-        }
+    const int mode = env ? atoi(env) : -1;
+    if (getenv("LBR_GEMM_TILE")) return LBR_OK;
     if (mode < 1) return LBR_OK;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     void* save = nullptr;
@@ -475,7 +491,7 @@ static int autotune_gemms(std::vector<Step>& steps) {
     if (err == hipSuccess) err = hipEventCreate(&e1);
     for (size_t i = 0; i < steps.size() && err == hipSuccess; ++i) {
         Step& s = steps[i];
-        if (!s.name || strncmp(s.name, "gemm_dma_f32", 12) != 0 || tabled[i]) continue;
+        if (!s.name || strncmp(s.name, "gemm_dma_f32", 12) != 0 || tabled[i] || s.i[10] > 1) continue;
         int cand[16];
         const int nc = gemm_dma_tune_candidates(s, cand, 16);
         // below 2^24 flops a launch lasts a few µs and the timing measures launch
@@ -633,8 +649,10 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
     if (!rc && fuse) rc = relay_head_outputs(p);
     if (!rc && fuse) rc = relay_gated_outputs(p);
     if (!rc && fuse) fragment_keys(p, nodes, n_nodes, live_ptr, live_bytes, n_live);
+    std::vector<char> tabled;
+    if (!rc) table_tiles(p->steps, &tabled);
     if (!rc) rc = assign_workspace(p->steps, &p->ws);
-    if (!rc) rc = autotune_gemms(p->steps);
+    if (!rc) rc = autotune_gemms(p->steps, tabled);
     if (rc) {
         free_plan(p);
         return rc;

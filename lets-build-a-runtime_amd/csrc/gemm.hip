@@ -826,14 +826,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
         }
         return;
     }
-    if (g.gF) {
+    if (FN % 2 == 0 && g.gF) {   // tiles with an odd block count never take a gated pair
         // gated pair: blocks j (gate) and j+1 (up) of this wave hold the same 16
         // output columns; out = act(gate (+ gated bias))·up, rounded like the
         // unfused GEMM → SLICE → GATED_ACT chain
         const int F = g.gF;
         float* __restrict__ C = g.C + bz * (long long)M * F;
 #pragma unroll
-        for (int j = 0; j < FN; j += 2) {
+        for (int j = 0; j + 1 < FN; j += 2) {
             const int o = tn * (TN / 2) + ((wn * FN + j) >> 1) * 16 + cl;
             if (o >= F) continue;
             const float bg = HAS_BIAS ? g.bias[g.gbase + o] : 0.f;
@@ -1210,6 +1210,15 @@ constexpr DmaTile kDmaTiles[] = {
     {32, 48, 8, 2, 0.80, "32x48", false, false},     // 2 wavefronts (2×1) of 16×48, 20 KB LDS
     {32, 48, 5, 2, 0.80, "32x48s4", false, false},   // the same with 4 LDS stages, 40 KB
     {64, 96, 4, 4, 0.85, "64x96", false, true},      // 4 wavefronts (4×1) of 16×96, 40 KB LDS
+    // Narrow 4-wavefront tiles for GEMMs of 512-1024 rows and K = 768-3072 (MI355X,
+    // GEMM steps of the GPT-2-shaped workloads): one or two rounds of small
+    // workgroups, each wavefront with few MFMA blocks, beat the 2-wavefront 32×48 and
+    // the 64×64 tiles there by 5-20% (e.g. 1024×2304×768: 35.0 µs for 32×96 against
+    // 43.3 for 32×48s4).
+    {32, 160, 3, 4, 0.85, "32x160", false, false},   // 4 wavefronts (2×2) of 16×80, 48 KB LDS
+    {64, 32, 6, 4, 0.80, "64x32", false, false},     // 4 wavefronts (2×2) of 32×16, 24 KB LDS
+    {32, 64, 6, 4, 0.80, "32x64", false, true},      // 4 wavefronts (2×2) of 16×32, 24 KB LDS
+    {32, 96, 5, 4, 0.80, "32x96", false, false},     // 4 wavefronts (2×2) of 16×48, 32 KB LDS
 };
 constexpr int kNumDmaTiles = sizeof(kDmaTiles) / sizeof(kDmaTiles[0]);
 
@@ -1274,6 +1283,10 @@ step_fn dma_launcher(int tile) {
         case 5: return launch_gemm_dma<32, 48, 2, 1, 4, HAS_BIAS, AHEADS, NORM>;
         case 6: return launch_gemm_dma<32, 48, 2, 1, 2, HAS_BIAS, AHEADS, NORM, 4>;
         case 7: return launch_gemm_dma<64, 96, 4, 1, 3, HAS_BIAS, AHEADS, NORM>;
+        case 8: return launch_gemm_dma<32, 160, 2, 2, 3, HAS_BIAS, AHEADS, NORM>;
+        case 9: return launch_gemm_dma<64, 32, 2, 2, 4, HAS_BIAS, AHEADS, NORM>;
+        case 10: return launch_gemm_dma<32, 64, 2, 2, 4, HAS_BIAS, AHEADS, NORM>;
+        case 11: return launch_gemm_dma<32, 96, 2, 2, 4, HAS_BIAS, AHEADS, NORM>;
         default: return launch_gemm_dma<64, 64, 2, 2, 4, HAS_BIAS, AHEADS, NORM>;
     }
 }
@@ -1385,6 +1398,29 @@ bool gemm_dma_split2(Step* s) {
     s->i[10] = 2;
     s->i[11] = chunk;
     s->ws_bytes = (size_t)2 * M * N * sizeof(float);
+    return true;
+}
+
+// Sets the number of K ranges of a one-batch DMA GEMM step to ks (ranges of
+// whole 32-wide K steps; the split-K reduce then carries the step's bias,
+// activation, residual or head scatter).  False, leaving the step unchanged,
+// for epilogues the reduce does not carry (gated pair, head prologue, norm
+// prologue), for a reduce that already normalises, or when K does not split
+// into ks such ranges.
+bool gemm_dma_set_ksplit(Step* s, int ks) {
+    const long long M = s->i[0], N = s->i[1], K = s->i[2];
+    if (!s->i[14] || s->i[3] != 1 || ks < 1 || s->i[16] || s->i[32] || s->i[18] || s->i[15]) return false;
+    if (ks == 1) {
+        s->i[10] = 1;
+        s->i[11] = K;
+        s->ws_bytes = 0;
+        return true;
+    }
+    const long long chunk = ((K + ks - 1) / ks + DBK - 1) / DBK * DBK;
+    if ((K + chunk - 1) / chunk != ks) return false;
+    s->i[10] = ks;
+    s->i[11] = chunk;
+    s->ws_bytes = (size_t)ks * M * N * sizeof(float);
     return true;
 }
 

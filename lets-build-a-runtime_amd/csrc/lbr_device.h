@@ -415,6 +415,7 @@ bool gemm_dma_tile_pairs(int tile);
 // norm); false leaves the step unchanged.
 bool gemm_dma_split2(Step* s);
 bool gemm_dma_retile(Step* s, int tile);
+bool gemm_dma_set_ksplit(Step* s, int ks);
 // Index of the DMA tile called `name` ("32x48", "64x64" ...), or -1.
 int gemm_dma_tile_by_name(const char* name);
 int gemm_dma_written(const Step& s, void** ptr, size_t* bytes, int cap);

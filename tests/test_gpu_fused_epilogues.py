@@ -82,7 +82,8 @@ ACTS = {OpType.RELU: lambda v: np.maximum(v, 0.0), OpType.GELU: cf_gelu_tanh, Op
 @pytest.mark.parametrize("op", list(ACTS), ids=lambda o: o.name)
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("tile,ks,M,N,K", [(None, None, 300, 520, 96), ("256x256", "1", 300, 520, 96),
-                                           ("64x128", "1", 70, 130, 64), ("128x128", "3", 200, 300, 3072)])
+                                           ("64x128", "1", 70, 130, 64), ("128x128", "3", 200, 300, 3072),
+                                           ("32x64", "1", 70, 130, 64), ("32x96", "2", 200, 300, 768)])
 def test_gemm_activation_epilogue(monkeypatch, op, bias, tile, ks, M, N, K):
     if tile:
         monkeypatch.setenv("LBR_GEMM_TILE", tile)
@@ -96,7 +97,7 @@ def test_gemm_activation_epilogue(monkeypatch, op, bias, tile, ks, M, N, K):
     _check(g, {"a": a}, ACTS[op](c), "gemm_act")
 
 
-@pytest.mark.parametrize("tile", [None, "256x256", "128x128", "128x64", "64x128", "64x64", "64x96"])
+@pytest.mark.parametrize("tile", [None, "256x256", "128x128", "128x64", "64x128", "64x64", "64x96", "32x64"])
 @pytest.mark.parametrize("act,gbias,order,mm_bias", [("silu", False, 0, False), ("gelu", True, 1, True),
                                                       ("silu", True, 0, True), ("gelu", False, 1, False)])
 def test_gemm_gated_epilogue(monkeypatch, tile, act, gbias, order, mm_bias):
@@ -129,7 +130,8 @@ def test_gemm_gated_epilogue(monkeypatch, tile, act, gbias, order, mm_bias):
 
 
 @pytest.mark.parametrize("tile,ks", [(None, None), ("256x256", "1"), ("128x64", "1"), ("64x64", "1"),
-                                     ("32x48", "1"), ("32x48s4", "1"), ("64x96", "1"),
+                                     ("32x48", "1"), ("32x48s4", "1"), ("64x96", "1"), ("32x64", "1"), ("64x32", "2"),
+                                     ("32x96", "1"), ("32x160", "1"),
                                      ("128x128", "3")])
 @pytest.mark.parametrize("H,S,hd,N,bias,resid", [(4, 300, 64, 200, True, True), (2, 130, 128, 96, False, True),
                                                   (8, 64, 32, 520, True, False), (4, 40, 16, 64, True, True),

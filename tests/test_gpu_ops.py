@@ -71,7 +71,7 @@ DMA_CASES = [
 
 
 @pytest.mark.parametrize("tile", ["256x256", "128x128", "128x64", "64x128", "64x64",
-                                  "32x48", "32x48s4", "64x96"])
+                                  "32x48", "32x48s4", "64x96", "32x160", "64x32", "32x64", "32x96"])
 @pytest.mark.parametrize("M,N,K,batches,b2d", DMA_CASES)
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_gemm_dma_tiles(monkeypatch, tile, M, N, K, batches, b2d, with_bias):
@@ -82,7 +82,9 @@ def test_gemm_dma_tiles(monkeypatch, tile, M, N, K, batches, b2d, with_bias):
 
 @pytest.mark.parametrize("tile,ks,M,N,K,batches", [("128x128", 3, 200, 300, 3072, 1), ("256x256", 5, 70, 90, 800, 2),
                                                    ("64x128", 2, 130, 260, 64, 1), ("64x64", 3, 100, 70, 960, 1),
-                                                   ("32x48s4", 3, 100, 130, 960, 1), ("64x96", 2, 70, 200, 512, 2)])
+                                                   ("32x48s4", 3, 100, 130, 960, 1), ("64x96", 2, 70, 200, 512, 2),
+                                                   ("32x96", 2, 100, 130, 960, 1), ("64x32", 3, 70, 200, 512, 2),
+                                                   ("32x160", 2, 130, 260, 640, 1), ("32x64", 4, 100, 70, 1024, 1)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_gemm_dma_ksplit(monkeypatch, tile, ks, M, N, K, batches, with_bias):
     monkeypatch.setenv("LBR_GEMM_TILE", tile)
