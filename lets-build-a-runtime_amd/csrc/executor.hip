@@ -492,8 +492,8 @@ static int autotune_gemms(std::vector<Step>& steps, const std::vector<char>& tab
     for (size_t i = 0; i < steps.size() && err == hipSuccess; ++i) {
         Step& s = steps[i];
         if (!s.name || strncmp(s.name, "gemm_dma_f32", 12) != 0 || tabled[i] || s.i[10] > 1) continue;
-        int cand[16];
-        const int nc = gemm_dma_tune_candidates(s, cand, 16);
+        int cand[32];
+        const int nc = gemm_dma_tune_candidates(s, cand, 32);
         // below 2^24 flops a launch lasts a few µs and the timing measures launch
         // gaps, not the tile: the model's choice stands
         const double flops = 2.0 * (double)s.i[0] * (double)s.i[1] * (double)s.i[2];
@@ -649,6 +649,11 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
     if (!rc && fuse) rc = relay_head_outputs(p);
     if (!rc && fuse) rc = relay_gated_outputs(p);
     if (!rc && fuse) fragment_keys(p, nodes, n_nodes, live_ptr, live_bytes, n_live);
+    for (size_t i = 0; i < p->steps.size() && !rc; ++i)
+        if (!p->steps[i].run) {
+            lbr_set_error("lbr_plan_create: step %zu (node %d) has no kernel", i, p->steps[i].node_index);
+            rc = LBR_ERR_INVALID;
+        }
     std::vector<char> tabled;
     if (!rc) table_tiles(p->steps, &tabled);
     if (!rc) rc = assign_workspace(p->steps, &p->ws);

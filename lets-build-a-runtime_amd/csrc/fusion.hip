@@ -746,8 +746,8 @@ bool match_transpose_gemm(const OpNode* nodes, int n, int i, const std::vector<R
     if (!(nd->out_shape[0] == B && nd->out_shape[1] == S && nd->out_shape[2] == H && nd->out_shape[3] == hd &&
           (hd % 32 == 0 || (32 % hd == 0 && hd % 4 == 0)) && mm->n_inputs >= 2 && mm->inputs[0] == nd->output && is_f32(mm) && gemm_step(mm, &ms) &&
           ms.i[14] && ms.i[3] == 1 && ms.i[0] == (long long)B * S && ms.i[2] == (long long)H * hd &&
-          lbr_aligned(nd->inputs[0], 16)))
-        return false;
+          lbr_aligned(nd->inputs[0], 16) && gemm_dma_heads_launcher((int)ms.i[14] - 1, ms.i[6] != 0)))
+        return false;   // (the 64-wide-K-step tiles have no head-layout form)
     std::vector<Rng> reads;
     gemm_input_rngs(mm, ms, &reads);
     reads[0] = rng(nd->inputs[0], (long long)B * H * S * hd * 4);   // A is read as O
@@ -1410,6 +1410,10 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
         }
         s->in[0] = f.src;
         s->run = gemm_dma_heads_launcher((int)s->i[14] - 1, s->i[6] != 0);
+        if (!s->run) {
+            lbr_set_error("fusion: GEMM node %d's tile has no head-layout form", f.first + 1);
+            return LBR_ERR_INVALID;
+        }
         s->i[35] = f.Hs[0];
         s->i[36] = f.S;
         s->i[37] = f.hd;

@@ -404,7 +404,9 @@ __global__ __launch_bounds__(NT, 2) void gemm_mfma_f32(GemmArgs g) {
 
 // ---------------------------------------------------------------- DMA GEMM (trans_b)
 // C = A · Bᵀ with A [M, K] and B [N, K] both K-contiguous, K a multiple of
-// DBK: the 16-byte direct-to-LDS form of buffer loads streams each K step
+// the tile's K step (DBK = 32 floats; a few tiles take 64, see KB below, with
+// 16 chunks a row, swizzled by r & 15, and 4 rows a DMA instruction): the
+// 16-byte direct-to-LDS form of buffer loads streams each K step
 // of the A and B tiles into LDS without passing through registers, into a
 // second LDS stage while the first is consumed (one barrier per K step).
 //
@@ -466,17 +468,23 @@ constexpr int waitcnt_vm(int n) { return lbr_waitcnt_vm(n); }
 // NS: LDS stages of the K pipeline.  Step kt+NS−1 is in flight while step kt
 // is consumed, so a grid that leaves one or two workgroups on a CU (nothing
 // else to hide a load round trip) can take more stages.
-template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS, bool AHEADS, int NORM = 0, int NS = 2>
+// KB: the K step, 32 (DBK) or 64 floats: a row of a stage is KB/4 chunks of 16
+// bytes, chunk c of row r stored at c ^ (r mod KB/4), and one DMA instruction
+// fills 64/(KB/4) rows.  A 64-wide step halves the barriers and waits per K.
+template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS, bool AHEADS, int NORM = 0, int NS = 2,
+          int KB = DBK>
 __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) {
     constexpr int NW = WGM * WGN;
-    constexpr int CH = DBK / 4;                 // 16-byte chunks per tile row
+    constexpr int CH = KB / 4;                  // 16-byte chunks per tile row
     constexpr int RPI = 64 / CH;                // tile rows per DMA instruction
     constexpr int FM = TM / WGM / 16, FN = TN / WGN / 16;
     constexpr int IA = TM / NW / RPI, IB = TN / NW / RPI;
     static_assert(IA * NW * RPI == TM && IB * NW * RPI == TN, "tile rows must split evenly over the waves");
-    static_assert(CH == 8 && FM * 16 * WGM == TM && FN * 16 * WGN == TN, "tile shape");
-    constexpr int GOFF = (TM + TN) * DBK;       // γ, then β, of the step (norm prologue)
-    constexpr int STAGE = GOFF + (NORM ? 2 * DBK : 0);
+    static_assert((CH == 8 || CH == 16) && FM * 16 * WGM == TM && FN * 16 * WGN == TN, "tile shape");
+    static_assert((TM / NW) % 8 == 0 && (TN / NW) % 8 == 0, "each wave's DMA rows start at a multiple of 8");
+    static_assert(!AHEADS || KB == DBK, "A in head layout takes the 32-wide K step");
+    constexpr int GOFF = (TM + TN) * KB;        // γ, then β, of the step (norm prologue)
+    constexpr int STAGE = GOFF + (NORM ? 2 * KB : 0);
     constexpr int NCC = CH / 4;                 // 16-wide K chunks per step
     static_assert(NS >= 2, "pipeline stages");
     // DMA instructions per wave per step: the A and B rows, plus the norm's γ
@@ -495,12 +503,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
 
-    // DMA sources: row clamped to the matrix (rows past the edge are never stored)
+    // DMA sources: row clamped to the matrix (rows past the edge are never stored);
+    // lane (dr, dp) lands at position dp of row `row` and fetches its logical chunk
+    // dp ^ (row mod CH)
     const int dr = lane / CH, dp = lane % CH;
     unsigned offA[IA], offB[IB];
 #pragma unroll
     for (int t = 0; t < IA; ++t) {
         const int row = wave * (TM / NW) + t * RPI + dr;
+        const int sw = dp ^ (row & (CH - 1));
         const int m = min(m0 + row, M - 1);
         if (AHEADS) {
             // head layout: row m = (b, s) starts at ((b·aH)·aS + s)·ahd.  The lane's 4 columns
@@ -508,15 +519,16 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
             // is a multiple of 32; 0 or 1 for ahd = 16) at offset c % ahd; the step's first head
             // goes in the scalar offset (soffA below)
             const int b = m / g.aS, s = m - b * g.aS;
-            const int c = (dp ^ dr) * 4;
+            const int c = sw * 4;
             offA[t] = (unsigned)(((b * g.aH) * g.aS + s) * g.ahd + (c / g.ahd) * g.aS * g.ahd + c % g.ahd) * 4u;
         } else {
-            offA[t] = (unsigned)(m * K + ((dp ^ dr) * 4)) * 4u;
+            offA[t] = (unsigned)(m * K + sw * 4) * 4u;
         }
     }
 #pragma unroll
     for (int t = 0; t < IB; ++t) {
         const int row = wave * (TN / NW) + t * RPI + dr;
+        const int sw = dp ^ (row & (CH - 1));
         int brow = min(n0 + row, N - 1);
         if (g.gF) {
             // gated pair: tile column blocks of 16 alternate gate, up for the same
@@ -525,7 +537,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
             const int o = min(tn * (TN / 2) + (jb >> 1) * 16 + (row & 15), g.gF - 1);
             brow = (jb & 1) ? (g.gbase ? 0 : g.gF) + o : g.gbase + o;
         }
-        offB[t] = (unsigned)(brow * K + ((dp ^ dr) * 4)) * 4u;
+        offB[t] = (unsigned)(brow * K + sw * 4) * 4u;
     }
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(g.A + bz * g.sA), (short)0, M * K * 4, 0x00020000);
@@ -537,20 +549,21 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
         if (NORM == 2) rbe = __builtin_amdgcn_make_buffer_rsrc((void*)g.nb, (short)0, K * 4, 0x00020000);
     }
     auto issue = [&](int k0, float* st) {
-        float* la = st + wave * (TM / NW) * DBK;
-        float* lb = st + TM * DBK + wave * (TN / NW) * DBK;
+        float* la = st + wave * (TM / NW) * KB;
+        float* lb = st + TM * KB + wave * (TN / NW) * KB;
         // K step k0 of A: column k0 (row-major), or head k0 / ahd at offset k0 % ahd (head
         // layout; ahd is a multiple of the step, or divides it so the step starts a head)
         const unsigned soffA =
             AHEADS ? (unsigned)((k0 / g.ahd) * g.aS * g.ahd + k0 % g.ahd) * 4u : (unsigned)k0 * 4u;
 #pragma unroll
-        for (int t = 0; t < IA; ++t) dma16(ra, la + t * RPI * DBK, offA[t], soffA);
+        for (int t = 0; t < IA; ++t) dma16(ra, la + t * RPI * KB, offA[t], soffA);
 #pragma unroll
-        for (int t = 0; t < IB; ++t) dma16(rb, lb + t * RPI * DBK, offB[t], (unsigned)k0 * 4u);
-        if (NORM && wave == 0) {   // the step's 32 γ (lanes 0-7) and β (lanes 8-15), 16 bytes a lane
-            if (lane < 8) dma16(rg, st + GOFF, (unsigned)lane * 16u, (unsigned)k0 * 4u);
-            if (NORM == 2 && lane >= 8 && lane < 16)
-                dma16(rbe, st + GOFF + DBK - 32, (unsigned)(lane - 8) * 16u, (unsigned)k0 * 4u);
+        for (int t = 0; t < IB; ++t) dma16(rb, lb + t * RPI * KB, offB[t], (unsigned)k0 * 4u);
+        if (NORM && wave == 0) {   // the step's KB γ (lanes 0 .. CH−1) and β (lanes CH .. 2CH−1, landing
+                                   // KB floats after γ), 16 bytes a lane
+            if (lane < CH) dma16(rg, st + GOFF, (unsigned)lane * 16u, (unsigned)k0 * 4u);
+            if (NORM == 2 && lane >= CH && lane < 2 * CH)
+                dma16(rbe, st + GOFF, (unsigned)(lane - CH) * 16u, (unsigned)k0 * 4u);
         }
     };
 
@@ -565,9 +578,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
     int rdA[NCC], rdB[NCC];
 #pragma unroll
     for (int cc = 0; cc < NCC; ++cc) {
-        const int o = fi * DBK + (((cc * 4 + kq) ^ (fi & 7)) * 4);
-        rdA[cc] = wm * (TM / WGM) * DBK + o;
-        rdB[cc] = TM * DBK + wn * (TN / WGN) * DBK + o;
+        const int o = fi * KB + (((cc * 4 + kq) ^ (fi & (CH - 1))) * 4);
+        rdA[cc] = wm * (TM / WGM) * KB + o;
+        rdB[cc] = TM * KB + wn * (TN / WGN) * KB + o;
     }
     floatx4 fa[2][FM], fb[2][FN];
     // norm prologue state: per fragment row (lane row fi of block i) the shift
@@ -579,9 +592,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
     for (int j = 0; j < FN; ++j) nu[j] = nv[j] = 0.f;
     auto frags = [&](const float* st, int cc, floatx4* a, floatx4* b) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const floatx4*>(st + rdA[cc] + i * 16 * DBK);
+        for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const floatx4*>(st + rdA[cc] + i * 16 * KB);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const floatx4*>(st + rdB[cc] + j * 16 * DBK);
+        for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const floatx4*>(st + rdB[cc] + j * 16 * KB);
         if (NORM) {   // k = step start + 16·cc + 4·kq + q for every fragment of the lane
             const floatx4 w = *reinterpret_cast<const floatx4*>(st + GOFF + cc * 16 + (lane >> 4) * 4);
             if (NORM == 1) {
@@ -591,7 +604,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
                     a[i] = a[i] * w;
                 }
             } else {
-                const floatx4 be = *reinterpret_cast<const floatx4*>(st + GOFF + DBK + cc * 16 + (lane >> 4) * 4);
+                const floatx4 be = *reinterpret_cast<const floatx4*>(st + GOFF + KB + cc * 16 + (lane >> 4) * 4);
 #pragma unroll
                 for (int i = 0; i < FM; ++i) {
                     const floatx4 d = a[i] - nc[i];
@@ -617,10 +630,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][q], b[j][q], acc[i][j], 0, 0, 0);
     };
 
-    // K range of this workgroup (split ks of ksplit; kchunk is a multiple of DBK)
+    // K range of this workgroup (split ks of ksplit; kchunk is a multiple of KB)
     const int ks = blockIdx.y;
     const int kbeg = ks * g.kchunk;
-    const int nk = (min(K, kbeg + g.kchunk) - kbeg) / DBK;
+    const int nk = (min(K, kbeg + g.kchunk) - kbeg) / KB;
     if (nk > 0) {
         // NS stages: steps 0 .. NS−1 issued up front; at the end of step kt, step
         // kt+1 must have landed while kt+2 .. kt+NS−1 may still be in flight, then
@@ -635,7 +648,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
                 nc[i] = g.A[(long long)min(m0 + wm * (TM / WGM) + i * 16 + fi, M - 1) * K];
         }
 #pragma unroll
-        for (int st = 0; st < NS; ++st) issue(kbeg + min(st, nk - 1) * DBK, lds + st * STAGE);
+        for (int st = 0; st < NS; ++st) issue(kbeg + min(st, nk - 1) * KB, lds + st * STAGE);
         if (wave == 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 1) * PER_STEP0));   // step 0 landed
         else __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 1) * PER_STEP));
         __syncthreads();
@@ -653,7 +666,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_f32(GemmArgs g) 
                     if (wave == 0) __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * PER_STEP0));
                     else __builtin_amdgcn_s_waitcnt(waitcnt_vm((NS - 2) * PER_STEP));
                     __syncthreads();   // ... and every wave's; stage cur fully read
-                    issue(kbeg + min(kt + NS, nk - 1) * DBK, lds + cur);
+                    issue(kbeg + min(kt + NS, nk - 1) * KB, lds + cur);
                     frags(lds + nxt, 0, fa[0], fb[0]);
                 }
                 mma(fa[cc & 1], fb[cc & 1]);
@@ -1172,7 +1185,8 @@ void launch_gemm_t(const Step& s, hipStream_t st) {
     if (g.ksplit > 1) launch_splitk_reduce<HAS_BIAS>(s, g, st);
 }
 
-template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS, bool AHEADS, int NORM = 0, int NS = 2>
+template <int TM, int TN, int WGM, int WGN, int OCC, bool HAS_BIAS, bool AHEADS, int NORM = 0, int NS = 2,
+          int KB = DBK>
 void launch_gemm_dma(const Step& s, hipStream_t st) {
     GemmArgs g = make_args(s);
     if (g.M <= 0 || g.N <= 0) return;
@@ -1180,15 +1194,15 @@ void launch_gemm_dma(const Step& s, hipStream_t st) {
     // a gated pair's tile covers TN/2 output columns (TN/2 gate + TN/2 up columns of C)
     g.tiles_n = g.gF ? (g.gF + TN / 2 - 1) / (TN / 2) : (g.N + TN - 1) / TN;
     dim3 grid(g.tiles_m * g.tiles_n, g.ksplit, (unsigned)s.i[3]);
-    hipLaunchKernelGGL((gemm_dma_f32<TM, TN, WGM, WGN, OCC, HAS_BIAS, AHEADS, NORM, NS>), grid, dim3(64 * WGM * WGN), 0,
-                       st, g);
+    hipLaunchKernelGGL((gemm_dma_f32<TM, TN, WGM, WGN, OCC, HAS_BIAS, AHEADS, NORM, NS, KB>), grid,
+                       dim3(64 * WGM * WGN), 0, st, g);
     if (g.ksplit > 1) launch_splitk_reduce<HAS_BIAS>(s, g, st);
 }
 
 // Tile shapes of the DMA GEMM: (TM, TN), workgroups resident per CU (LDS
 // and registers), and measured steady-state fraction of the fp32 MFMA peak.
 struct DmaTile {
-    int tm, tn, occ, waves;
+    int tm, tn, occ, waves, kb;   // kb: K step (32 or 64 floats)
     double eff;
     const char* name;
     bool model;    // chosen by choose_dma's model; the others only by measurement
@@ -1196,29 +1210,35 @@ struct DmaTile {
     bool pairs;    // an even number of 16-column blocks per wavefront (gated pairs)
 };
 constexpr DmaTile kDmaTiles[] = {
-    {256, 256, 1, 8, 0.94, "256x256", true, true},   // 8 wavefronts (4×2), 128 KB LDS
-    {128, 128, 2, 4, 0.92, "128x128", true, true},   // 4 wavefronts (2×2), 64 KB LDS
-    {128, 64, 3, 4, 0.9225, "128x64", true, true},   // 4 wavefronts (2×2), 48 KB LDS
-    {64, 128, 3, 4, 0.9225, "64x128", true, true},
-    {64, 64, 4, 4, 0.90, "64x64", true, true},       // 4 wavefronts (2×2) of 32×32, 32 KB LDS
+    {256, 256, 1, 8, 32, 0.94, "256x256", true, true},   // 8 wavefronts (4×2), 128 KB LDS
+    {128, 128, 2, 4, 32, 0.92, "128x128", true, true},   // 4 wavefronts (2×2), 64 KB LDS
+    {128, 64, 3, 4, 32, 0.9225, "128x64", true, true},   // 4 wavefronts (2×2), 48 KB LDS
+    {64, 128, 3, 4, 32, 0.9225, "64x128", true, true},
+    {64, 64, 4, 4, 32, 0.90, "64x64", true, true},       // 4 wavefronts (2×2) of 32×32, 32 KB LDS
     // Small-grid tiles.  The model cannot rank them against 64×64 (its error on
     // GPT-2-width GEMMs, ~18%, exceeds their differences, 5–20%): a 32×48 grid
     // wins where 64×64 leaves a fractional last round (1024×2304×768: 40.6 µs
     // with 4 stages vs 43.8; 512×2304×768: 24.9 vs 31.0; 512×3072×768: 26.8 vs
     // 31.3) and loses where it leaves two 2-wavefront workgroups per CU
     // (1024×768×768: 24.8 vs 20.0), so they are picked by timing.
-    {32, 48, 8, 2, 0.80, "32x48", false, false},     // 2 wavefronts (2×1) of 16×48, 20 KB LDS
-    {32, 48, 5, 2, 0.80, "32x48s4", false, false},   // the same with 4 LDS stages, 40 KB
-    {64, 96, 4, 4, 0.85, "64x96", false, true},      // 4 wavefronts (4×1) of 16×96, 40 KB LDS
+    {32, 48, 8, 2, 32, 0.80, "32x48", false, false},     // 2 wavefronts (2×1) of 16×48, 20 KB LDS
+    {32, 48, 5, 2, 32, 0.80, "32x48s4", false, false},   // the same with 4 LDS stages, 40 KB
+    {64, 96, 4, 4, 32, 0.85, "64x96", false, true},      // 4 wavefronts (4×1) of 16×96, 40 KB LDS
     // Narrow 4-wavefront tiles for GEMMs of 512-1024 rows and K = 768-3072 (MI355X,
     // GEMM steps of the GPT-2-shaped workloads): one or two rounds of small
     // workgroups, each wavefront with few MFMA blocks, beat the 2-wavefront 32×48 and
     // the 64×64 tiles there by 5-20% (e.g. 1024×2304×768: 35.0 µs for 32×96 against
     // 43.3 for 32×48s4).
-    {32, 160, 3, 4, 0.85, "32x160", false, false},   // 4 wavefronts (2×2) of 16×80, 48 KB LDS
-    {64, 32, 6, 4, 0.80, "64x32", false, false},     // 4 wavefronts (2×2) of 32×16, 24 KB LDS
-    {32, 64, 6, 4, 0.80, "32x64", false, true},      // 4 wavefronts (2×2) of 16×32, 24 KB LDS
-    {32, 96, 5, 4, 0.80, "32x96", false, false},     // 4 wavefronts (2×2) of 16×48, 32 KB LDS
+    {32, 160, 3, 4, 32, 0.85, "32x160", false, false},   // 4 wavefronts (2×2) of 16×80, 48 KB LDS
+    {64, 32, 6, 4, 32, 0.80, "64x32", false, false},     // 4 wavefronts (2×2) of 32×16, 24 KB LDS
+    {32, 64, 6, 4, 32, 0.80, "32x64", false, true},      // 4 wavefronts (2×2) of 16×32, 24 KB LDS
+    {32, 96, 5, 4, 32, 0.80, "32x96", false, false},     // 4 wavefronts (2×2) of 16×48, 32 KB LDS
+    // 64-wide K steps (K a multiple of 64; not with A in head layout), for the
+    // timing at plan creation: on the GPT-2-shaped GEMMs they run within ±4% of the
+    // same tiles with 32-wide steps (1024×768×3072 unsplit: 47.7 µs for 32×96k64
+    // against 51.5), so halving the barriers per K is not what those GEMMs lack
+    {32, 96, 2, 4, 64, 0.80, "32x96k64", false, false},     // 64 KB LDS
+    {64, 64, 2, 4, 64, 0.90, "64x64k64", false, true},      // 64 KB LDS
 };
 constexpr int kNumDmaTiles = sizeof(kDmaTiles) / sizeof(kDmaTiles[0]);
 
@@ -1244,9 +1264,10 @@ void choose_dma(long long M, long long N, int K, long long batches, int cus, int
     for (int t = 0; t < kNumDmaTiles; ++t) {
         const DmaTile& d = kDmaTiles[t];
         if (force_tile ? strcmp(force_tile, d.name) != 0 : !d.model) continue;
+        if (K % d.kb) continue;
         const long long tiles = ((M + d.tm - 1) / d.tm) * ((N + d.tn - 1) / d.tn) * batches;
         for (int s = 1; s <= 16; ++s) {
-            const int chunk = ((K + s - 1) / s + DBK - 1) / DBK * DBK;
+            const int chunk = ((K + s - 1) / s + d.kb - 1) / d.kb * d.kb;
             const int s_eff = (K + chunk - 1) / chunk;
             if (force_ks) {
                 if (s != atoi(force_ks) || s_eff != s) continue;
@@ -1287,6 +1308,9 @@ step_fn dma_launcher(int tile) {
         case 9: return launch_gemm_dma<64, 32, 2, 2, 4, HAS_BIAS, AHEADS, NORM>;
         case 10: return launch_gemm_dma<32, 64, 2, 2, 4, HAS_BIAS, AHEADS, NORM>;
         case 11: return launch_gemm_dma<32, 96, 2, 2, 4, HAS_BIAS, AHEADS, NORM>;
+        // 64-wide K steps: no A-in-head-layout form
+        case 12: if constexpr (AHEADS) return nullptr; else return launch_gemm_dma<32, 96, 2, 2, 2, HAS_BIAS, AHEADS, NORM, 2, 64>;
+        case 13: if constexpr (AHEADS) return nullptr; else return launch_gemm_dma<64, 64, 2, 2, 2, HAS_BIAS, AHEADS, NORM, 2, 64>;
         default: return launch_gemm_dma<64, 64, 2, 2, 4, HAS_BIAS, AHEADS, NORM>;
     }
 }
@@ -1387,13 +1411,14 @@ static step_fn dma_family_launcher(const Step& s, int tile) {
 }
 
 // Two K ranges for an unsplit one-batch DMA GEMM step (K ≥ 512, ranges a
-// multiple of the 32-wide K step): its reduce kernel can then take a norm of
+// multiple of its tile's K step): its reduce kernel can then take a norm of
 // its output.  False leaves the step unchanged.
 bool gemm_dma_split2(Step* s) {
     const long long M = s->i[0], N = s->i[1], K = s->i[2];
     if (!s->i[14] || s->i[10] > 1 || s->i[3] != 1 || K < 512 || s->i[19] || s->i[32] || s->i[15] || s->i[18])
         return false;
-    const long long chunk = (K / 2 + DBK - 1) / DBK * DBK;
+    const int kb = kDmaTiles[s->i[14] - 1].kb;
+    const long long chunk = (K / 2 + kb - 1) / kb * kb;
     if ((K + chunk - 1) / chunk != 2) return false;
     s->i[10] = 2;
     s->i[11] = chunk;
@@ -1402,7 +1427,7 @@ bool gemm_dma_split2(Step* s) {
 }
 
 // Sets the number of K ranges of a one-batch DMA GEMM step to ks (ranges of
-// whole 32-wide K steps; the split-K reduce then carries the step's bias,
+// whole K steps of its tile; the split-K reduce then carries the step's bias,
 // activation, residual or head scatter).  False, leaving the step unchanged,
 // for epilogues the reduce does not carry (gated pair, head prologue, norm
 // prologue), for a reduce that already normalises, or when K does not split
@@ -1416,7 +1441,8 @@ bool gemm_dma_set_ksplit(Step* s, int ks) {
         s->ws_bytes = 0;
         return true;
     }
-    const long long chunk = ((K + ks - 1) / ks + DBK - 1) / DBK * DBK;
+    const int kb = kDmaTiles[s->i[14] - 1].kb;
+    const long long chunk = ((K + ks - 1) / ks + kb - 1) / kb * kb;
     if ((K + chunk - 1) / chunk != ks) return false;
     s->i[10] = ks;
     s->i[11] = chunk;
@@ -1444,11 +1470,12 @@ int gemm_dma_tune_candidates(const Step& s, int* tiles, int cap) {
     if (!s.i[14] || s.i[10] > 1 || s.i[3] != 1) return 0;   // one batch, no K split
     // tiles the model prices at more than twice its best are not timed (the
     // 256×256 tile on a 1024-row GEMM, say): only near-ties need measuring
+    auto usable = [&](int t) { return dma_family_launcher(s, t) && s.i[2] % kDmaTiles[t].kb == 0; };
     double best = 1e30;
     for (int t = 0; t < kNumDmaTiles; ++t)
-        if (dma_family_launcher(s, t)) best = std::min(best, dma_model_time(s.i[0], s.i[1], (int)s.i[2], lbr_device_cus(), t));
+        if (usable(t)) best = std::min(best, dma_model_time(s.i[0], s.i[1], (int)s.i[2], lbr_device_cus(), t));
     for (int t = 0; t < kNumDmaTiles && n < cap; ++t)
-        if (dma_family_launcher(s, t) && dma_model_time(s.i[0], s.i[1], (int)s.i[2], lbr_device_cus(), t) <= 2.0 * best)
+        if (usable(t) && dma_model_time(s.i[0], s.i[1], (int)s.i[2], lbr_device_cus(), t) <= 2.0 * best)
             tiles[n++] = t;
     return n;
 }
@@ -1465,7 +1492,8 @@ int gemm_dma_tile_by_name(const char* name) {
 
 bool gemm_dma_retile(Step* s, int tile) {
     const step_fn run = dma_family_launcher(*s, tile);
-    if (!run) return false;
+    // the K ranges must stay whole steps of the new tile
+    if (!run || s->i[2] % kDmaTiles[tile].kb || s->i[11] % kDmaTiles[tile].kb) return false;
     s->run = run;
     s->i[14] = tile + 1;
     return true;

@@ -522,6 +522,15 @@ def test_transpose_gemm_refusals():
     assert all(k != "transpose_gemm" for _, _, k in _windows(_tgemm(0, 1 * MB, 2 * MB, 3 * MB, later=[reader])))
 
 
+def test_transpose_gemm_needs_a_head_layout_tile(monkeypatch):
+    """The 64-wide-K-step tiles have no head-layout form: a GEMM forced onto one keeps
+    its TRANSPOSE as a node of its own (instead of a fused step with no kernel)."""
+    monkeypatch.setenv("LBR_GEMM_TILE", "32x96k64")
+    assert _windows(_tgemm(0, 1 * MB, 2 * MB, 3 * MB)) == [(1, 2, "gemm_resid")]   # GEMM + ADD only
+    monkeypatch.setenv("LBR_GEMM_TILE", "32x96")
+    assert _windows(_tgemm(0, 1 * MB, 2 * MB, 3 * MB)) == [(0, 3, "transpose_gemm")]
+
+
 # ------------------------------------------------------------ index arithmetic
 
 def test_fast_divisor_matches_integer_division():

@@ -83,7 +83,8 @@ ACTS = {OpType.RELU: lambda v: np.maximum(v, 0.0), OpType.GELU: cf_gelu_tanh, Op
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("tile,ks,M,N,K", [(None, None, 300, 520, 96), ("256x256", "1", 300, 520, 96),
                                            ("64x128", "1", 70, 130, 64), ("128x128", "3", 200, 300, 3072),
-                                           ("32x64", "1", 70, 130, 64), ("32x96", "2", 200, 300, 768)])
+                                           ("32x64", "1", 70, 130, 64), ("32x96", "2", 200, 300, 768),
+                                           ("32x96k64", "1", 70, 130, 128), ("64x64k64", "2", 200, 300, 768)])
 def test_gemm_activation_epilogue(monkeypatch, op, bias, tile, ks, M, N, K):
     if tile:
         monkeypatch.setenv("LBR_GEMM_TILE", tile)
@@ -97,7 +98,8 @@ def test_gemm_activation_epilogue(monkeypatch, op, bias, tile, ks, M, N, K):
     _check(g, {"a": a}, ACTS[op](c), "gemm_act")
 
 
-@pytest.mark.parametrize("tile", [None, "256x256", "128x128", "128x64", "64x128", "64x64", "64x96", "32x64"])
+@pytest.mark.parametrize("tile", [None, "256x256", "128x128", "128x64", "64x128", "64x64", "64x96", "32x64",
+                                  "64x64k64"])
 @pytest.mark.parametrize("act,gbias,order,mm_bias", [("silu", False, 0, False), ("gelu", True, 1, True),
                                                       ("silu", True, 0, True), ("gelu", False, 1, False)])
 def test_gemm_gated_epilogue(monkeypatch, tile, act, gbias, order, mm_bias):
@@ -106,7 +108,7 @@ def test_gemm_gated_epilogue(monkeypatch, tile, act, gbias, order, mm_bias):
     if tile:
         monkeypatch.setenv("LBR_GEMM_TILE", tile)
         monkeypatch.setenv("LBR_GEMM_KSPLIT", "1")
-    M, F, K = 300, 200, 96
+    M, F, K = 300, 200, 128   # K: two steps of the 64-wide-step tiles, four of the others
     r = rng(M + F + K + order)
     g = Graph()
     a, c = _gemm_graph(g, r, M, 2 * F, K, mm_bias)

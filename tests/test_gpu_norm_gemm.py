@@ -87,7 +87,7 @@ def _graph(r, norm, M, N, K, bias, act, offset):
 @pytest.mark.parametrize("norm", ["layer", "rms"])
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("tile", [None, "128x128", "128x64", "64x128", "64x64", "32x48", "32x48s4", "64x96",
-                                  "32x160", "64x32", "32x64", "32x96"])
+                                  "32x160", "64x32", "32x64", "32x96", "32x96k64", "64x64k64"])
 @pytest.mark.parametrize("M,N,K", [(300, 520, 96), (32, 192, 64), (1000, 300, 768)])
 def test_norm_gemm(monkeypatch, norm, bias, tile, M, N, K):
     monkeypatch.setenv("LBR_NORM_PROLOGUE", "always")   # the default takes small GEMMs only

@@ -63,7 +63,8 @@ def test_gemm(monkeypatch, kernel, M, N, K, trans_b, batches, b2d, with_bias):
 
 DMA_CASES = [
     # (M, N, K, batches, b_is_2d)
-    (300, 520, 96, 1, True),      # ragged M and N edges, 3 K steps
+    (300, 520, 96, 1, True),      # ragged M and N edges, 3 K steps (a 64-wide-step tile falls back)
+    (200, 330, 192, 1, True),     # 3 steps of 64
     (513, 257, 64, 1, True),
     (64, 64, 32, 1, True),        # a single K step
     (96, 200, 160, 3, False),     # batched, B [batches, N, K]
@@ -71,7 +72,8 @@ DMA_CASES = [
 
 
 @pytest.mark.parametrize("tile", ["256x256", "128x128", "128x64", "64x128", "64x64",
-                                  "32x48", "32x48s4", "64x96", "32x160", "64x32", "32x64", "32x96"])
+                                  "32x48", "32x48s4", "64x96", "32x160", "64x32", "32x64", "32x96",
+                                  "32x96k64", "64x64k64"])
 @pytest.mark.parametrize("M,N,K,batches,b2d", DMA_CASES)
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_gemm_dma_tiles(monkeypatch, tile, M, N, K, batches, b2d, with_bias):
@@ -84,7 +86,8 @@ def test_gemm_dma_tiles(monkeypatch, tile, M, N, K, batches, b2d, with_bias):
                                                    ("64x128", 2, 130, 260, 64, 1), ("64x64", 3, 100, 70, 960, 1),
                                                    ("32x48s4", 3, 100, 130, 960, 1), ("64x96", 2, 70, 200, 512, 2),
                                                    ("32x96", 2, 100, 130, 960, 1), ("64x32", 3, 70, 200, 512, 2),
-                                                   ("32x160", 2, 130, 260, 640, 1), ("32x64", 4, 100, 70, 1024, 1)])
+                                                   ("32x160", 2, 130, 260, 640, 1), ("32x64", 4, 100, 70, 1024, 1),
+                                                   ("32x96k64", 3, 100, 130, 960, 1), ("64x64k64", 2, 70, 200, 512, 2)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_gemm_dma_ksplit(monkeypatch, tile, ks, M, N, K, batches, with_bias):
     monkeypatch.setenv("LBR_GEMM_TILE", tile)
