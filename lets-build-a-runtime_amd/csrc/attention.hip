@@ -1439,7 +1439,12 @@ int decode_attention(const OpNode* n, Step* s) {
             for (int q = 0; q < nq; ++q) head_tiles += attn16_block_tiles(seq, causal != 0, q);
             const long long total = head_tiles * bh;
             long long wg = 0;
-            if (!s->i[6] && nq * bh < 2LL * cus) {
+            // The key-range split described above, except when the heaviest block holds at
+            // most 4 key tiles (S <= 128): the merge launch then costs more than the shorter
+            // chain saves (one attention node,
+            // back-to-back replays: H4 S128 hd 48 21.7 us split against 18.4 us whole, hd 16
+            // 18.5 against 16.1; H8 S256 hd 48 22.1 against 27.8, H4 S512 23.0 against 46.8)
+            if (!s->i[6] && nq * bh < 2LL * cus && attn16_block_tiles(seq, causal != 0, (int)nq - 1) > 4) {
                 const int min_share = hd <= 64 ? 4 : 8;
                 const long long rounds = std::min(2LL, total / ((long long)min_share * cus));
                 // too few tiles for a whole round: shares of 2 tiles (hd <= 64), which

@@ -332,6 +332,15 @@ def test_attention_transpose_output_over_v(monkeypatch):
     assert _windows(_attn_transpose(26 * MB)) == [(0, 2, "attn_transpose")]
 
 
+def test_tiny_attention_grid_takes_no_split():
+    # head dim 48 (no key-quartered form): 4 heads × S 128 hold 4 key tiles a block, too few
+    # for the key-range split to pay for its merge launch, so there is no deferred store and
+    # an output over V is refused; at S 256 (8 tiles a block) the split, and the fusion, return
+    assert _windows(_attn_transpose(20 * MB, hd=48)) == []
+    assert _windows(_attn_transpose(26 * MB, hd=48)) == [(0, 2, "attn_transpose")]
+    assert _windows(_attn_transpose(20 * MB, S=256, hd=48)) == [(0, 2, "attn_transpose")]
+
+
 def test_attention_transpose_refuses_output_over_v_on_a_full_grid():
     # 32 heads × S 4096 × hd 128 fill the CUs with folded query blocks: no split, no deferred
     # store, so an output over V is refused while one elsewhere fuses

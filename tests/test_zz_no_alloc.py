@@ -7,8 +7,9 @@ both forced here: every GEMM runs in 2 K ranges whose partial sums go to
 the workspace, and the attention takes the key-range split with shares of
 4 key tiles, so most query blocks are cut into segments whose partials go
 to the workspace.  The second call runs the same body at
-S=512.  A node array whose workspace need exceeds the scratch array is
-rejected before any launch.
+S=512.  Every benchmark workload's one-kernel-per-node array fits the scratch
+array and runs through it.  A node array whose workspace need exceeds the
+scratch array is rejected before any launch.
 """
 
 import ctypes
@@ -63,6 +64,37 @@ def test_noalloc_matches_execute_twice(hip_lib, monkeypatch):
         print(f"gpt2 body S={seq}: noalloc == execute bitwise: {np.array_equal(y, y_exec)}; vs oracle rel {e:.2e}")
         np.testing.assert_array_equal(y, y_exec)
         assert np.isfinite(y).all() and e <= 1e-3
+
+
+@pytest.mark.parametrize("key", ["toy", "gpt2w", "gpt2", "gpt2_lm", "7b4k", "qwen3_4b", "qwen3_4b_lm"])
+def test_noalloc_takes_every_workload(hip_lib, key):
+    """The scratch array holds the workspace of every benchmark workload's one-kernel-per-node
+    array at its benchmark size (the largest, the Qwen3-4B body's split attention, needs 66
+    MiB): lbr_execute_noalloc runs it and matches lbr_execute bit for bit."""
+    from runtime.executor.compiled import CompiledExecutor
+    from runtime.planner import plan
+    from workloads import export_workload
+    from runtime.passes import run_pipeline
+    lib = hip_lib
+    _, x, graph = export_workload(key)
+    run_pipeline(graph, None)
+    ex = CompiledExecutor(fuse=False)
+    ex.compile(plan(graph))
+    try:
+        n = len(ex.dispatch_order)
+        name_in, name_out = graph.inputs[0], graph.outputs[0]
+        ex.upload_inputs({name_in: x})
+        lib.check(lib.lbr_execute(ex._nodes, n), "lbr_execute")
+        y_exec = ex.download_outputs()[name_out]
+        out_ptr = ctypes.c_void_p(ex.device_address(name_out))
+        lib.check(lib.lbr_memset(out_ptr, 0, y_exec.nbytes), "lbr_memset")
+        ex.upload_inputs({name_in: x})
+        lib.check(lib.lbr_execute_noalloc(ex._nodes, n), "lbr_execute_noalloc")
+        y = ex.download_outputs()[name_out]
+    finally:
+        ex.close()
+    print(f"{key}: noalloc == execute bitwise: {np.array_equal(y, y_exec)}")
+    np.testing.assert_array_equal(y, y_exec)
 
 
 def test_noalloc_rejects_oversized_workspace(hip_lib, monkeypatch):
