@@ -442,7 +442,8 @@ struct TunedTile {
 static const TunedTile kTunedTiles[] = {
     // GPT-2-width block (512 rows; µs for the listed tile against the model's)
     {"gemm_dma_f32_nt+heads", 512, 2304, 768, "32x160", 0},      // QKV: 24.6 against 26.6 (32x48)
-    {"gemm_dma_f32_nt+tin+resid", 512, 768, 768, "32x64", 1},    // O proj: 12.2 against 14.1 (64x64, 2 ranges)
+    {"gemm_dma_f32_nt+tin+resid+layernorm", 512, 768, 768, "32x96", 0},   // O proj + LN2 (2 ranges): 12.7 against 14.0 (64x64)
+    {"gemm_dma_f32_nt+tin+resid", 512, 768, 768, "32x64", 1},    // O proj, LN apart: 12.2 against 14.1 (64x64, 2 ranges)
     {"gemm_dma_f32_nt+act", 512, 3072, 768, "32x64", 0},         // FFN1: 25.6 against 27.5 (32x48)
     {"gemm_dma_f32_nt+resid", 512, 768, 3072, "32x96", 2},       // FFN2: 28.2 against 30.4 (64x64, 8 ranges)
     // GPT-2 body and LM (1024 rows)
@@ -453,12 +454,12 @@ static const TunedTile kTunedTiles[] = {
 
 // The tiles (and K ranges) of kTunedTiles, before the plan's workspace is
 // sized; marks the steps it set.  Skipped under LBR_GEMM_AUTOTUNE=0 or 2 and
-// under a tile forced by LBR_GEMM_TILE.
+// under a tile or K split forced by LBR_GEMM_TILE / LBR_GEMM_KSPLIT.
 static void table_tiles(std::vector<Step>& steps, std::vector<char>* tabled) {
     tabled->assign(steps.size(), 0);
     const char* env = getenv("LBR_GEMM_AUTOTUNE");
     const int mode = env ? atoi(env) : -1;
-    if (mode == 0 || mode == 2 || getenv("LBR_GEMM_TILE")) return;
+    if (mode == 0 || mode == 2 || getenv("LBR_GEMM_TILE") || getenv("LBR_GEMM_KSPLIT")) return;
     for (size_t i = 0; i < steps.size(); ++i) {
         Step& s = steps[i];
         if (!s.name || strncmp(s.name, "gemm_dma_f32", 12) != 0 || !s.i[14] || s.i[3] != 1) continue;

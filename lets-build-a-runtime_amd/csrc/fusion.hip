@@ -1849,7 +1849,10 @@ bool lbr_merge_reduce_norm(Step* g, const Step& n) {
     const char* sp = getenv("LBR_REDUCE_NORM_SPLIT");
     const bool split2 = !(sp && strcmp(sp, "0") == 0) && g->i[10] <= 1 &&
                         2.0 * g->i[0] * g->i[1] * g->i[2] <= 4294967296.0;
-    if (g->fuse_kind != LBR_FUSE_GEMM_RESID || !g->in[3] || (g->i[10] <= 1 && !split2) || g->i[3] != 1 ||
+    // a GEMM + residual ADD, with A row-major or read in head layout (TRANSPOSE_GEMM: the
+    // reduce never reads A)
+    const bool tin = g->fuse_kind == LBR_FUSE_TRANSPOSE_GEMM;
+    if ((g->fuse_kind != LBR_FUSE_GEMM_RESID && !tin) || !g->in[3] || (g->i[10] <= 1 && !split2) || g->i[3] != 1 ||
         !g->i[12] || g->i[19] || g->i[32] || g->i[31] || g->i[16] || g->i[18] || !n.name)
         return false;
     const bool rms = strcmp(n.name, "rmsnorm") == 0;
@@ -1879,8 +1882,10 @@ bool lbr_merge_reduce_norm(Step* g, const Step& n) {
     g->f[2] = n.f[0];
     g->n_nodes += 1;
     const bool dma = g->i[14] != 0;
-    g->name = dma ? (rms ? "gemm_dma_f32_nt+resid+rmsnorm" : "gemm_dma_f32_nt+resid+layernorm")
-                  : (rms ? "gemm_mfma_f32+resid+rmsnorm" : "gemm_mfma_f32+resid+layernorm");
+    if (tin) g->name = rms ? "gemm_dma_f32_nt+tin+resid+rmsnorm" : "gemm_dma_f32_nt+tin+resid+layernorm";
+    else
+        g->name = dma ? (rms ? "gemm_dma_f32_nt+resid+rmsnorm" : "gemm_dma_f32_nt+resid+layernorm")
+                      : (rms ? "gemm_mfma_f32+resid+rmsnorm" : "gemm_mfma_f32+resid+layernorm");
     return true;
 }
 

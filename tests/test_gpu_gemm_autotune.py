@@ -120,8 +120,8 @@ def test_autotune_workload_bitwise(monkeypatch, key, seq):
 
 def test_default_plan_takes_the_table_tiles_every_time():
     """GPT-2-width at S=512: every GEMM step takes the table's tile and K ranges (QKV
-    32x160, O projection 32x64 unsplit, FFN1 32x64, FFN2 32x96 in 2 ranges),
-    identically in every plan creation."""
+    32x160, O projection with LayerNorm 2 in its reduce 32x96 in 2 ranges, FFN1 32x64,
+    FFN2 32x96 in 2 ranges), identically in every plan creation."""
     from runtime.executor.compiled import CompiledExecutor
     from runtime.passes import run_pipeline
     from runtime.planner import plan
@@ -140,5 +140,5 @@ def test_default_plan_takes_the_table_tiles_every_time():
             ex.close()
     assert picks[0] == picks[1] == picks[2], picks
     by_name = {name: (tile, ks) for name, m, n, k, tile, ks in picks[0]}
-    assert by_name == {"gemm_dma_f32_nt+heads": ("32x160", 1), "gemm_dma_f32_nt+tin+resid": ("32x64", 1),
+    assert by_name == {"gemm_dma_f32_nt+heads": ("32x160", 1), "gemm_dma_f32_nt+tin+resid+layernorm": ("32x96", 2),
                        "gemm_dma_f32_nt+act": ("32x64", 1), "gemm_dma_f32_nt+resid": ("32x96", 2)}, picks[0]

@@ -93,6 +93,65 @@ def test_reduce_norm(monkeypatch, norm, bias, M, N, K):
         assert normwise_rel(got, o[name]) <= 1e-4, name
 
 
+def _tin_graph(r, H, S, hd, N, norm):
+    """O [1, H, S, hd] → TRANSPOSE(1, 2) → RESHAPE [1, S, H·hd] → MATMUL_ADD → ADD(x, C) → norm: the
+    GEMM reads O in its head layout (GPT-2-width's attention projection and second LayerNorm)."""
+    K = H * hd
+    o, x = randn(r, 1, H, S, hd), randn(r, 1, S, N)
+    w, b = randn(r, N, K, scale=0.05), randn(r, N)
+    gam = (1.0 + 0.5 * randn(r, N)).astype(np.float32)
+    bet = randn(r, N)
+    g = Graph()
+    for name, arr in (("o", o), ("x", x)):
+        g.add_tensor(name, arr.shape)
+        g.inputs.append(name)
+    for name, arr in (("w", w), ("b", b), ("gam", gam), ("bet", bet)):
+        g.add_tensor(name, arr.shape).buffer = arr
+        g.constants.append(name)
+    g.add_tensor("t", (1, S, H, hd))
+    g.add_node(OpType.TRANSPOSE, ["o"], "t", {"dim0": 1, "dim1": 2})
+    g.add_tensor("a", (1, S, K))
+    g.add_node(OpType.RESHAPE, ["t"], "a", {"shape": (1, S, K)})
+    g.add_tensor("c", (1, S, N))
+    g.add_node(OpType.MATMUL_ADD, ["a", "w", "b"], "c", {"transpose_b": True})
+    g.add_tensor("h", (1, S, N))
+    g.add_node(OpType.ADD, ["x", "c"], "h", {})
+    h = np.swapaxes(o, 1, 2).reshape(1, S, K).astype(np.float64) @ w.T.astype(np.float64) + b + x
+    g.add_tensor("n", (1, S, N))
+    if norm == "rms":
+        g.add_node(OpType.RMSNORM, ["h", "gam"], "n", {"eps": 1e-6})
+        n = cf_rmsnorm(h, gam, 1e-6)
+    else:
+        g.add_node(OpType.LAYERNORM, ["h", "gam", "bet"], "n", {"eps": 1e-5})
+        n = cf_layernorm(h, gam, bet, 1e-5)
+    g.outputs += ["h", "n"]
+    return g, {"o": o, "x": x}, h, n
+
+
+@pytest.mark.parametrize("norm", ["rms", "layer"])
+@pytest.mark.parametrize("H,S,hd,N", [(12, 512, 64, 768), (4, 100, 32, 520), (8, 64, 128, 1024)])
+def test_reduce_norm_after_head_layout_gemm(monkeypatch, norm, H, S, hd, N):
+    """The attention projection reading its A in head layout, + residual, + norm: one GEMM
+    (two K ranges when its own choice is unsplit) whose reduce writes C and the normalised
+    rows, bit-equal to the plan with the norm kernel apart (both in two K ranges)."""
+    monkeypatch.setenv("LBR_GEMM_KSPLIT", "2")
+    g, ins, h64, n64 = _tin_graph(rng(H + S + hd + N), H, S, hd, N, norm)
+    h, n, names = _run(g, ins)
+    monkeypatch.setenv("LBR_REDUCE_NORM", "0")
+    h2, n2, names2 = _run(g, ins)
+    print(names, names2)
+    suffix = "+tin+resid+rmsnorm" if norm == "rms" else "+tin+resid+layernorm"
+    assert any(nm.endswith(suffix) for nm in names), names
+    assert any(nm.endswith("+tin+resid") for nm in names2), names2
+    np.testing.assert_array_equal(h, h2)
+    np.testing.assert_array_equal(n, n2)
+    from oracle.host_exec import OracleRun
+    from runtime.planner import plan
+    o = OracleRun(plan(g)).run(ins)
+    assert normwise_rel(n, n64) <= 1e-4 and normwise_rel(h, h64) <= 1e-4
+    assert normwise_rel(n, o["n"]) <= 1e-4 and normwise_rel(o["n"], n64) <= 1e-4
+
+
 @pytest.mark.parametrize("N", [6000, 256])
 def test_reduce_norm_other_widths_stay_apart(monkeypatch, N):
     """Rows above 4096 or of at most 256 columns keep the norm kernel."""
