@@ -173,12 +173,12 @@ class Workload:
     def model(self, seed: int = 0) -> nn.Module:
         return init_weights(self.build(), seed)
 
-    def input(self, seed: int = 0, seq_len: int | None = None) -> np.ndarray:
+    def input(self, seed: int = 0, seq_len: int | None = None, batch: int = 1) -> np.ndarray:
         s = self.seq_len if seq_len is None else seq_len
         rng = np.random.default_rng(seed)
         if self.vocab:
-            return rng.integers(0, self.vocab, (1, s), dtype=np.int64)
-        return rng.standard_normal((1, s, self.d_model)).astype(np.float32)
+            return rng.integers(0, self.vocab, (batch, s), dtype=np.int64)
+        return rng.standard_normal((batch, s, self.d_model)).astype(np.float32)
 
 
 WORKLOADS: dict[str, Workload] = {
@@ -203,12 +203,12 @@ CONFIG_ORDER = ["toy", "gpt2w", "gpt2", "7b4k", "qwen3_4b"]
 LM_ORDER = ["gpt2_lm", "qwen3_4b_lm"]
 
 
-def export_workload(key: str, seed: int = 0, seq_len: int | None = None):
-    """(model, input numpy, exported Graph) for a workload."""
+def export_workload(key: str, seed: int = 0, seq_len: int | None = None, batch: int = 1):
+    """(model, input numpy, exported Graph) for a workload (the BASELINE configs are batch 1)."""
     from runtime.exporter import export_model
     w = WORKLOADS[key]
     model = w.model(seed)
-    x = w.input(seed, seq_len)
+    x = w.input(seed, seq_len, batch)
     graph = export_model(model, (torch.from_numpy(x),))
     return model, x, graph
 

@@ -46,6 +46,30 @@ def test_workload_parity(key, seq):
     assert e_go <= TOL
 
 
+# Batch > 1 at sequence lengths that are multiples of no tile (the BASELINE configs are
+# batch 1): the head scatter and head prologue take (b, s) from the GEMM row, attention runs
+# over B·H heads with causal rows per batch, RoPE reads a table row per token, GEMM tiles
+# and attention blocks end mid-tile, and the norm joins run over B·S rows.
+@pytest.mark.parametrize("key,seq,batch", [("toy", 20, 3), ("gpt2w", 300, 2), ("gpt2", 200, 2),
+                                           ("qwen3_4b", 136, 2), ("7b4k", 100, 2), ("gpt2_lm", 72, 2),
+                                           ("qwen3_4b_lm", 40, 2)])
+def test_workload_parity_batched_ragged(key, seq, batch):
+    from workloads import export_workload, reference_forward
+    from oracle.host_exec import OracleRun
+    model, x, graph = export_workload(key, seq_len=seq, batch=batch)
+    y, sess = _session_run(graph, x)
+    runs = sess.executor.fused_runs()
+    o = OracleRun(sess.memory_plan).run({graph.inputs[0]: x})[graph.outputs[0]]
+    sess.close()
+    ref = reference_forward(model, x)
+    e_gpu, e_orc, e_go = normwise_rel(y, ref), normwise_rel(o, ref), normwise_rel(y, o)
+    print(f"{key} B={batch} S={seq}: {len(runs)} fused runs {sorted({k for _, _, k in runs})}; gpu-vs-torch64 "
+          f"{e_gpu:.2e}; oracle-vs-torch64 {e_orc:.2e}; gpu-vs-oracle {e_go:.2e} abs {np.abs(y - o).max():.2e}")
+    assert y.shape == ref.shape and np.isfinite(y).all()
+    assert runs, "the batched graph took no fused run"
+    assert e_orc <= TOL and e_gpu <= TOL and e_go <= TOL
+
+
 # Full BASELINE sizes where the float64 PyTorch leg would take minutes on the host:
 # the GPU output against the oracle on the same plan and input (the oracle itself is
 # pinned against float64 PyTorch by the reduced-size cases above and by
