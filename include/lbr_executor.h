@@ -256,6 +256,21 @@ int lbr_fusion_windows(const OpNode* nodes, int n_nodes,
                        const void* const* live_ptr, const size_t* live_bytes,
                        int n_live, lbr_window* out, int cap, int* n_out);
 
+/* The host half of lbr_plan_create (fuse = 0) or lbr_plan_create_fused
+ * (fuse = 1) without touching a device: every record checked (counts within
+ * its arrays, elem_size 1, 2, 4 or 8, no negative dim, at most 2^40
+ * elements), every node decoded and its extras checked against its shape,
+ * the fused runs found and their steps and step joins built.  Returns the
+ * status and error those calls would report for a malformed or unsupported
+ * node array, and the number of kernel steps in *n_steps (may be NULL).
+ * Choices that depend on the device take 256 CUs before lbr_init.  No
+ * counterpart in the reference (its execute(), csrc/executor.c:409-452, trusts
+ * the host layer's records): for callers that build node arrays themselves
+ * and want them checked before a device is touched. */
+int lbr_check_nodes(const OpNode* nodes, int n_nodes, int fuse,
+                    const void* const* live_ptr, const size_t* live_bytes,
+                    int n_live, int* n_steps);
+
 /* lbr_plan_create with peephole fusion (live-out ranges as above). */
 int lbr_plan_create_fused(const OpNode* nodes, int n_nodes, int use_graph,
                           const void* const* live_ptr,

@@ -386,11 +386,19 @@ int fill_broadcast(const OpNode* n, int base, Step* s) {
         as[d] = n->extra[base + 1 + d];
         bs[d] = n->extra[base + 1 + nd + d];
         shape[d] = n->extra[base + 1 + 2 * nd + d];
-        if (shape[d] < 0) {
-            lbr_set_error("broadcast: negative dim");
+        if (shape[d] < 0 || as[d] < 0 || bs[d] < 0) {
+            lbr_set_error("broadcast: negative dim or stride");
+            return LBR_ERR_INVALID;
+        }
+        if (shape[d] > 0 && total > LBR_MAX_ELEMENTS / shape[d]) {
+            lbr_set_error("broadcast: more than 2^40 elements");
             return LBR_ERR_INVALID;
         }
         total *= shape[d];
+    }
+    if (total != node_total(n)) {
+        lbr_set_error("broadcast: %lld elements, the output has %lld", total, node_total(n));
+        return LBR_ERR_INVALID;
     }
     // drop size-1 dims, then merge neighbours that stay linear for both operands
     long long cs[MAX_DIMS], ca[MAX_DIMS], cb[MAX_DIMS];

@@ -244,6 +244,32 @@ static decode_fn decoder_for(int op) {
     }
 }
 
+int lbr_node_check(const OpNode* n, int index) {
+    if (n->n_inputs < 0 || n->n_inputs > MAX_INPUTS || n->n_dims < 0 || n->n_dims > MAX_DIMS) {
+        lbr_set_error("executor: node %d has n_inputs=%d n_dims=%d", index, n->n_inputs, n->n_dims);
+        return LBR_ERR_INVALID;
+    }
+    if (n->elem_size != 1 && n->elem_size != 2 && n->elem_size != 4 && n->elem_size != 8) {
+        lbr_set_error("executor: node %d has elem_size %d", index, n->elem_size);
+        return LBR_ERR_INVALID;
+    }
+    long long total = 1;
+    for (int i = 0; i < n->n_dims; ++i) {
+        if (n->out_shape[i] < 0) {
+            lbr_set_error("executor: node %d has a negative dim", index);
+            return LBR_ERR_INVALID;
+        }
+        // 2^40 elements is more than any device holds; the bound keeps every product of
+        // dims (and of dims with the op's extras, each < 2^31) inside 64 bits
+        if (n->out_shape[i] > 0 && total > LBR_MAX_ELEMENTS / n->out_shape[i]) {
+            lbr_set_error("executor: node %d has more than 2^40 elements", index);
+            return LBR_ERR_INVALID;
+        }
+        total *= n->out_shape[i];
+    }
+    return LBR_OK;
+}
+
 static int decode_node(const OpNode* n, int index, Step* s) {
     memset(s, 0, sizeof(*s));
     s->node_index = index;
@@ -253,15 +279,7 @@ static int decode_node(const OpNode* n, int index, Step* s) {
         lbr_set_error("executor: unknown op %d (node %d)", n->op, index);
         return LBR_ERR_UNSUPPORTED;
     }
-    if (n->n_inputs < 0 || n->n_inputs > MAX_INPUTS || n->n_dims < 0 || n->n_dims > MAX_DIMS) {
-        lbr_set_error("executor: node %d has n_inputs=%d n_dims=%d", index, n->n_inputs, n->n_dims);
-        return LBR_ERR_INVALID;
-    }
-    for (int i = 0; i < n->n_dims; ++i)
-        if (n->out_shape[i] < 0) {
-            lbr_set_error("executor: node %d has a negative dim", index);
-            return LBR_ERR_INVALID;
-        }
+    if (int rc = lbr_node_check(n, index)) return rc;
     s->n_in = n->n_inputs;
     int rc = d(n, s);
     if (rc != LBR_OK) {
@@ -560,25 +578,21 @@ static int autotune_gemms(std::vector<Step>& steps, const std::vector<char>& tab
 
 // Decode every node (so each is validated exactly as without fusion), then
 // replace the fused runs by their steps; capture a hipGraph if asked.
-static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fuse, const void* const* live_ptr,
-                       const size_t* live_bytes, int n_live, lbr_plan** out_plan) {
-    lbr_plan* p = new lbr_plan();
+// The host half of plan creation: decode every node, find the fused runs, build
+// their steps and join steps (no device call).  The plan's steps and node map
+// are filled; on an error they are left partial.
+static int build_steps(lbr_plan* p, const OpNode* nodes, int n_nodes, bool fuse, const void* const* live_ptr,
+                       const size_t* live_bytes, int n_live) {
     p->n_nodes = n_nodes;
     std::vector<Step> decoded((size_t)n_nodes);
     for (int i = 0; i < n_nodes; ++i) {
         int rc = decode_node(&nodes[i], i, &decoded[i]);
-        if (rc) {
-            delete p;
-            return rc;
-        }
+        if (rc) return rc;
     }
     std::vector<FusedRun> runs;
     if (fuse) {
         int rc = lbr_find_fusions(nodes, n_nodes, live_ptr, live_bytes, n_live, &runs);
-        if (rc) {
-            delete p;
-            return rc;
-        }
+        if (rc) return rc;
     }
     p->node_step.assign((size_t)n_nodes, -1);
     size_t r = 0;
@@ -587,10 +601,7 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
         if (r < runs.size() && runs[r].first == i) {
             Step s;
             int rc = lbr_fused_step(nodes, runs[r], &s);
-            if (rc) {
-                delete p;
-                return rc;
-            }
+            if (rc) return rc;
             s.fuse_kind = runs[r].kind;
             i += runs[r].count;
             ++r;
@@ -598,10 +609,7 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
             if (r < runs.size() && runs[r].first == i && runs[r].kind == LBR_FUSE_HEAD_PROLOGUE) {
                 Step s2;
                 rc = lbr_fused_step(nodes, runs[r], &s2);
-                if (rc) {
-                    delete p;
-                    return rc;
-                }
+                if (rc) return rc;
                 s2.fuse_kind = runs[r].kind;
                 if (lbr_merge_head_steps(&s, s2)) {
                     i += runs[r].count;
@@ -614,10 +622,7 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
                 s.fuse_kind == LBR_FUSE_TRANSPOSE_GEMM) {
                 Step s2;
                 rc = lbr_fused_step(nodes, runs[r], &s2);
-                if (rc) {
-                    delete p;
-                    return rc;
-                }
+                if (rc) return rc;
                 s2.fuse_kind = runs[r].kind;
                 if (lbr_merge_proj_mlp(&s2, s)) {
                     s = s2;
@@ -650,15 +655,31 @@ static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fus
             ++i;
         }
     }
-    int rc = !fuse ? LBR_OK : relay_attention_outputs(p, nodes, n_nodes, live_ptr, live_bytes, n_live);
+    return LBR_OK;
+}
+
+static int check_kernels(const lbr_plan& p) {
+    for (size_t i = 0; i < p.steps.size(); ++i)
+        if (!p.steps[i].run) {
+            lbr_set_error("lbr_plan_create: step %zu (node %d) has no kernel", i, p.steps[i].node_index);
+            return LBR_ERR_INVALID;
+        }
+    return LBR_OK;
+}
+
+static int create_plan(const OpNode* nodes, int n_nodes, int use_graph, bool fuse, const void* const* live_ptr,
+                       const size_t* live_bytes, int n_live, lbr_plan** out_plan) {
+    lbr_plan* p = new lbr_plan();
+    int rc = build_steps(p, nodes, n_nodes, fuse, live_ptr, live_bytes, n_live);
+    if (rc) {
+        delete p;
+        return rc;
+    }
+    rc = !fuse ? LBR_OK : relay_attention_outputs(p, nodes, n_nodes, live_ptr, live_bytes, n_live);
     if (!rc && fuse) rc = relay_head_outputs(p);
     if (!rc && fuse) rc = relay_gated_outputs(p);
     if (!rc && fuse) fragment_keys(p, nodes, n_nodes, live_ptr, live_bytes, n_live);
-    for (size_t i = 0; i < p->steps.size() && !rc; ++i)
-        if (!p->steps[i].run) {
-            lbr_set_error("lbr_plan_create: step %zu (node %d) has no kernel", i, p->steps[i].node_index);
-            rc = LBR_ERR_INVALID;
-        }
+    if (!rc) rc = check_kernels(*p);
     std::vector<char> tabled;
     if (!rc) table_tiles(p->steps, &tabled);
     if (!rc) rc = assign_workspace(p->steps, &p->ws);
@@ -707,6 +728,7 @@ int lbr_init(int device) {
         lbr_set_error("lbr_init: device %d is %s; this library is built for gfx950", device, prop.gcnArchName);
         return LBR_ERR_NO_DEVICE;
     }
+    HIP_TRY(mlp_prepare_device());
     // this device's copy of the no-allocation scratch array (see lbr_execute_noalloc)
     if (device < LBR_MAX_DEVICES && !g_scratch_dev[device]) {
         void* ptr = nullptr;
@@ -979,6 +1001,19 @@ int lbr_fusion_windows(const OpNode* nodes, int n_nodes, const void* const* live
     }
     *n_out = (int)runs.size();
     return LBR_OK;
+}
+
+int lbr_check_nodes(const OpNode* nodes, int n_nodes, int fuse, const void* const* live_ptr,
+                    const size_t* live_bytes, int n_live, int* n_steps) {
+    if (n_nodes < 0 || (n_nodes > 0 && !nodes) || bad_live(live_ptr, live_bytes, n_live)) {
+        lbr_set_error("lbr_check_nodes: bad arguments");
+        return LBR_ERR_INVALID;
+    }
+    lbr_plan p;
+    int rc = build_steps(&p, nodes, n_nodes, fuse != 0, live_ptr, live_bytes, n_live);
+    if (!rc) rc = check_kernels(p);
+    if (!rc && n_steps) *n_steps = (int)p.steps.size();
+    return rc;
 }
 
 int lbr_plan_num_steps(const lbr_plan* p) { return p ? (int)p->steps.size() : 0; }

@@ -1022,6 +1022,9 @@ bool lbr_frag_keys_ok(const OpNode* nodes, int n, const Step& gm, int k, const S
 int lbr_find_fusions(const OpNode* nodes, int n, const void* const* live_ptr, const size_t* live_bytes, int n_live,
                      std::vector<FusedRun>* out) {
     out->clear();
+    // every record within its arrays and sizes before any matcher reads one
+    for (int k = 0; k < n; ++k)
+        if (int rc = lbr_node_check(&nodes[k], k)) return rc;
     std::vector<Rng> live;
     for (int k = 0; k < n_live; ++k) live.push_back(rng(live_ptr[k], (long long)live_bytes[k]));
     int i = 0;
@@ -1455,8 +1458,8 @@ int lbr_fused_step(const OpNode* nodes, const FusedRun& f, Step* s) {
         s->f[2] = f.norm_eps;
         s->run = mlp_launcher(s1.i[2], f.act);
         if (!s->run) {
-            lbr_set_error("fusion: the MLP kernel's LDS limit could not be raised (node %d)", f.first + 1);
-            return LBR_ERR_HIP;
+            lbr_set_error("fusion: no MLP kernel for D=%lld (node %d)", s1.i[2], f.first + 1);
+            return LBR_ERR_INVALID;
         }
         s->name = f.norm ? "mlp_rows+norm" : "mlp_rows";
     } else if (f.kind == LBR_FUSE_NORM_GEMM) {

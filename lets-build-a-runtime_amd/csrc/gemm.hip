@@ -1561,7 +1561,7 @@ int decode_matmul(const OpNode* n, Step* s) {
         batches = 1;
         for (int i = 0; i < n->n_dims - 2; ++i) batches *= n->out_shape[i];
     }
-    if (M > INT32_MAX || N < 0 || K < 0 || batches > 65535) {
+    if (M > INT32_MAX || N < 0 || K < 0 || N > (1 << 30) || K > (1 << 30) || batches > 65535) {
         lbr_set_error("matmul: unsupported sizes M=%lld N=%d K=%d batches=%lld", M, N, K, batches);
         return LBR_ERR_UNSUPPORTED;
     }

@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <initializer_list>
+
 #include "../../include/lbr_executor.h"
 
 #define LBR_WAVE 64
@@ -436,9 +438,17 @@ const char* lbr_attn_step_name(const Step& s, bool v, bool t, int store);
 // the one-kernel form; its launcher (Step layout in mlp.hip).
 bool mlp_shape_ok(long long M, long long D, long long H, long long D2);
 step_fn mlp_launcher(long long D, int act, bool oproj = false);
+// Raises the MLP kernels' dynamic LDS limit on the current device (lbr_init).
+hipError_t mlp_prepare_device();
 // Whether the MLP kernel can also compute its input rows x = O·Woᵀ (+ bo)
 // (+ R0) from O in head layout (head dim hd, K0 = O's row width).
 bool mlp_proj_ok(long long D, long long H, long long K0, long long hd);
+
+// A node record's counts within its arrays (n_inputs ≤ MAX_INPUTS, n_dims ≤
+// MAX_DIMS), elem_size 1, 2, 4 or 8, no negative dim and at most
+// LBR_MAX_ELEMENTS elements; else an error naming node `index`.
+#define LBR_MAX_ELEMENTS (1LL << 40)
+int lbr_node_check(const OpNode* n, int index);
 
 // Helpers over the node record (same meaning as csrc/executor.c:30-48).
 static inline long long node_total(const OpNode* n) {
@@ -453,6 +463,16 @@ static inline long long node_leading(const OpNode* n) {
 }
 static inline int node_last_dim(const OpNode* n) {
     return n->n_dims > 0 ? n->out_shape[n->n_dims - 1] : 1;
+}
+// Whether extents an op's extras give (each ≥ 0) multiply to the node's
+// element count, without overflow.
+static inline bool lbr_sizes_match(const OpNode* n, std::initializer_list<long long> ext) {
+    long long t = 1;
+    for (long long e : ext) {
+        if (e < 0 || (e > 0 && t > LBR_MAX_ELEMENTS / e)) return false;
+        t *= e;
+    }
+    return t == node_total(n);
 }
 static inline float node_extra_float(const OpNode* n, int idx) {
     union { int i; float f; } u;

@@ -487,23 +487,32 @@ bool mlp_shape_ok(long long M, long long D, long long H, long long D2) {
            mlp_lds_bytes(D, H, false) + 2 * MLP_WMAX * sizeof(float) <= MLP_LDS_MAX;
 }
 
-// The kernel's LDS (128 KB static + xs, hs) exceeds the default: the dynamic
-// limit is raised once per instantiation, at plan creation (outside any graph
-// capture).
-template <int ACT, int VPL, bool OPROJ>
-static step_fn mlp_prepared() {
-    static const bool raised =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&mlp_rows<ACT, VPL, OPROJ>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)(MLP_LDS_MAX - 2 * MLP_WMAX * sizeof(float))) == hipSuccess;
-    return raised ? launch_mlp<ACT, VPL, OPROJ> : nullptr;
+template <int ACT, bool OPROJ>
+static hipError_t mlp_raise_lds() {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&mlp_rows<ACT, 1, OPROJ>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)(MLP_LDS_MAX - 2 * MLP_WMAX * sizeof(float)));
+}
+
+// The kernel's LDS (128 KB static + xs, hs) exceeds the default: lbr_init
+// raises the dynamic limit of every instantiation the launcher hands out, on
+// the device it initialises (outside any graph capture), so choosing the
+// kernel at plan creation makes no device call.
+hipError_t mlp_prepare_device() {
+    hipError_t e = mlp_raise_lds<LBR_ACT_RELU, false>();
+    if (e == hipSuccess) e = mlp_raise_lds<LBR_ACT_RELU, true>();
+    if (e == hipSuccess) e = mlp_raise_lds<LBR_ACT_GELU, false>();
+    if (e == hipSuccess) e = mlp_raise_lds<LBR_ACT_GELU, true>();
+    if (e == hipSuccess) e = mlp_raise_lds<LBR_ACT_SILU, false>();
+    if (e == hipSuccess) e = mlp_raise_lds<LBR_ACT_SILU, true>();
+    return e;
 }
 
 // D ≤ 256 always holds (each wave's W1 fragments, ceil(H/64)·D/16, are at
 // most 16), so the rows take one float4 a lane.
 template <int ACT>
 static step_fn mlp_launcher_act(bool oproj) {
-    return oproj ? mlp_prepared<ACT, 1, true>() : mlp_prepared<ACT, 1, false>();
+    return oproj ? launch_mlp<ACT, 1, true> : launch_mlp<ACT, 1, false>;
 }
 
 step_fn mlp_launcher(long long D, int act, bool oproj) {

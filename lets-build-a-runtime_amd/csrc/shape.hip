@@ -249,6 +249,11 @@ int decode_transpose(const OpNode* n, Step* s) {
             lbr_set_error("transpose2d: elem_size %d", n->elem_size);
             return LBR_ERR_UNSUPPORTED;
         }
+        if (n->extra[0] < 0 || n->extra[1] < 0 || (long long)n->extra[0] * n->extra[1] != node_total(n)) {
+            lbr_set_error("transpose2d: %d x %d does not match the output's %lld elements", n->extra[0],
+                          n->extra[1], node_total(n));
+            return LBR_ERR_INVALID;
+        }
         s->i[0] = n->extra[0];
         s->i[1] = n->extra[1];
         s->i[2] = n->elem_size;
@@ -257,6 +262,11 @@ int decode_transpose(const OpNode* n, Step* s) {
         return LBR_OK;
     }
     const long long outer = n->extra[0], A = n->extra[1], mid = n->extra[2], B = n->extra[3], inner = n->extra[4];
+    if (!lbr_sizes_match(n, {outer, A, mid, B, inner})) {
+        lbr_set_error("transpose: extents %lld x %lld x %lld x %lld x %lld do not match the output's %lld elements",
+                      outer, A, mid, B, inner, node_total(n));
+        return LBR_ERR_INVALID;
+    }
     const long long chunk = inner * n->elem_size;
     const int w = word_size(chunk, chunk, n->inputs[0], n->output);
     s->i[0] = outer;
@@ -278,6 +288,11 @@ int decode_slice(const OpNode* n, Step* s) {
     const long long es = n->elem_size;
     if (start < 0 || len < 0 || start + len > orig) {
         lbr_set_error("slice: start %lld len %lld outside dim %lld", start, len, orig);
+        return LBR_ERR_INVALID;
+    }
+    if (!lbr_sizes_match(n, {outer, len, inner})) {
+        lbr_set_error("slice: %lld x %lld x %lld does not match the output's %lld elements", outer, len, inner,
+                      node_total(n));
         return LBR_ERR_INVALID;
     }
     const long long src_stride = orig * inner * es, dst_stride = len * inner * es, copy = len * inner * es;
@@ -304,12 +319,27 @@ int decode_cat(const OpNode* n, Step* s) {
         return LBR_ERR_INVALID;
     }
     const int dim = n->extra[0];
+    if (dim < 0 || dim >= n->n_dims) {
+        lbr_set_error("cat: dim %d outside the output's %d dims", dim, n->n_dims);
+        return LBR_ERR_INVALID;
+    }
     long long outer = 1, inner = 1;
     for (int i = 0; i < dim; ++i) outer *= n->out_shape[i];
     for (int i = dim + 1; i < n->n_dims; ++i) inner *= n->out_shape[i];
     const long long es = n->elem_size;
     long long total_dim = 0;
-    for (int k = 0; k < nin; ++k) total_dim += n->extra[1 + k];
+    for (int k = 0; k < nin; ++k) {
+        if (n->extra[1 + k] < 0) {
+            lbr_set_error("cat: input %d has a negative extent", k);
+            return LBR_ERR_INVALID;
+        }
+        total_dim += n->extra[1 + k];
+    }
+    if (total_dim != n->out_shape[dim]) {
+        lbr_set_error("cat: the inputs' extents sum to %lld, the output's dim %d is %d", total_dim, dim,
+                      n->out_shape[dim]);
+        return LBR_ERR_INVALID;
+    }
     // widest word every segment allows
     int w = 16;
     for (;;) {
@@ -345,6 +375,10 @@ int decode_embedding(const OpNode* n, Step* s) {
     if (rc) return rc;
     if (n->extra[1] <= 0) {
         lbr_set_error("embedding: extra[1] must hold the table row count");
+        return LBR_ERR_INVALID;
+    }
+    if (n->extra[0] < 0 || n->extra[0] != node_last_dim(n)) {
+        lbr_set_error("embedding: embed_dim %d is not the output's last dim %d", n->extra[0], node_last_dim(n));
         return LBR_ERR_INVALID;
     }
     s->i[2] = n->extra[1];

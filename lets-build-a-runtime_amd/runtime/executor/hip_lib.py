@@ -78,6 +78,7 @@ class HipLibrary:
             "lbr_fusion_windows": ([P(COpNode), c_int, P(c_vp), P(c_size), c_int, P(LbrWindow), c_int, P(c_int)],
                                    c_int),
             "lbr_plan_create_fused": ([P(COpNode), c_int, c_int, P(c_vp), P(c_size), c_int, P(c_vp)], c_int),
+            "lbr_check_nodes": ([P(COpNode), c_int, c_int, P(c_vp), P(c_size), c_int, P(c_int)], c_int),
             "lbr_plan_num_steps": ([c_vp], c_int),
             "lbr_plan_step_info": ([c_vp, c_int, P(c_int), P(c_int), P(c_int)], c_int),
             "lbr_plan_step_args": ([c_vp, c_int, P(ctypes.c_longlong), c_int], c_int),
@@ -131,6 +132,14 @@ class HipLibrary:
         self.check(self._lib.lbr_fusion_windows(nodes, n, lp, lb, len(live), out, cap, ctypes.byref(n_out)),
                    "lbr_fusion_windows")
         return [(out[k].first, out[k].count, FUSE_KINDS.get(out[k].kind, "?")) for k in range(n_out.value)]
+
+    def check_nodes(self, nodes, n: int, live: list[tuple[int, int]], fuse: bool = True) -> int:
+        """Kernel steps lbr_plan_create[_fused] would build from `nodes`, or its error; needs no device."""
+        lp, lb = live_arrays(live)
+        steps = ctypes.c_int(0)
+        self.check(self._lib.lbr_check_nodes(nodes, n, int(fuse), lp, lb, len(live), ctypes.byref(steps)),
+                   "lbr_check_nodes")
+        return steps.value
 
 
 def live_arrays(live: list[tuple[int, int]]):

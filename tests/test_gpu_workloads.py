@@ -34,6 +34,10 @@ def test_workload_parity(key, seq):
     from oracle.host_exec import OracleRun
     model, x, graph = export_workload(key, seq_len=seq)
     y, sess = _session_run(graph, x)
+    # the host half of plan creation, run alone (lbr_check_nodes), builds the plan's steps
+    ex = sess.executor
+    n_steps = len(ex.step_params())
+    assert ex._lib.check_nodes(ex._nodes, len(ex._order), ex.live_outs()) == n_steps
     o = OracleRun(sess.memory_plan).run({graph.inputs[0]: x})[graph.outputs[0]]
     ref = reference_forward(model, x)
     sess.close()

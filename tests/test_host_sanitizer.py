@@ -1,6 +1,7 @@
 """The library's host code (node decoders, the fusion matcher, plan joins,
 launch planning) under AddressSanitizer and UndefinedBehaviorSanitizer, on the
-CPU: the fusion-matcher and host-layer tests run in a subprocess against the
+CPU: the fusion-matcher (with malformed node arrays) and host-layer tests run
+in a subprocess against the
 sanitized build (build_native.build(sanitize=True), made by the graft build),
 with the shared ASan runtime preloaded.  A planted out-of-bounds read of a node
 array shows that the sanitizer is live in that setting.
@@ -42,7 +43,7 @@ def _run(args, env, timeout=900):
 def test_host_layer_tests_pass_under_asan_and_ubsan():
     env = _san_env()
     res = _run(["-m", "pytest", "-q", "-x", "-p", "no:cacheprovider", "tests/test_fusion.py",
-                "tests/test_host_layer.py", "-k",
+                "tests/test_fusion_fuzz.py", "tests/test_host_layer.py", "-k",
                 "not stream_counts and not plan_integrity and not graph_save_load and not dynamic_seq"], env)
     out = res.stdout + res.stderr
     print(out[-2000:])
