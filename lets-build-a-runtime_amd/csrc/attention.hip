@@ -1360,6 +1360,11 @@ int decode_attention(const OpNode* n, Step* s) {
             lbr_set_error("attention: input %d is null", i);
             return LBR_ERR_INVALID;
         }
+    if (n->out_shape[n->n_dims - 2] != seq || n->out_shape[n->n_dims - 1] != hd) {
+        lbr_set_error("attention: seq_len %d / head_dim %d are not the output's last dims %d x %d", seq, hd,
+                      n->out_shape[n->n_dims - 2], n->out_shape[n->n_dims - 1]);
+        return LBR_ERR_INVALID;
+    }
     long long bh = 1;
     for (int i = 0; i < n->n_dims - 2; ++i) bh *= n->out_shape[i];
     if (seq <= 0 || hd <= 0 || bh > 65535 || (group > 1 && bh % group != 0)) {

@@ -142,3 +142,13 @@ def test_fusion_matcher_rejects_out_of_range_records():
         arr[5].out_shape[0] = -2
         with pytest.raises(RuntimeError, match="node 5"):
             call(arr)
+    # extras that disagree with the output's shape (the kernels would index past it)
+    ops = [nd.op for nd in base]
+    for op, field, j, value, msg in [(1002, "extra", 0, 32, "seq_len"), (1002, "extra", 1, 32, "head_dim"),
+                                     (503, "extra", 3, 1, "slice"), (501, "extra", 4, 1, "transpose")]:
+        k = ops.index(op)
+        arr = _copy(base)
+        getattr(arr[k], field)[j] = value
+        for call in calls[1:]:
+            with pytest.raises(RuntimeError, match=msg):
+                call(arr)
