@@ -260,7 +260,9 @@ int lbr_fusion_windows(const OpNode* nodes, int n_nodes,
  * (fuse = 1) without touching a device: every record checked (counts within
  * its arrays, elem_size 1, 2, 4 or 8, no negative dim, at most 2^40
  * elements), every node decoded and its extras checked against its shape,
- * the fused runs found and their steps and step joins built.  Returns the
+ * the fused runs found and their steps and step joins built, the key layout
+ * and the tile table applied (not the relay buffers, which are allocated).
+ * Returns the
  * status and error those calls would report for a malformed or unsupported
  * node array, and the number of kernel steps in *n_steps (may be NULL).
  * Choices that depend on the device take 256 CUs before lbr_init.  No

@@ -376,7 +376,7 @@ step_fn bcast_for(int opc) {
 // a is dense" layout gets a vectorised kernel.
 int fill_broadcast(const OpNode* n, int base, Step* s) {
     const int nd = n->extra[base];
-    if (nd < 1 || 1 + 3 * nd > MAX_DIMS - base) {
+    if (nd < 1 || nd > (MAX_DIMS - base - 1) / 3) {
         lbr_set_error("broadcast: ndim %d does not fit the extras", nd);
         return LBR_ERR_INVALID;
     }

@@ -259,13 +259,14 @@ int lbr_node_check(const OpNode* n, int index) {
             lbr_set_error("executor: node %d has a negative dim", index);
             return LBR_ERR_INVALID;
         }
-        // 2^40 elements is more than any device holds; the bound keeps every product of
-        // dims (and of dims with the op's extras, each < 2^31) inside 64 bits
+        // 2^40 elements is more than any device holds; the bound (on the nonzero dims, so
+        // that it holds for every subset of them) keeps every product of dims, and of dims
+        // with one of the op's extras (each < 2^31), inside 64 bits
         if (n->out_shape[i] > 0 && total > LBR_MAX_ELEMENTS / n->out_shape[i]) {
             lbr_set_error("executor: node %d has more than 2^40 elements", index);
             return LBR_ERR_INVALID;
         }
-        total *= n->out_shape[i];
+        if (n->out_shape[i] > 0) total *= n->out_shape[i];
     }
     return LBR_OK;
 }
@@ -1011,7 +1012,14 @@ int lbr_check_nodes(const OpNode* nodes, int n_nodes, int fuse, const void* cons
     }
     lbr_plan p;
     int rc = build_steps(&p, nodes, n_nodes, fuse != 0, live_ptr, live_bytes, n_live);
+    // the plan's other host passes that need no device (the relays allocate their
+    // buffers, so they are left out: they change pointers, not the steps)
+    if (!rc && fuse) fragment_keys(&p, nodes, n_nodes, live_ptr, live_bytes, n_live);
     if (!rc) rc = check_kernels(p);
+    if (!rc) {
+        std::vector<char> tabled;
+        table_tiles(p.steps, &tabled);
+    }
     if (!rc && n_steps) *n_steps = (int)p.steps.size();
     return rc;
 }

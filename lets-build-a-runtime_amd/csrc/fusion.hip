@@ -361,14 +361,26 @@ Rng input_rng(const OpNode* nd, int k) {
     const long long lead = last ? total / last : 0;
     const int* x = nd->extra;
     long long e = -1;   // elements read; −1: not fixed by the node
+    // products of extents, −1 when a factor is negative or the product passes
+    // 2^40 elements (no node's operand is that large: the extent is then not fixed)
+    auto mul = [](std::initializer_list<long long> f) {
+        long long r = 1;
+        for (long long v : f) {
+            if (v < 0 || (v > 0 && r > LBR_MAX_ELEMENTS / v)) return -1LL;
+            r *= v;
+        }
+        return r;
+    };
     auto bcast = [&](int base) {   // [ndim, a strides, b strides, out shape] at extra[base]
         const int nd_ = x[base];
-        if (nd_ < 0 || base + 1 + 3 * nd_ > MAX_DIMS || k > 1) return -1LL;
+        if (nd_ < 0 || nd_ > (MAX_DIMS - 1 - base) / 3 || k > 1) return -1LL;
         long long span = 1;
         for (int d = 0; d < nd_; ++d) {
             const long long s = x[base + 1 + 2 * nd_ + d];
             if (s == 0) return 0LL;
-            span += (s - 1) * x[base + 1 + k * nd_ + d];
+            const long long t = mul({s - 1, x[base + 1 + k * nd_ + d]});
+            if (t < 0 || span > LBR_MAX_ELEMENTS - t) return -1LL;
+            span += t;
         }
         return span;
     };
@@ -384,29 +396,29 @@ Rng input_rng(const OpNode* nd, int k) {
             e = x[0] == 2 ? bcast(1) : (k == 0 || x[0] == 0) ? total : -1;
             break;
         case OP_MAX: case OP_SUM:
-            e = x[0] >= 0 ? prod_dims(nd, 0, x[0]) * x[1] * prod_dims(nd, x[0], nd->n_dims) : (long long)x[1] * total;
+            e = x[0] >= 0 ? mul({prod_dims(nd, 0, x[0]), x[1], prod_dims(nd, x[0], nd->n_dims)}) : mul({x[1], total});
             break;
         case OP_MATMUL: case OP_MATMUL_ADD: {
             const long long K = x[0], N = last;
             const bool b2d = x[2] != 0;
             const long long M = b2d ? lead : (nd->n_dims >= 2 ? nd->out_shape[nd->n_dims - 2] : 1);
             const long long batches = b2d ? 1 : prod_dims(nd, 0, nd->n_dims - 2);
-            e = k == 0 ? batches * M * K : k == 1 ? batches * N * K : k == 2 ? N : -1;
+            e = k == 0 ? mul({batches, M, K}) : k == 1 ? mul({batches, N, K}) : k == 2 ? N : -1;
             break;
         }
         case OP_TRANSPOSE:
-            e = nd->n_dims == 2 ? (long long)x[0] * x[1] : (long long)x[0] * x[1] * x[2] * x[3] * x[4];
+            e = nd->n_dims == 2 ? mul({x[0], x[1]}) : mul({x[0], x[1], x[2], x[3], x[4]});
             break;
         case OP_SLICE:
-            e = (long long)x[0] * x[1] * x[4];
+            e = mul({x[0], x[1], x[4]});
             break;
         case OP_CAT:
             e = (x[0] >= 0 && k < MAX_DIMS - 1)
-                    ? prod_dims(nd, 0, x[0]) * x[1 + k] * prod_dims(nd, x[0] + 1, nd->n_dims) : -1;
+                    ? mul({prod_dims(nd, 0, x[0]), x[1 + k], prod_dims(nd, x[0] + 1, nd->n_dims)}) : -1;
             break;
         case OP_EMBEDDING:
             if (k == 0) return {p, p + (uintptr_t)(lead * 8)};
-            e = x[1] > 0 ? (long long)x[1] * last : -1;
+            e = x[1] > 0 ? mul({x[1], last}) : -1;
             break;
         case OP_LAYERNORM: case OP_RMSNORM: case OP_FUSED_BIAS_RELU:
             e = k == 0 ? total : last;
@@ -417,7 +429,7 @@ Rng input_rng(const OpNode* nd, int k) {
         case OP_ATTENTION: {
             const long long S = x[0], hd = x[1], group = x[4] > 0 ? x[4] : 1;
             const long long bh = prod_dims(nd, 0, nd->n_dims - 2), kvh = bh ? (bh - 1) / group + 1 : 0;
-            e = k == 0 ? bh * S * hd : k <= 2 ? kvh * S * hd : (k == 3 && x[3]) ? bh * S * S : -1;
+            e = k == 0 ? mul({bh, S, hd}) : k <= 2 ? mul({kvh, S, hd}) : (k == 3 && x[3]) ? mul({bh, S, S}) : -1;
             break;
         }
         default:

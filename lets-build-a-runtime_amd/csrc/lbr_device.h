@@ -446,7 +446,8 @@ bool mlp_proj_ok(long long D, long long H, long long K0, long long hd);
 
 // A node record's counts within its arrays (n_inputs ≤ MAX_INPUTS, n_dims ≤
 // MAX_DIMS), elem_size 1, 2, 4 or 8, no negative dim and at most
-// LBR_MAX_ELEMENTS elements; else an error naming node `index`.
+// LBR_MAX_ELEMENTS as the product of its nonzero dims; else an error naming
+// node `index`.
 #define LBR_MAX_ELEMENTS (1LL << 40)
 int lbr_node_check(const OpNode* n, int index);
 

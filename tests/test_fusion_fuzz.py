@@ -47,7 +47,7 @@ def _copy(arr):
 def _mutate(r: np.random.Generator, arr, n: int) -> str:
     i = int(r.integers(n))
     nd = arr[i]
-    k = int(r.integers(9))
+    k = int(r.integers(10))
     pick = lambda xs: xs[int(r.integers(len(xs)))]   # noqa: E731
     if k == 0:
         j = int(r.integers(8))
@@ -77,11 +77,14 @@ def _mutate(r: np.random.Generator, arr, n: int) -> str:
     if k == 7:
         nd.elem_size = pick([0, 1, 2, 4, 8, -4])
         return f"node {i} elem_size={nd.elem_size}"
-    # every dim of a node huge: element counts past 2^63 if multiplied unchecked
+    # every dim of a node huge (element counts past 2^63 if multiplied unchecked), or one
+    # of them 0 (no elements, but products over the other dims still huge)
     nd.n_dims = pick([4, 8, 24])
     for j in range(nd.n_dims):
         nd.out_shape[j] = pick([65535, (1 << 31) - 1])
-    return f"node {i} huge dims x{nd.n_dims}"
+    if k == 9:
+        nd.out_shape[int(r.integers(nd.n_dims))] = 0
+    return f"node {i} huge dims x{nd.n_dims}{' with a 0' if k == 9 else ''}"
 
 
 @pytest.mark.parametrize("key,seq", [("toy", 32), ("gpt2w", 64), ("gpt2", 64), ("qwen3_4b", 64),
@@ -136,6 +139,9 @@ def test_fusion_matcher_rejects_out_of_range_records():
         arr[3].n_dims = 8
         for j in range(8):
             arr[3].out_shape[j] = 65535
+        with pytest.raises(RuntimeError, match="node 3 has more than 2\\^40 elements"):
+            call(arr)
+        arr[3].out_shape[0] = 0   # no elements, but the other dims' product is bounded too
         with pytest.raises(RuntimeError, match="node 3 has more than 2\\^40 elements"):
             call(arr)
         arr = _copy(base)
