@@ -333,23 +333,26 @@ struct BoolTag {
 
 // Key tiles query block `qblk` needs: all of them, or (causal) up to the one
 // holding its last row's diagonal.
-__device__ __forceinline__ int attn16_tiles(const AttnArgs& g, int qblk, bool causal) {
+__device__ __forceinline__ int attn16_tiles(const AttnArgs& g, int qblk, bool causal, int qb = A16_QB) {
     const int nt = (g.S + A16_KB - 1) / A16_KB;
-    return causal ? min(nt, min(g.S - 1, qblk * A16_QB + A16_QB - 1) / A16_KB + 1) : nt;
+    return causal ? min(nt, min(g.S - 1, qblk * qb + qb - 1) / A16_KB + 1) : nt;
 }
 
-// One 128-row query block of one head over key tiles [t0, t1): streams them
-// through Ks/Vs.  slot < 0: the range is the whole row, write O.  slot >= 0:
-// write the unnormalised partial (Σ p·V, running max m, Σ p) of this key
-// range to the split workspace for attn_split_merge.
-template <int DP, bool CAUSAL, bool HAS_MASK, bool SPLIT, bool DB = SPLIT>
+// One query block (16·NWQ rows, NWQ wavefronts of 16) of one head over key
+// tiles [t0, t1): streams them through Ks/Vs.  slot < 0: the range is the
+// whole row, write O (or, deferred, stage the row in the workspace for
+// attn_kq_flush).  slot >= 0: write the unnormalised partial (Σ p·V, running
+// max m, Σ p) of this key range to the split workspace for attn_split_merge.
+template <int DP, bool CAUSAL, bool HAS_MASK, bool SPLIT, bool DB = SPLIT, int NWQ = 8>
 __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qblk, int t0_, int t1, long long slot,
                                               float (*Ks)[DP + 4], float (*Vs)[DP + 4]) {
     constexpr int NCH = DP / 16;     // 16-wide d chunks (S reduction) and d blocks (O)
     constexpr int W = NCH < 4 ? NCH : 4;
     typedef float VW __attribute__((ext_vector_type(W)));
+    constexpr int NT = 64 * NWQ, QB = 16 * NWQ;                  // threads, query rows
+    static_assert(!SPLIT || NWQ == 8, "the split's partial slots hold 128 rows");
     constexpr int TILE4 = A16_KB * DP / 4;                       // float4 granules per K (or V) tile
-    constexpr int PER = (TILE4 + A16_NT - 1) / A16_NT;
+    constexpr int PER = (TILE4 + NT - 1) / NT;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
@@ -367,7 +370,7 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
         Vb = g.V + b * S * g.v_ld + (kvh - b * g.v_heads) * D;
         vst = g.v_ld;
     }
-    const int q_wave0 = qblk * A16_QB + wave * 16;
+    const int q_wave0 = qblk * QB + wave * 16;
     const int q = q_wave0 + lr;
 
     floatx4 qf[NCH];
@@ -398,7 +401,7 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
     int t_fast = t0;
     if (!HAS_MASK && D == DP) {
         int e = S / A16_KB;
-        if (CAUSAL) e = min(e, (qblk * A16_QB + 1) / A16_KB);
+        if (CAUSAL) e = min(e, (qblk * QB + 1) / A16_KB);
         t_fast = max(t0, min(t1, e));
     }
 
@@ -407,7 +410,7 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
         constexpr bool CHECKED = decltype(checked_tag)::value;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int idx = tid + i * A16_NT;
+            const int idx = tid + i * NT;
             const int r = idx / (DP / 4), d = (idx % (DP / 4)) * 4;
             const long long voff = (long long)(k0 + r) * vst + d;
             if (CHECKED) {
@@ -415,7 +418,7 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
                 const long long off = (long long)(k0 + r) * D + d;
                 kr[i] = ok ? *reinterpret_cast<const float4*>(Kb + off) : make_float4(0.f, 0.f, 0.f, 0.f);
                 vr[i] = ok ? *reinterpret_cast<const float4*>(Vb + voff) : make_float4(0.f, 0.f, 0.f, 0.f);
-            } else if (TILE4 % A16_NT == 0 || idx < TILE4) {
+            } else if (TILE4 % NT == 0 || idx < TILE4) {
                 // D == DP: granule idx of the K tile is float offset 4·idx from row k0
                 const long long off = (long long)k0 * DP + 4 * idx;
                 kr[i] = *reinterpret_cast<const float4*>(Kb + off);
@@ -431,7 +434,7 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
         float (*Vd)[DP + 4] = Vs + buf * A16_KB;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int idx = tid + i * A16_NT;
+            const int idx = tid + i * NT;
             if (idx < TILE4) {
                 const int r = idx / (DP / 4), d = (idx % (DP / 4)) * 4;
                 *reinterpret_cast<float4*>(&Kd[r][d]) = kr[i];
@@ -553,7 +556,10 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
         const bool part = SPLIT && slot >= 0;
         const long long prow = slot * A16_QB + (q - qblk * A16_QB);   // partial row in the workspace
         const float inv_l = part ? 1.0f : 1.0f / l_run;
-        float* __restrict__ Ob = part ? g.part + prow * D : attn_out_row(g, bh, q);
+        // a deferred unsplit block stages its rows as [bh, S, D] for attn_kq_flush
+        float* __restrict__ Ob = part ? g.part + prow * D
+                                      : (!SPLIT && g.sk_defer) ? g.part + (bh * S + q) * (long long)D
+                                                               : attn_out_row(g, bh, q);
         if (part && lg == 0) {
             g.ml[2 * prow] = m_run;
             g.ml[2 * prow + 1] = l_run;
@@ -608,19 +614,27 @@ __device__ __forceinline__ int sk_block_start(const AttnArgs& g, int qb, bool ca
     return t;
 }
 
-template <int DP, bool CAUSAL, bool HAS_MASK>
-__global__ __launch_bounds__(A16_NT, 4) void attn_fwd_mfma16(AttnArgs g) {
-    __shared__ float Ks[A16_KB][DP + 4];
-    __shared__ float Vs[A16_KB][DP + 4];
+// NWQ = 8: 128-row blocks, a few workgroups a CU.  NWQ = 4: 64-row blocks,
+// folded, for causal grids the 128-row fold leaves short of one workgroup a CU
+// (Qwen3-4B S1024: 32 heads × 8 pairs of 64-row blocks = 256 workgroups, one a
+// CU with equal work, where 128-row blocks give 128 pairs or a key-range
+// split and its merge); one workgroup a CU holds two K/V tiles in LDS, so a
+// tile ends with one barrier.
+template <int DP, bool CAUSAL, bool HAS_MASK, int NWQ = 8>
+__global__ __launch_bounds__(64 * NWQ, NWQ == 8 ? 4 : 1) void attn_fwd_mfma16(AttnArgs g) {
+    constexpr bool DB = NWQ == 4;
+    constexpr int QB = 16 * NWQ;
+    __shared__ float Ks[(DB ? 2 : 1) * A16_KB][DP + 4];
+    __shared__ float Vs[(DB ? 2 : 1) * A16_KB][DP + 4];
     const int j = blockIdx.x, last = g.n_qblocks - 1 - j;
     if (!CAUSAL) {
-        attn16_qblock<DP, CAUSAL, HAS_MASK, false>(g, 0, j, 0, attn16_tiles(g, j, false), -1, Ks, Vs);
+        attn16_qblock<DP, CAUSAL, HAS_MASK, false, DB, NWQ>(g, 0, j, 0, attn16_tiles(g, j, false, QB), -1, Ks, Vs);
         return;
     }
-    attn16_qblock<DP, CAUSAL, HAS_MASK, false>(g, 0, last, 0, attn16_tiles(g, last, true), -1, Ks, Vs);
+    attn16_qblock<DP, CAUSAL, HAS_MASK, false, DB, NWQ>(g, 0, last, 0, attn16_tiles(g, last, true, QB), -1, Ks, Vs);
     if (g.fold && j < last) {   // folded second block: query block j
         __syncthreads();
-        attn16_qblock<DP, CAUSAL, HAS_MASK, false>(g, 0, j, 0, attn16_tiles(g, j, true), -1, Ks, Vs);
+        attn16_qblock<DP, CAUSAL, HAS_MASK, false, DB, NWQ>(g, 0, j, 0, attn16_tiles(g, j, true, QB), -1, Ks, Vs);
     }
 }
 
@@ -1085,6 +1099,7 @@ __global__ __launch_bounds__(256) void attn_fwd_rows(AttnArgs g, int causal) {
 //          [14]=deferred output (the merge kernel, or attn_kq_flush, writes every row of O)
 //          [15]=key-quartered kernel (attn_fwd_kq) [16]=K stored fragment-major (key-quartered
 //          kernel only; set by the plan with the QKV GEMM's head scatter, lbr_frag_keys_ok)
+//          [18]=16x16 kernel on folded 64-row query blocks (4 wavefronts)
 AttnArgs make_args(const Step& s) {
     AttnArgs g;
     g.Q = (const float*)s.in[0];
@@ -1152,6 +1167,19 @@ void launch_attn16(const Step& s, hipStream_t st) {
         return;
     }
     g.part = g.ml = nullptr;
+    if (s.i[18]) {
+        // 64-row folded blocks; a deferred store stages the rows for attn_kq_flush
+        g.n_qblocks = (g.S + 63) / 64;
+        g.sk_defer = s.i[14] != 0;
+        if (g.sk_defer) g.part = (float*)s.ws;
+        const unsigned gx = g.fold ? (unsigned)(g.n_qblocks + 1) / 2 : (unsigned)g.n_qblocks;
+        hipLaunchKernelGGL((attn_fwd_mfma16<DP, CAUSAL, HAS_MASK, 4>), dim3(gx, (unsigned)s.i[0]), dim3(256), 0, st, g);
+        if (g.sk_defer)
+            hipLaunchKernelGGL(attn_kq_flush, dim3((unsigned)(((long long)g.S * (g.D / 4) + 255) / 256),
+                                                   (unsigned)s.i[0]),
+                               dim3(256), 0, st, g);
+        return;
+    }
     const unsigned gx = g.fold ? (unsigned)(g.n_qblocks + 1) / 2 : (unsigned)g.n_qblocks;
     hipLaunchKernelGGL((attn_fwd_mfma16<DP, CAUSAL, HAS_MASK>), dim3(gx, (unsigned)s.i[0]), dim3(A16_NT), 0, st, g);
 }
@@ -1241,9 +1269,10 @@ step_fn pick_kq(bool causal, bool mask) {
 
 void lbr_attn_defer(Step* s) {
     s->i[14] = 1;
-    // the key-quartered kernel stages every row of O ([bh, S, D]) for attn_kq_flush; the
-    // split's workspace (its partials) already covers every block
-    if (s->i[15] == 1) s->ws_bytes = (size_t)s->i[0] * (size_t)s->i[1] * (size_t)s->i[2] * sizeof(float) + 256;
+    // the key-quartered kernel and the 64-row fold stage every row of O ([bh, S, D]) for
+    // attn_kq_flush; the split's workspace (its partials) already covers every block
+    if (s->i[15] == 1 || s->i[18] == 1)
+        s->ws_bytes = (size_t)s->i[0] * (size_t)s->i[1] * (size_t)s->i[2] * sizeof(float) + 256;
 }
 
 const char* lbr_attn_step_name(const Step& s, bool v, bool t, int store) {
@@ -1349,7 +1378,10 @@ extern "C" int lbr_attn_kq_grid(long long bh, int seq, int causal, int cus, int*
 }
 
 int decode_attention(const OpNode* n, Step* s) {
-    const int seq = n->extra[0], hd = n->extra[1], causal = n->extra[2] != 0, has_mask = n->extra[3] != 0;
+    // an additive mask replaces the causal pattern: the reference applies one or the other,
+    // never both (attn.c:40-48; its flash path, the only other, takes no mask, executor.c:389)
+    const int has_mask = n->extra[3] != 0;
+    const int seq = n->extra[0], hd = n->extra[1], causal = n->extra[2] != 0 && !has_mask;
     const int group = n->extra[4] > 0 ? n->extra[4] : 1;
     if (n->n_inputs < (has_mask ? 4 : 3) || !n->output || n->n_dims < 2) {
         lbr_set_error("attention: malformed node");
@@ -1438,6 +1470,21 @@ int decode_attention(const OpNode* n, Step* s) {
                     s->name = "attn_fwd_kq_f32";
                     s->i[10] = 1;   // can write O as [B, S, H, D] and read a strided V, like the 16x16 kernel
                     return LBR_OK;
+                }
+            }
+            // Causal grids the 128-row fold leaves short of one workgroup a CU, head dim
+            // > 64: folded 64-row blocks (4 wavefronts) when their pairs give every CU one
+            // workgroup of equal work, no split and no merge.  Qwen3-4B S1024 (32 heads):
+            // 256 workgroups.  LBR_ATTN_FOLD64=1 forces it for any causal grid, 0 turns it
+            // off; a forced schedule (LBR_ATTN_FOLD / _SPLIT / _SPLIT_WG) keeps it off.
+            {
+                const long long n64 = (seq + 63) / 64;
+                const bool forced = getenv("LBR_ATTN_FOLD") || getenv("LBR_ATTN_SPLIT") || getenv("LBR_ATTN_SPLIT_WG");
+                bool fold64 = causal && !s->i[6] && !forced && (n64 + 1) / 2 * bh >= cus;
+                if (const char* f64 = getenv("LBR_ATTN_FOLD64")) fold64 = atoi(f64) != 0 && causal && !forced;
+                if (fold64) {
+                    s->i[6] = 1;
+                    s->i[18] = 1;
                 }
             }
             long long head_tiles = 0;

@@ -424,9 +424,9 @@ int gemm_dma_written(const Step& s, void** ptr, size_t* bytes, int cap);
 int decode_attention(const OpNode* n, Step* s);
 // Whether a decoded attention step can defer its store (its rows staged, then
 // written by a second kernel after every read of Q, K and V, so that O may lie
-// over them): the key-range split (merge kernel) and the key-quartered kernel
-// (attn_kq_flush).
-inline bool lbr_attn_can_defer(const Step& s) { return s.i[7] > 0 || s.i[15] == 1; }
+// over them): the key-range split (merge kernel), the key-quartered kernel and
+// the 16x16 kernel on folded 64-row blocks (attn_kq_flush).
+inline bool lbr_attn_can_defer(const Step& s) { return s.i[7] > 0 || s.i[15] == 1 || s.i[18] == 1; }
 // Marks a decoded attention step (lbr_attn_can_defer) as deferring its store,
 // with the workspace that needs.
 void lbr_attn_defer(Step* s);

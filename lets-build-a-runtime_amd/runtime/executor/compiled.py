@@ -284,7 +284,8 @@ class CompiledExecutor(Executor):
                  "count": count.value, "kind": FUSE_KINDS.get(kind.value, "?")}
             if d["kernel"].startswith(("attn_fwd_mfma16", "attn_fwd_kq")):
                 d.update(fold=bool(ints[6]), split_wg=int(ints[7]), defer=bool(ints[14]), kq=bool(ints[15]),
-                         k_frag=bool(ints[15]) and bool(ints[16]))
+                         k_frag=bool(ints[15]) and bool(ints[16]),
+                         block_rows=16 if ints[15] else 64 if ints[18] else 128)
             elif d["kernel"].startswith("gemm_"):
                 d.update(m=int(ints[0]), n=int(ints[1]), k=int(ints[2]),
                          tile=lib.lbr_gemm_tile_name(int(ints[14]) - 1).decode() or "legacy",

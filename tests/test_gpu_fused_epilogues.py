@@ -224,16 +224,21 @@ def test_attention_sliced_v(monkeypatch, split, H, Hkv, S, hd, causal):
     _check(g, {"q": q, "k": k, "kv": kv}, ref, "attn_sliced_v")
 
 
+@pytest.mark.parametrize("fold64", [False, True], ids=["default", "fold64"])
 @pytest.mark.parametrize("H,S,hd", [(12, 1024, 64), (8, 640, 128)])
-def test_attention_sliced_v_over_its_source(H, S, hd):
+def test_attention_sliced_v_over_its_source(monkeypatch, H, S, hd, fold64):
     """kv = RELU(kv_in) in the arena → SLICE (V columns) → RESHAPE → TRANSPOSE → V of a causal
     ATTENTION small enough for the key-range split → TRANSPOSE: the planner puts the output over
     kv's rows, which the fused kernel reads V from.  The run is still one kernel: every row
     goes through the split's workspace and the merge kernel writes the output after kv has
-    been read (bit-identical to the plan without fusion)."""
+    been read (bit-identical to the plan without fusion).  fold64: the 16x16 kernel on folded
+    64-row blocks (LBR_ATTN_FOLD64=1) stages its rows and attn_kq_flush stores them."""
     from helpers import cf_attention
     from runtime.executor.compiled import CompiledExecutor
     from runtime.planner import plan
+    if fold64:
+        monkeypatch.setenv("LBR_ATTN_FOLD64", "1")
+        monkeypatch.setenv("LBR_ATTN_KQ", "0")
     r = rng(H * S + hd + 1)
     W = H * hd
     q, k, kv_in = randn(r, 1, H, S, hd), randn(r, 1, H, S, hd), randn(r, 1, S, 2 * W)
@@ -261,6 +266,9 @@ def test_attention_sliced_v_over_its_source(H, S, hd):
     ex.compile(mem)
     try:
         assert any(n.endswith("+v+transpose+defer") for n in ex.kernel_names())
+        if fold64:
+            att = [p for p in ex.step_params() if p["kernel"].startswith("attn_fwd_mfma16")]
+            assert att and all(p["block_rows"] == 64 and p["defer"] for p in att), att
     finally:
         ex.close()
     kv = np.maximum(kv_in, 0.0)
@@ -269,15 +277,21 @@ def test_attention_sliced_v_over_its_source(H, S, hd):
     _check(g, {"q": q, "k": k, "kv_in": kv_in}, ref, "attn_sliced_v")
 
 
-@pytest.mark.parametrize("H,S,hd,causal", [(12, 1024, 64, True), (8, 640, 128, True), (4, 700, 64, False)])
-def test_attention_transpose_over_v(H, S, hd, causal):
+@pytest.mark.parametrize("H,S,hd,causal,fold64", [(12, 1024, 64, True, False), (8, 640, 128, True, False),
+                                                  (4, 700, 64, False, False), (8, 640, 128, True, True),
+                                                  (3, 333, 64, True, True)])
+def test_attention_transpose_over_v(monkeypatch, H, S, hd, causal, fold64):
     """V = RELU(x) lives in the arena and is dead after an ATTENTION small enough for the
     key-range split; the planner puts the output TRANSPOSE(1, 2) over V's memory.  The fused
     kernel sends every row through the split's workspace and the merge kernel, which runs
-    after V has been read, writes the [B, S, H, hd] output (bit-identical to the direct store)."""
+    after V has been read, writes the [B, S, H, hd] output (bit-identical to the direct store).
+    fold64: the folded 64-row schedule, rows staged for attn_kq_flush."""
     from helpers import cf_attention
     from runtime.executor.compiled import CompiledExecutor
     from runtime.planner import plan
+    if fold64:
+        monkeypatch.setenv("LBR_ATTN_FOLD64", "1")
+        monkeypatch.setenv("LBR_ATTN_KQ", "0")
     r = rng(H * S + hd)
     q, k, x = randn(r, 1, H, S, hd), randn(r, 1, H, S, hd), randn(r, 1, H, S, hd)
     g = Graph()
@@ -297,14 +311,18 @@ def test_attention_transpose_over_v(H, S, hd, causal):
     ex.compile(mem)
     try:
         assert any(n.endswith("+transpose+defer") for n in ex.kernel_names())
+        if fold64:
+            att = [p for p in ex.step_params() if p["kernel"].startswith("attn_fwd_mfma16")]
+            assert att and all(p["block_rows"] == 64 and p["defer"] for p in att), att
     finally:
         ex.close()
     ref = np.swapaxes(cf_attention(q, k, np.maximum(x, 0.0), causal=causal), 1, 2)
     _check(g, {"q": q, "k": k, "x": x}, ref, "attn_transpose")
 
 
-@pytest.mark.parametrize("H,S,hd,causal", [(12, 1024, 64, True), (8, 640, 128, True), (4, 700, 64, False)])
-def test_attention_output_relay(monkeypatch, H, S, hd, causal):
+@pytest.mark.parametrize("H,S,hd,causal,fold64", [(12, 1024, 64, True, False), (8, 640, 128, True, False),
+                                                  (4, 700, 64, False, False), (8, 640, 128, True, True)])
+def test_attention_output_relay(monkeypatch, H, S, hd, causal, fold64):
     """The output TRANSPOSE over V, as above, read only by the projection GEMM after it: the plan
     gives the attention a buffer of its own and points the GEMM's A there, so the store is not
     deferred (only cut blocks go through the merge kernel).  Bit-equal to the deferred plan
@@ -312,6 +330,9 @@ def test_attention_output_relay(monkeypatch, H, S, hd, causal):
     from helpers import cf_attention
     from runtime.executor.compiled import CompiledExecutor
     from runtime.planner import plan
+    if fold64:
+        monkeypatch.setenv("LBR_ATTN_FOLD64", "1")
+        monkeypatch.setenv("LBR_ATTN_KQ", "0")
     r = rng(H * S + hd + 2)
     W, N = H * hd, 96
     q, k, x = randn(r, 1, H, S, hd), randn(r, 1, H, S, hd), randn(r, 1, H, S, hd)

@@ -247,6 +247,19 @@ def test_attention_kq(monkeypatch, B, H, S, hd, causal, group):
     _attention_case(B, H, S, hd, causal, group, kernel="attn_fwd_kq_f32")
 
 
+# The 16x16 kernel on folded 64-row query blocks (4 wavefronts, one workgroup a CU at Qwen3's
+# 32 heads × S1024, the default there): forced on ragged, padded, GQA, odd-block-count and
+# one-row shapes, and on Qwen3's own.
+@pytest.mark.parametrize("B,H,S,hd,group", [(1, 4, 257, 128, 1), (1, 8, 300, 128, 4), (2, 3, 70, 64, 1),
+                                            (1, 2, 1, 128, 1), (1, 4, 100, 48, 1), (1, 2, 64, 16, 1),
+                                            (1, 4, 130, 96, 2), (1, 6, 200, 32, 3), (1, 32, 1024, 128, 4)])
+def test_attention_fold64(monkeypatch, B, H, S, hd, group):
+    if (H, S) != (32, 1024):
+        monkeypatch.setenv("LBR_ATTN_FOLD64", "1")
+    monkeypatch.setenv("LBR_ATTN_KQ", "0")
+    _attention_case(B, H, S, hd, True, group, kernel="attn_fwd_mfma16_f32")
+
+
 @pytest.mark.parametrize("B,H,S,hd", [(1, 12, 512, 64), (1, 12, 1024, 64), (1, 4, 32, 16)])
 def test_attention_small_grid_default(B, H, S, hd):
     # the schedule small grids take by default: the key-quartered kernel for head dim 32 / 64,
@@ -256,11 +269,13 @@ def test_attention_small_grid_default(B, H, S, hd):
 
 
 @pytest.mark.parametrize("S", [16, 300])
-@pytest.mark.parametrize("split", ["0", "2", "kq"])
+@pytest.mark.parametrize("split", ["0", "2", "kq", "causal_flag"])
 def test_attention_mask(monkeypatch, S, split):
+    # causal_flag: the node also sets causal; the reference then applies the mask alone
+    # (attn.c:40-48, "either custom additive mask or causal (never both)")
     if split == "kq":
         monkeypatch.setenv("LBR_ATTN_KQ", "1")
-    else:
+    elif split != "causal_flag":
         monkeypatch.setenv("LBR_ATTN_SPLIT", split)
     r = rng(S)
     B, H, hd = 1, 2, 64
@@ -268,7 +283,8 @@ def test_attention_mask(monkeypatch, S, split):
     mask = np.where(r.random((B, H, S, S)) < 0.2, -1e9, 0.0).astype(np.float32)
     for i in range(S):
         mask[..., i, i] = 0.0
-    g = one_node_graph(OpType.ATTENTION, {"q": q, "k": k, "v": v, "mask": mask}, (B, H, S, hd), {})
+    g = one_node_graph(OpType.ATTENTION, {"q": q, "k": k, "v": v, "mask": mask}, (B, H, S, hd),
+                       {"causal": True} if split == "causal_flag" else {})
     ref = cf_attention(q, k, v, mask=mask)
     _check(g, {"q": q, "k": k, "v": v, "mask": mask}, ref, 1e-4)
 

@@ -36,8 +36,13 @@ def test_workload_parity(key, seq):
     y, sess = _session_run(graph, x)
     # the host half of plan creation, run alone (lbr_check_nodes), builds the plan's steps
     ex = sess.executor
-    n_steps = len(ex.step_params())
+    params = ex.step_params()
+    n_steps = len(params)
     assert ex._lib.check_nodes(ex._nodes, len(ex._order), ex.live_outs()) == n_steps
+    if key == "qwen3_4b":
+        # 32 heads × 8 pairs of 64-row blocks: one folded workgroup a CU, no key-range split
+        att = [p for p in params if p["kernel"] == "attn_fwd_mfma16_f32"]
+        assert len(att) == 2 and all(p["block_rows"] == 64 and p["fold"] and not p["split_wg"] for p in att), att
     o = OracleRun(sess.memory_plan).run({graph.inputs[0]: x})[graph.outputs[0]]
     ref = reference_forward(model, x)
     sess.close()

@@ -93,6 +93,23 @@ def test_oracle_attention_mask_long_sequence():
     _ok(g, {"q": q, "k": k, "v": v, "mask": mask}, cf_attention(q, k, v, mask=mask), 1e-5)
 
 
+@pytest.mark.parametrize("S", [12, 280])
+def test_oracle_attention_mask_replaces_causal(S):
+    """A node with both a mask and the causal flag: the reference applies the additive mask
+    alone (attn.c:40-48, "either custom additive mask or causal (never both)"), and with a
+    mask never takes the flash path (executor.c:389).  The closed form of the mask alone
+    holds; the mask plus the causal pattern, which differs in every row but the last, does not."""
+    r = rng(S + 3)
+    q, k, v = randn(r, 1, 2, S, 16), randn(r, 1, 2, S, 16), randn(r, 1, 2, S, 16)
+    mask = np.where(r.random((1, 2, S, S)) < 0.3, -1e9, 0.0).astype(np.float32)
+    for i in range(S):
+        mask[..., i, i] = 0.0
+    g = one_node_graph(OpType.ATTENTION, {"q": q, "k": k, "v": v, "mask": mask}, q.shape, {"causal": True})
+    _ok(g, {"q": q, "k": k, "v": v, "mask": mask}, cf_attention(q, k, v, mask=mask), 1e-5)
+    both = cf_attention(q, k, v, mask=mask, causal=True)
+    assert normwise_rel(both, cf_attention(q, k, v, mask=mask)) > 1e-2
+
+
 def test_oracle_norms_softmax():
     r = rng(1)
     x = randn(r, 1, 9, 300) * 4 + 2.5
