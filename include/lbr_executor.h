@@ -148,12 +148,12 @@ int lbr_execute_workspace_bytes(size_t* out_bytes);
  * (its execute never allocates, because its kernels need no device
  * workspace); it is for callers that cannot allocate device memory: code
  * that must not call hipMalloc/hipFree (serving loops, harnesses that forbid
- * it).  The workspace is a fixed 72 MiB device array inside the library,
+ * it).  The workspace is a fixed 48 MiB device array inside the library,
  * one copy per GPU, held until the process ends; its address is resolved by
  * lbr_init, which must have run on the current device first (this call does
  * no set-up).  Node arrays whose kernels need more workspace than that (GEMM
  * split-K partial sums, attention key-range partials) are rejected with
- * LBR_ERR_INVALID before anything is launched (72 MiB holds the 66 MiB the
+ * LBR_ERR_INVALID before anything is launched (48 MiB holds the 40 MiB the
  * largest benchmark workload, the Qwen3-4B body at S=1024, needs).  All calls on one GPU share
  * that array and keep the last call's contents (nothing relies on them);
  * calls overlapping on one GPU would race on it, so the library serialises

@@ -127,10 +127,11 @@ static int exec_workspace(size_t need, void** out) {
 // kernels.  Nothing in it needs to start at zero: the GEMM split-K ranges
 // and the attention key-range segments write every partial they later read.
 // Size: the largest per-call workspace of the seven benchmark workloads'
-// one-kernel-per-node arrays is 66 MiB (the Qwen3-4B body's split attention,
-// 32 heads x 8 blocks x 4 segments x 128 rows x 130 floats); GPT-2 S=1024 and
-// the 7B block need 12 MiB.
-#define LBR_SCRATCH_BYTES ((size_t)72 << 20)
+// one-kernel-per-node arrays is 40 MiB (the Qwen3-4B body's down projection,
+// 4 K ranges x 1024 x 2560 floats of partial sums; its attention runs on
+// folded 64-row blocks with no workspace); the GPT-2 and 7B workloads need at
+// most 25 MiB.
+#define LBR_SCRATCH_BYTES ((size_t)48 << 20)
 #define LBR_MAX_DEVICES 64
 static __device__ __align__(256) unsigned char scratch[LBR_SCRATCH_BYTES];
 static void* g_scratch_dev[LBR_MAX_DEVICES] = {};
