@@ -356,8 +356,8 @@ __device__ __forceinline__ void attn16_qblock(const AttnArgs& g, int bhi, int qb
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int lr = lane & 15, lg = lane >> 4;
-    // without a split the head is the grid's y index and the range starts at tile 0
-    const long long bh = SPLIT ? (long long)bhi : (long long)blockIdx.y;
+    // the caller passes the head; without a split the range starts at tile 0
+    const long long bh = bhi;
     const int t0 = SPLIT ? t0_ : 0;
     const long long kvh = bh / g.group_size;
     const int S = g.S, D = g.D;
@@ -620,21 +620,33 @@ __device__ __forceinline__ int sk_block_start(const AttnArgs& g, int qb, bool ca
 // CU with equal work, where 128-row blocks give 128 pairs or a key-range
 // split and its merge); one workgroup a CU holds two K/V tiles in LDS, so a
 // tile ends with one barrier.
+// NWQ = 4 runs a one-dimensional grid of (head, block) pairs numbered head-major,
+// remapped so that XCD x (workgroups w ≡ x mod 8) takes the contiguous x-th eighth:
+// whole heads, so a GQA group's K/V rows stay in that XCD's L2 (Qwen3-4B: 4 query
+// heads, one K/V head of 1 MB, per XCD) instead of every XCD streaming all of them.
 template <int DP, bool CAUSAL, bool HAS_MASK, int NWQ = 8>
 __global__ __launch_bounds__(64 * NWQ, NWQ == 8 ? 4 : 1) void attn_fwd_mfma16(AttnArgs g) {
     constexpr bool DB = NWQ == 4;
     constexpr int QB = 16 * NWQ;
     __shared__ float Ks[(DB ? 2 : 1) * A16_KB][DP + 4];
     __shared__ float Vs[(DB ? 2 : 1) * A16_KB][DP + 4];
-    const int j = blockIdx.x, last = g.n_qblocks - 1 - j;
+    int j = blockIdx.x, bh = blockIdx.y;
+    if (NWQ == 4) {
+        const int per_head = g.fold ? (g.n_qblocks + 1) / 2 : g.n_qblocks;
+        const int total = gridDim.x, w = blockIdx.x;
+        const int t = total % 8 == 0 ? (w % 8) * (total / 8) + w / 8 : w;
+        bh = t / per_head;
+        j = t - bh * per_head;
+    }
+    const int last = g.n_qblocks - 1 - j;
     if (!CAUSAL) {
-        attn16_qblock<DP, CAUSAL, HAS_MASK, false, DB, NWQ>(g, 0, j, 0, attn16_tiles(g, j, false, QB), -1, Ks, Vs);
+        attn16_qblock<DP, CAUSAL, HAS_MASK, false, DB, NWQ>(g, bh, j, 0, attn16_tiles(g, j, false, QB), -1, Ks, Vs);
         return;
     }
-    attn16_qblock<DP, CAUSAL, HAS_MASK, false, DB, NWQ>(g, 0, last, 0, attn16_tiles(g, last, true, QB), -1, Ks, Vs);
+    attn16_qblock<DP, CAUSAL, HAS_MASK, false, DB, NWQ>(g, bh, last, 0, attn16_tiles(g, last, true, QB), -1, Ks, Vs);
     if (g.fold && j < last) {   // folded second block: query block j
         __syncthreads();
-        attn16_qblock<DP, CAUSAL, HAS_MASK, false, DB, NWQ>(g, 0, j, 0, attn16_tiles(g, j, true, QB), -1, Ks, Vs);
+        attn16_qblock<DP, CAUSAL, HAS_MASK, false, DB, NWQ>(g, bh, j, 0, attn16_tiles(g, j, true, QB), -1, Ks, Vs);
     }
 }
 
@@ -1173,7 +1185,8 @@ void launch_attn16(const Step& s, hipStream_t st) {
         g.sk_defer = s.i[14] != 0;
         if (g.sk_defer) g.part = (float*)s.ws;
         const unsigned gx = g.fold ? (unsigned)(g.n_qblocks + 1) / 2 : (unsigned)g.n_qblocks;
-        hipLaunchKernelGGL((attn_fwd_mfma16<DP, CAUSAL, HAS_MASK, 4>), dim3(gx, (unsigned)s.i[0]), dim3(256), 0, st, g);
+        hipLaunchKernelGGL((attn_fwd_mfma16<DP, CAUSAL, HAS_MASK, 4>), dim3(gx * (unsigned)s.i[0]), dim3(256), 0, st,
+                           g);
         if (g.sk_defer)
             hipLaunchKernelGGL(attn_kq_flush, dim3((unsigned)(((long long)g.S * (g.D / 4) + 255) / 256),
                                                    (unsigned)s.i[0]),
